@@ -1,0 +1,245 @@
+/*
+ * ms_gpu.h -- C ABI of the MI355X (gfx950) implementation of MojoStream's
+ * Gemma-4 per-token layer loop.
+ *
+ * Conventions
+ *   - Every function returns MS_OK (0) or a negative MS_E* code; the message
+ *     of the last failure on the calling thread is ms_last_error().  No C++
+ *     exception crosses this boundary.  A caller that mirrors the reference's
+ *     fail-fast loaders turns a nonzero code into `raise Error(ms_last_error())`.
+ *   - Pointers named d_* are device pointers (ms_malloc); h_* are host
+ *     pointers.  The caller owns host memory; the library owns what it
+ *     allocates behind opaque handles.
+ *   - Work is ordered on the library's stream and asynchronous, except
+ *     functions that return host data (they synchronize).
+ *   - One host thread per library instance (the reference's callers are
+ *     single-threaded; its `workers` argument has no GPU meaning and is not
+ *     part of this ABI).
+ *   - Q4 weights: the reference layout is row-major [K][N/2] bytes, byte j of
+ *     row k holding column 2j in its low nibble and 2j+1 in its high nibble,
+ *     w = (nibble - 8) * scale with one fp32 scale per tensor
+ *     (kernels.mojo:66-69).  On the device they live repacked in the
+ *     "panel" layout produced by ms_q4_pack (same byte count, K%128==0,
+ *     N%16==0 required).
+ *
+ * Reference citations are relative to the MojoStream repository.
+ */
+#ifndef MS_GPU_H
+#define MS_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MS_OK 0
+#define MS_E_INVALID (-1)   /* bad argument / shape violation */
+#define MS_E_HIP (-2)       /* HIP runtime failure */
+#define MS_E_STATE (-3)     /* library not initialised / wrong call order */
+#define MS_E_NOMEM (-4)     /* allocation failed */
+#define MS_E_IO (-5)        /* file / guard failure (host helpers) */
+
+/* ---- context ------------------------------------------------------------ */
+/* No reference counterpart (the reference runs on CPU threads); replaces the
+ * implicit set-up before matmul_q4_bpack_raw's first `parallelize`
+ * (kernels.mojo:266-267). */
+int ms_init(int device);
+int ms_shutdown(void);
+const char *ms_last_error(void);
+int ms_synchronize(void);
+/* Device name / CU count / HBM bytes for reports. */
+int ms_device_info(char *name, size_t name_len, int *n_cu, size_t *hbm_bytes);
+
+/* ---- memory ------------------------------------------------------------- */
+/* Device buffers replace the reference's List-backed Matrix storage
+ * (kernels.mojo:34-61) and the weight buffers of Gemma4LayerWeights
+ * (main.mojo:305-337). */
+int ms_malloc(void **d_ptr, size_t bytes);
+int ms_free(void *d_ptr);
+int ms_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes);
+int ms_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes);
+int ms_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes);
+int ms_memset(void *d_dst, int value, size_t bytes);
+/* Pinned host memory (hipHostMalloc) for the streaming double buffer; replaces
+ * the scratch List of StreamingRunner (stream_runner.mojo:388-409). */
+int ms_host_alloc(void **h_ptr, size_t bytes);
+int ms_host_free(void *h_ptr);
+
+/* ---- seeded synthetic data ---------------------------------------------- */
+/* Counter-based generator (splitmix64 of seed, stream, index).  Host and
+ * device produce identical bytes.  Replaces the unseeded `rand` fills of
+ * Q4Matrix.fill_random / init_random_layer_weights (kernels.mojo:91-92,
+ * main.mojo:616-633) and create_fake_model.py's rng.integers(0,256)
+ * (create_fake_model.py:94-97). */
+int ms_fill_random_u8(uint8_t *d_dst, size_t n, uint64_t seed, uint64_t stream);
+void ms_host_fill_random_u8(uint8_t *h_dst, size_t n, uint64_t seed,
+                            uint64_t stream);
+/* Uniform [lo,hi) float for (seed, stream, index) (scales: U(0.04,0.15),
+ * PLE: U(0.8,1.2), create_fake_model.py:95,203). */
+float ms_host_uniform(uint64_t seed, uint64_t stream, uint64_t index, float lo,
+                      float hi);
+/* Standard normal fp32 values (Box-Muller) for activation inputs. */
+void ms_host_fill_normal(float *h_dst, size_t n, uint64_t seed, uint64_t stream);
+
+/* ---- Q4 kernels (kernel-level parity entry points) ---------------------- */
+/* Bytes of the panel layout (== K*N/2). */
+size_t ms_q4_packed_bytes(int K, int N);
+/* Repack reference row-major Q4 into the panel layout (device->device).
+ * Replaces the byte copy of load_weights_from_ms (harness.mojo:80-122). */
+int ms_q4_pack(uint8_t *d_packed, const uint8_t *d_rowmajor, int K, int N);
+/* Same repack on the host (streaming mode packs once into pinned memory). */
+int ms_host_q4_pack(uint8_t *h_packed, const uint8_t *h_rowmajor, int K, int N);
+/* Dequantize to fp32 [K][N]: dequant_vec, kernels.mojo:100-108 (row-major
+ * input), and the same from the panel layout (bit-exact check of packing). */
+int ms_dequant_q4(float *d_out, const uint8_t *d_rowmajor, int K, int N,
+                  float scale);
+int ms_dequant_q4_packed(float *d_out, const uint8_t *d_packed, int K, int N,
+                         float scale);
+/* C (+)= A . deq(W): matmul_q4_bpack_raw, kernels.mojo:201-267 (and
+ * matmul_q4_bpack :122-193 on a Q4Matrix).  A fp32 [M][K], W panel layout,
+ * C fp32 [M][N].  accumulate=1 keeps the reference's C += semantics,
+ * accumulate=0 overwrites.  M <= 16 runs the decode GEMV, larger M the
+ * prefill GEMM. */
+int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
+                 int K, int N, float scale, int accumulate);
+
+/* ---- elementwise kernels ------------------------------------------------ */
+/* rmsnorm_inplace, kernels.mojo:474-489 */
+int ms_rmsnorm(float *d_x, int rows, int cols);
+/* rmsnorm_weighted_inplace, kernels.mojo:598-613 (d_gamma may be NULL = 1) */
+int ms_rmsnorm_weighted(float *d_x, const float *d_gamma, int rows, int cols);
+/* ple_scale_inplace, kernels.mojo:506-516 */
+int ms_ple_scale(float *d_x, size_t n, float s);
+/* swiglu_inplace, kernels.mojo:519-532 (result in d_up) */
+int ms_swiglu(const float *d_gate, float *d_up, size_t n);
+/* apply_rope_inplace, kernels.mojo:553-595: `rows` rows of stride row_stride,
+ * row r at position base_pos + r; n_heads heads of stride head_stride; the
+ * first rot_dim dims of each head rotate (partial use gemma4_e4b.mojo:489-500).
+ * cos/sin use the reference's fp32 formula, evaluated on the host. */
+int ms_rope(float *d_x, int rows, int row_stride, int n_heads, int head_stride,
+            int rot_dim, float theta, int base_pos);
+
+/* ---- attention (kernel level) ------------------------------------------- */
+#define MS_CACHE_LINEAR 0   /* KVCache (main.mojo:257-301), full cache (gemma4_e4b.mojo:231-249) */
+#define MS_CACHE_CIRCULAR 1 /* sliding cache, slot = pos % window (gemma4_e4b.mojo:211-228) */
+
+typedef struct {
+  int q_dim, kv_dim, head_dim, n_heads, n_kv_heads;
+  int rot_dim;     /* rotated dims per head */
+  float theta;     /* RoPE base */
+  int cache_kind;  /* MS_CACHE_* */
+  int cache_len;   /* linear: positions; circular: window */
+  int clamp_reads; /* linear: attend min(pos+1, cache_len) keys (gemma4_e4b.mojo:362-363) */
+} ms_layer_desc;
+
+/* Causal GQA attention of T rows of one sequence at positions
+ * base..base+T-1 (compute_sliding_attention gemma4_e4b.mojo:259-338,
+ * compute_full_attention :341-411, gqa_attention_decode main.mojo:445-519),
+ * followed by the cache write of the T rows (write_kv_*: :211-249).  q/k/v
+ * are final (after RoPE for q and k).  Keys of the T rows come from
+ * d_knew/d_vnew, older keys from the cache. */
+int ms_attention(const ms_layer_desc *desc, const float *d_q,
+                 const float *d_knew, const float *d_vnew, float *d_kcache,
+                 float *d_vcache, int T, int base, float *d_out);
+
+/* ---- LM head (kernel level) --------------------------------------------- */
+/* logits = x . deq(W_lm) (project_lm_head, lm_head.mojo:146-168) and the
+ * greedy id per row (temperature_sampling T<=0.01 branch, :224-230: first
+ * index of the strict maximum).  d_logits may be NULL. */
+int ms_lm_head_argmax(const float *d_x, int M, int D, const uint8_t *d_packed,
+                      int vocab, float scale, float *d_logits, int32_t *d_ids);
+/* get_token_embedding Q4 branch (lm_head.mojo:186-195): column `token` of the
+ * tied head, dequantized, for each of n tokens -> d_out [n][D]. */
+int ms_embed_q4(const uint8_t *d_packed, int D, int vocab, float scale,
+                const int32_t *d_tokens, int n, float *d_out);
+
+/* ---- model (layer loop) --------------------------------------------------- */
+typedef struct ms_model ms_model;
+
+typedef struct {
+  int hidden;      /* D */
+  int ffn;         /* F */
+  int n_layers;
+  int vocab;       /* 0: no LM head (demo model) */
+  int max_seqs;    /* independent sequences, each with its own caches */
+  int max_rows;    /* rows per sequence per call (T) */
+  int max_pos;     /* highest position + 1 the RoPE tables cover */
+  int resident;    /* 1: weights resident in HBM; 0: streamed per layer from
+                      pinned host memory through two HBM slots */
+} ms_model_desc;
+
+/* Creates a model with per-layer shapes (ModelRunner / Gemma4Config /
+ * E4BLayerRef shapes: main.mojo:230-253, gemma4_e4b.mojo:125-174) and
+ * allocates KV caches (KVCache main.mojo:257-301, HybridKVCache
+ * gemma4_e4b.mojo:83-116). */
+int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *layers,
+                    ms_model **out);
+int ms_model_destroy(ms_model *m);
+/* Binds one of the 7 matrices (0 Q,1 K,2 V,3 O,4 Gate,5 Up,6 Down -- the
+ * .mojostream type tag minus one, mojostream.mojo:21-28) of a layer.
+ * `src` is row-major reference Q4, on the device if src_on_device else host.
+ * Resident models pack it into HBM; streaming models require host memory
+ * from ms_host_alloc and keep a packed pinned copy.
+ * Replaces load_weights_from_ms (harness.mojo:80-122) and
+ * get_layer_ref (sparse_pin.mojo:295-330). */
+int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_t *src,
+                        int src_on_device, float scale);
+int ms_model_set_ple(ms_model *m, int layer, float ple);
+/* Tied Q4 LM head (LMHead v1, lm_head.mojo:41-116); h_gamma NULL = ones. */
+int ms_model_set_lm_head(ms_model *m, const uint8_t *src, int src_on_device,
+                         float scale, const float *h_gamma);
+/* KVCache.reset (main.mojo:295-297): positions restart at 0. */
+int ms_model_reset(ms_model *m);
+
+/* One layer over rows d_x [n_seqs*T][D] in place, sequence s at positions
+ * h_base[s]..h_base[s]+T-1 (e4b_forward_layer gemma4_e4b.mojo:459-540,
+ * gemma4_forward_layer main.mojo:538-613, gemma4_forward_stream
+ * stream_runner.mojo:101-161). */
+int ms_layer_forward(ms_model *m, int layer, float *d_x, int n_seqs, int T,
+                     const int *h_base);
+/* All layers in order (the per-step loops of demo_first_light main.mojo:685-695,
+ * run_harness harness.mojo:256-269).  d_hidden (optional) receives every
+ * layer's output [n_layers][n_seqs*T][D]. */
+int ms_forward(ms_model *m, float *d_x, int n_seqs, int T, const int *h_base,
+               float *d_hidden);
+
+/* Greedy decode with the tied head (gemma4_e4b_infer.mojo:163-186 with T=0):
+ * ms_decode_begin sets, per sequence, the current token and its position;
+ * ms_decode_run performs n_steps steps (embedding -> layers -> final norm ->
+ * logits -> argmax -> next token) on the device and returns the generated ids
+ * [n_steps][n_seqs].  use_graph=1 replays one captured HIP graph per step. */
+int ms_decode_begin(ms_model *m, int n_seqs, const int32_t *h_tokens,
+                    const int32_t *h_pos);
+int ms_decode_run(ms_model *m, int n_steps, int use_graph, int32_t *h_ids_out);
+/* Prompt processing for one sequence (the prompt loop of
+ * gemma4_e4b_infer.mojo:114-130 done in row chunks): runs the prompt tokens at
+ * positions h_pos0.. and returns the first greedy id (TTFT path). */
+int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_tokens,
+               int pos0, int32_t *h_first_id);
+
+/* ---- streaming statistics ------------------------------------------------ */
+typedef struct {
+  double io_ms;        /* host->HBM copy time of the last ms_forward/decode call */
+  double compute_ms;   /* kernel time */
+  double wait_ms;      /* time compute waited for a copy (measured with events) */
+  double total_ms;
+} ms_stream_stats;
+/* I/O vs compute of the last call (run_streaming_bench stream_runner.mojo:503-546
+ * reports the same split analytically). */
+int ms_model_stream_stats(ms_model *m, ms_stream_stats *out);
+
+/* ---- profiling ------------------------------------------------------------ */
+/* When enabled, ms_decode_run (eager mode) records HIP events around every
+ * launch of each kernel class on the library stream; ms_prof_get returns
+ * launch counts and total milliseconds per class. */
+#define MS_PROF_CLASSES 8
+int ms_prof_enable(int on);
+int ms_prof_get(int cls, const char **name, long *launches, double *total_ms,
+                double *bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

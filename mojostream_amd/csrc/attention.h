@@ -1,0 +1,39 @@
+// Decode / chunked-prefill attention interface.
+#pragma once
+#include "common.h"
+
+namespace ms {
+
+struct AttnArgs {
+  int B, T;                 // sequences, rows per sequence
+  int q_dim, kv_dim, hd, n_heads, n_kv, rot;
+  int cache_kind, cache_len, clamp;
+  float scale;              // 1/sqrt(head_dim)
+  // q|k|v source: split-K partial sums [S][B*T][ld]; q at column 0,
+  // k at q_dim, v at q_dim + kv_dim
+  const float *qkv;
+  int S;
+  size_t split_stride;
+  int ld;
+  int apply_rope;
+  const float *cos_t, *sin_t;  // [positions][rot/2]
+  const int32_t *pos;          // base position per sequence [B]
+  float *kc, *vc;              // caches [B][cache_len][kv_dim]
+  size_t cache_seq_stride;     // floats between sequences
+  int n_chunks, CH;
+  float *part;                 // [B][n_kv][n_chunks][T*G][hd+2]
+  unsigned *counters;          // [B*n_kv], zero between uses
+  float *out;                  // [B*T][q_dim] or null
+  _Float16 *out_hi, *out_lo;   // [B*T][q_dim] or null
+  float out_prescale;
+  int write_cache;
+};
+
+constexpr int kAttnChunk = 32;
+constexpr int kAttnMaxTG = 20;   // T * (n_heads / n_kv)
+constexpr int kAttnLds = 12288;  // floats of q/k/v staging
+
+int launch_attention(const AttnArgs &a, hipStream_t st);
+int attn_check(const AttnArgs &a);
+
+}  // namespace ms

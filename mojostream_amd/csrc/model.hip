@@ -1,0 +1,1037 @@
+// The Gemma-4 per-token layer loop on one MI355X.
+//
+// Per layer (e4b_forward_layer gemma4_e4b.mojo:459-540; gemma4_forward_layer
+// main.mojo:538-613) five launches on one stream:
+//   1. QKV GEMV   x_norm -> q|k|v split-K partials (Q, K, V fused, 3 scales)
+//   2. attention  partial sums + RoPE + causal GQA over the cache; the last
+//                 block per (seq, kv head) merges chunks, writes the O input
+//                 (fp16 hi/lo) and appends K/V to the cache
+//   3. O GEMV     -> partials; last block: x2 = x_norm + attn.Wo,
+//                 x2n = rmsnorm(x2), GateUp input
+//   4. GateUp     gate and up panels of the same columns in one block;
+//                 epilogue up*gate*sigmoid(gate) -> Down input
+//   5. Down GEMV  -> partials; last block: x_out = x2n + ffn.Wd (the layer
+//                 output), then PLE scale + rmsnorm of the next layer's input
+//                 (or the final weighted norm for the LM head).
+// The residual adds to the normalized stream, as in the reference
+// (gemma4_e4b.mojo:520-538, gen_reference.py:160-172).
+//
+// Decode (T=1 per sequence) keeps token ids and positions on the device, so
+// one captured HIP graph runs every step unchanged.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "attention.h"
+#include "q4.h"
+#include "rope.h"
+
+namespace ms {
+
+struct RopeTab {
+  int rot = 0;
+  float theta = 0.f;
+  float *cs = nullptr, *sn = nullptr;
+};
+
+struct Layer {
+  ms_layer_desc d{};
+  uint8_t *w[7] = {};        // device panel-layout weights (resident) or slot pointers
+  uint8_t *h_packed[7] = {}; // pinned packed copies (streaming)
+  size_t bytes[7] = {};
+  size_t off[7] = {};        // offsets inside a streaming slot
+  float scale[7] = {};
+  int set_mask = 0;
+  float ple = 1.f;
+  float *kc = nullptr, *vc = nullptr;
+  size_t cache_seq_stride = 0;
+  int rope = 0;
+  float o_prescale = 1.f, f_prescale = 1.f;
+  int S_qkv = 1, S_o = 1, S_d = 1, n_chunks = 1;
+};
+
+// profiling classes
+enum { PC_QKV, PC_ATTN, PC_O, PC_GATEUP, PC_DOWN, PC_LM, PC_PREP, PC_OTHER };
+static const char *kProfNames[MS_PROF_CLASSES] = {"qkv_gemv", "attention", "o_gemv",
+                                                  "gateup_gemv", "down_gemv", "lm_head",
+                                                  "embed_prep", "other"};
+struct Prof {
+  bool on = false;
+  long launches[MS_PROF_CLASSES] = {};
+  double ms[MS_PROF_CLASSES] = {};
+  double bytes[MS_PROF_CLASSES] = {};
+  std::vector<hipEvent_t> pool;
+  struct Rec {
+    int cls;
+    hipEvent_t a, b;
+    double bytes;
+  };
+  std::vector<Rec> pending;
+  size_t used = 0;
+};
+static Prof g_prof;
+
+}  // namespace ms
+
+struct ms_model {
+  ms_model_desc d{};
+  std::vector<ms::Layer> L;
+  std::vector<ms::RopeTab> ropes;
+  int qkv_max = 0, q_max = 0, kv_max = 0, hd_max = 0;
+  int Mmax = 0;
+  // LM head
+  uint8_t *lm_w = nullptr;
+  float lm_scale = 0.f;
+  float *gamma = nullptr;
+  bool has_lm = false;
+  // workspaces
+  float *x_in = nullptr, *xn = nullptr, *x2n = nullptr;
+  _Float16 *aA_hi = nullptr, *aA_lo = nullptr, *aO_hi = nullptr, *aO_lo = nullptr,
+           *aF_hi = nullptr, *aF_lo = nullptr;
+  float *qkv_part = nullptr, *attn_part = nullptr, *o_part = nullptr,
+        *down_part = nullptr;
+  size_t qkv_part_stride = 0, o_part_stride = 0, d_part_stride = 0;
+  unsigned *counters = nullptr;  // [0] O, [1] Down, [2] LM, [16..] attention
+  int32_t *pos = nullptr, *tok = nullptr, *ids_hist = nullptr, *step = nullptr;
+  int hist_cap = 1024;
+  float *arg_val = nullptr;
+  int32_t *arg_idx = nullptr;
+  int lm_blocks = 0;
+  // host mirror of positions
+  std::vector<int> h_pos;
+  int dec_nseq = 0;
+  // graph
+  hipGraphExec_t gexec = nullptr;
+  int g_nseq = 0;
+  // streaming
+  uint8_t *slot[2] = {nullptr, nullptr};
+  size_t slot_bytes = 0;
+  hipEvent_t ev_free[2] = {}, ev_ready[2] = {};
+  std::vector<hipEvent_t> io_ev;  // per-call timing events
+  ms_stream_stats stats{};
+  std::vector<void *> allocs;
+};
+
+namespace ms {
+
+static int dmalloc(ms_model *m, void **p, size_t bytes) {
+  if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess)
+    return fail(MS_E_NOMEM, "model: out of device memory");
+  m->allocs.push_back(*p);
+  return MS_OK;
+}
+
+static float pow2_prescale(double bound) {
+  // largest power of two p <= 1 with bound * p <= 32768 (fp16 max 65504)
+  int e = 0;
+  while (bound * std::ldexp(1.0, -e) > 32768.0 && e < 60) ++e;
+  return (float)std::ldexp(1.0, -e);
+}
+
+static int pick_split(int panels, int KG, int target_blocks) {
+  int S = 1;
+  while ((long)panels * S < target_blocks && S * 2 <= KG) S *= 2;
+  return S;
+}
+
+// ---- profiling helpers -------------------------------------------------------
+static bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus s = hipStreamCaptureStatusNone;
+  (void)hipStreamIsCapturing(st, &s);
+  return s != hipStreamCaptureStatusNone;
+}
+static hipEvent_t prof_event() {
+  if (g_prof.used == g_prof.pool.size()) {
+    hipEvent_t e;
+    (void)hipEventCreate(&e);
+    g_prof.pool.push_back(e);
+  }
+  return g_prof.pool[g_prof.used++];
+}
+struct ProfScope {
+  int cls;
+  double bytes;
+  hipStream_t st;
+  hipEvent_t b{};
+  bool active;
+  ProfScope(int c, double by, hipStream_t s) : cls(c), bytes(by), st(s) {
+    active = g_prof.on && !capturing(s);
+    if (active) {
+      hipEvent_t a = prof_event();
+      b = prof_event();
+      (void)hipEventRecord(a, st);
+      g_prof.pending.push_back({cls, a, b, bytes});
+    }
+  }
+  ~ProfScope() {
+    if (active) (void)hipEventRecord(b, st);
+  }
+};
+static void prof_collect() {
+  for (auto &r : g_prof.pending) {
+    float ms = 0.f;
+    (void)hipEventSynchronize(r.b);
+    (void)hipEventElapsedTime(&ms, r.a, r.b);
+    g_prof.launches[r.cls] += 1;
+    g_prof.ms[r.cls] += ms;
+    g_prof.bytes[r.cls] += r.bytes;
+  }
+  g_prof.pending.clear();
+  g_prof.used = 0;
+}
+
+// ---- per-layer enqueue --------------------------------------------------------
+struct RunCfg {
+  int B, T;                 // sequences, rows per sequence
+  int last_fin;             // what the last Down block does after the final layer
+  float *out_rows;          // LAST_OUTPUT: layer output rows
+  float *hidden;            // optional [L][M][D]
+  int first_layer, n_layers;
+  int seq0;                 // first sequence (caches / positions offset)
+};
+enum { LAST_OUTPUT = 0, LAST_LM = 1 };
+
+static FinArgs fin_next(ms_model *m, const RunCfg &rc, int l, const float *base,
+                        const float *parts, int n_parts, size_t stride) {
+  FinArgs f{};
+  const int M = rc.B * rc.T;
+  f.M = M;
+  f.D = m->d.hidden;
+  f.base = base;
+  f.parts = parts;
+  f.n_parts = n_parts;
+  f.part_stride = stride;
+  f.a_prescale = 1.f;
+  const int last = rc.first_layer + rc.n_layers - 1;
+  if (rc.hidden && l >= 0)
+    f.hidden_out = rc.hidden + (size_t)(l - rc.first_layer) * M * m->d.hidden;
+  if (l < last) {
+    f.pre_scale = m->L[l + 1].ple;
+    f.normalize = 1;
+    f.xn_out = m->xn;
+    f.a_hi = m->aA_hi;
+    f.a_lo = m->aA_lo;
+  } else if (rc.last_fin == LAST_LM) {
+    f.pre_scale = 1.f;
+    f.normalize = 1;
+    f.gamma = m->gamma;
+    f.a_hi = m->aA_hi;
+    f.a_lo = m->aA_lo;
+  } else {
+    // plain layer output: write into the caller's rows, no normalisation
+    f.pre_scale = 1.f;
+    f.normalize = 0;
+    if (!f.hidden_out) f.hidden_out = rc.out_rows;
+  }
+  return f;
+}
+
+static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
+  Layer &Ly = m->L[l];
+  const ms_layer_desc &d = Ly.d;
+  const int M = rc.B * rc.T;
+  const int D = m->d.hidden, F = m->d.ffn;
+  const int ld = d.q_dim + 2 * d.kv_dim;
+
+  // 1. QKV
+  {
+    GemvArgs a{};
+    a.epi = EPI_STORE;
+    a.K = D;
+    a.M = M;
+    a.a_hi = m->aA_hi;
+    a.a_lo = m->aA_lo;
+    a.lda = D;
+    a.out_mul = 1.f;
+    a.seg[0] = GemvSeg{Ly.w[0], Ly.scale[0], d.q_dim, 0};
+    a.seg[1] = GemvSeg{Ly.w[1], Ly.scale[1], d.kv_dim, d.q_dim};
+    a.seg[2] = GemvSeg{Ly.w[2], Ly.scale[2], d.kv_dim, d.q_dim + d.kv_dim};
+    a.nseg = 3;
+    a.P = 1;
+    a.S = Ly.S_qkv;
+    a.waves = 4;
+    a.out = m->qkv_part;
+    a.ldo = ld;
+    a.split_stride = (size_t)M * ld;
+    ProfScope ps(PC_QKV, (double)D * ld / 2, st);
+    if (int rc2 = launch_gemv(a, st)) return rc2;
+  }
+  // 2. attention
+  {
+    AttnArgs a{};
+    a.B = rc.B;
+    a.T = rc.T;
+    a.q_dim = d.q_dim;
+    a.kv_dim = d.kv_dim;
+    a.hd = d.head_dim;
+    a.n_heads = d.n_heads;
+    a.n_kv = d.n_kv_heads;
+    a.rot = d.rot_dim;
+    a.cache_kind = d.cache_kind;
+    a.cache_len = d.cache_len;
+    a.clamp = d.clamp_reads;
+    a.scale = 1.0f / sqrtf((float)d.head_dim);
+    a.qkv = m->qkv_part;
+    a.S = Ly.S_qkv;
+    a.split_stride = (size_t)M * ld;
+    a.ld = ld;
+    a.apply_rope = 1;
+    a.cos_t = m->ropes[Ly.rope].cs;
+    a.sin_t = m->ropes[Ly.rope].sn;
+    a.pos = m->pos + rc.seq0;
+    a.kc = Ly.kc + (size_t)rc.seq0 * Ly.cache_seq_stride;
+    a.vc = Ly.vc + (size_t)rc.seq0 * Ly.cache_seq_stride;
+    a.cache_seq_stride = Ly.cache_seq_stride;
+    a.CH = kAttnChunk;
+    a.n_chunks = Ly.n_chunks;
+    a.part = m->attn_part;
+    a.counters = m->counters + 16;
+    a.out = nullptr;
+    a.out_hi = m->aO_hi;
+    a.out_lo = m->aO_lo;
+    a.out_prescale = Ly.o_prescale;
+    a.write_cache = 1;
+    ProfScope ps(PC_ATTN, 0.0, st);
+    if (int rc2 = launch_attention(a, st)) return rc2;
+  }
+  // 3. O projection; last block: residual + post-attention norm
+  {
+    GemvArgs a{};
+    a.epi = EPI_STORE;
+    a.K = d.q_dim;
+    a.M = M;
+    a.a_hi = m->aO_hi;
+    a.a_lo = m->aO_lo;
+    a.lda = d.q_dim;
+    a.out_mul = 1.0f / Ly.o_prescale;
+    a.seg[0] = GemvSeg{Ly.w[3], Ly.scale[3], D, 0};
+    a.nseg = 1;
+    a.P = 1;
+    a.S = Ly.S_o;
+    a.waves = 4;
+    a.out = m->o_part;
+    a.ldo = D;
+    a.split_stride = (size_t)M * D;
+    a.counter = m->counters + 0;
+    a.fin_kind = 1;
+    FinArgs &f = a.fin;
+    f.M = M;
+    f.D = D;
+    f.base = m->xn;
+    f.parts = m->o_part;
+    f.n_parts = Ly.S_o;
+    f.part_stride = (size_t)M * D;
+    f.pre_scale = 1.f;
+    f.normalize = 1;
+    f.xn_out = m->x2n;
+    f.a_hi = m->aA_hi;
+    f.a_lo = m->aA_lo;
+    f.a_prescale = 1.f;
+    ProfScope ps(PC_O, (double)d.q_dim * D / 2, st);
+    if (int rc2 = launch_gemv(a, st)) return rc2;
+  }
+  // 4. Gate + Up with SwiGLU epilogue
+  {
+    GemvArgs a{};
+    a.epi = EPI_SWIGLU;
+    a.K = D;
+    a.M = M;
+    a.a_hi = m->aA_hi;
+    a.a_lo = m->aA_lo;
+    a.lda = D;
+    a.out_mul = 1.f;
+    a.seg[0] = GemvSeg{Ly.w[4], Ly.scale[4], F, 0};
+    a.seg[1] = GemvSeg{Ly.w[5], Ly.scale[5], F, 0};
+    a.nseg = 2;
+    a.P = 2;
+    a.S = 1;
+    a.waves = 4;
+    a.out = nullptr;
+    a.sw_hi = m->aF_hi;
+    a.sw_lo = m->aF_lo;
+    a.ldo_sw = F;
+    a.sw_prescale = Ly.f_prescale;
+    ProfScope ps(PC_GATEUP, (double)D * F, st);
+    if (int rc2 = launch_gemv(a, st)) return rc2;
+  }
+  // 5. Down; last block: residual, then the next layer's PLE + norm
+  {
+    GemvArgs a{};
+    a.epi = EPI_STORE;
+    a.K = F;
+    a.M = M;
+    a.a_hi = m->aF_hi;
+    a.a_lo = m->aF_lo;
+    a.lda = F;
+    a.out_mul = 1.0f / Ly.f_prescale;
+    a.seg[0] = GemvSeg{Ly.w[6], Ly.scale[6], D, 0};
+    a.nseg = 1;
+    a.P = 1;
+    a.S = Ly.S_d;
+    a.waves = 4;
+    a.out = m->down_part;
+    a.ldo = D;
+    a.split_stride = (size_t)M * D;
+    a.counter = m->counters + 1;
+    a.fin_kind = 1;
+    a.fin = fin_next(m, rc, l, m->x2n, m->down_part, Ly.S_d, (size_t)M * D);
+    ProfScope ps(PC_DOWN, (double)F * D / 2, st);
+    if (int rc2 = launch_gemv(a, st)) return rc2;
+  }
+  return MS_OK;
+}
+
+// ---- streaming: two HBM slots filled on the copy stream ----------------------
+static int stream_prefetch(ms_model *m, int l, hipStream_t st) {
+  const int s = l & 1;
+  Layer &Ly = m->L[l];
+  // the slot is free once the layer that used it two steps ago has finished
+  MS_HIP_TRY(hipStreamWaitEvent(ctx().copy_stream, m->ev_free[s], 0));
+  for (int i = 0; i < 7; ++i)
+    MS_HIP_TRY(hipMemcpyAsync(m->slot[s] + Ly.off[i], Ly.h_packed[i], Ly.bytes[i],
+                              hipMemcpyHostToDevice, ctx().copy_stream));
+  MS_HIP_TRY(hipEventRecord(m->ev_ready[s], ctx().copy_stream));
+  (void)st;
+  return MS_OK;
+}
+
+static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
+  const bool streaming = !m->d.resident;
+  const int l0 = rc.first_layer, l1 = rc.first_layer + rc.n_layers;
+  if (streaming) {
+    // per-call timing: [copy start, copy end] per layer and compute waits
+    m->stats = ms_stream_stats{};
+    auto t0 = std::chrono::steady_clock::now();
+    std::vector<hipEvent_t> ev;
+    auto mk = [&]() {
+      hipEvent_t e;
+      (void)hipEventCreate(&e);
+      ev.push_back(e);
+      return e;
+    };
+    MS_HIP_TRY(hipEventRecord(m->ev_free[0], st));
+    MS_HIP_TRY(hipEventRecord(m->ev_free[1], st));
+    std::vector<hipEvent_t> cp0, cp1, w0, w1;
+    for (int l = l0; l < l1; ++l) {
+      hipEvent_t a = mk(), b = mk();
+      MS_HIP_TRY(hipEventRecord(a, ctx().copy_stream));
+      if (int r = stream_prefetch(m, l, st)) return r;
+      MS_HIP_TRY(hipEventRecord(b, ctx().copy_stream));
+      cp0.push_back(a);
+      cp1.push_back(b);
+      const int s = l & 1;
+      hipEvent_t c = mk(), e = mk();
+      MS_HIP_TRY(hipEventRecord(c, st));
+      MS_HIP_TRY(hipStreamWaitEvent(st, m->ev_ready[s], 0));
+      MS_HIP_TRY(hipEventRecord(e, st));
+      w0.push_back(c);
+      w1.push_back(e);
+      for (int i = 0; i < 7; ++i) m->L[l].w[i] = m->slot[s] + m->L[l].off[i];
+      if (int r = enqueue_layer(m, l, rc, st)) return r;
+      MS_HIP_TRY(hipEventRecord(m->ev_free[s], st));
+    }
+    MS_HIP_TRY(hipStreamSynchronize(st));
+    MS_HIP_TRY(hipStreamSynchronize(ctx().copy_stream));
+    double io = 0, wait = 0;
+    for (size_t i = 0; i < cp0.size(); ++i) {
+      float a = 0, b = 0;
+      (void)hipEventElapsedTime(&a, cp0[i], cp1[i]);
+      (void)hipEventElapsedTime(&b, w0[i], w1[i]);
+      io += a;
+      wait += b;
+    }
+    for (auto e : ev) (void)hipEventDestroy(e);
+    const double total =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
+            .count();
+    m->stats.io_ms = io;
+    m->stats.wait_ms = wait;
+    m->stats.total_ms = total;
+    m->stats.compute_ms = total - wait;
+    return MS_OK;
+  }
+  for (int l = l0; l < l1; ++l)
+    if (int r = enqueue_layer(m, l, rc, st)) return r;
+  return MS_OK;
+}
+
+static int check_positions(ms_model *m, const int *base, int B, int T, int extra) {
+  for (int b = 0; b < B; ++b) {
+    MS_CHECK_ARG(base[b] >= 0, "model: negative position");
+    MS_CHECK_ARG(base[b] + T + extra <= m->d.max_pos,
+                 "model: position beyond max_pos (RoPE tables)");
+    for (auto &Ly : m->L)
+      if (Ly.d.cache_kind == MS_CACHE_LINEAR && !Ly.d.clamp_reads)
+        MS_CHECK_ARG(base[b] + T + extra <= Ly.d.cache_len,
+                     "model: positions exceed a linear KV cache (the reference reads "
+                     "out of bounds here, main.mojo:463,476-477)");
+  }
+  return MS_OK;
+}
+
+static int check_ready(ms_model *m, bool need_lm) {
+  for (size_t l = 0; l < m->L.size(); ++l)
+    if (m->L[l].set_mask != 0x7f)
+      return fail(MS_E_STATE, "model: layer " + std::to_string(l) + " has unset matrices");
+  if (need_lm && !m->has_lm) return fail(MS_E_STATE, "model: LM head not set");
+  return MS_OK;
+}
+
+}  // namespace ms
+
+using namespace ms;
+
+extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *layers,
+                               ms_model **out) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(desc && layers && out, "model_create: null argument");
+  const ms_model_desc &d = *desc;
+  MS_CHECK_ARG(d.hidden > 0 && d.hidden % 128 == 0, "model: hidden % 128 != 0");
+  MS_CHECK_ARG(d.ffn > 0 && d.ffn % 128 == 0, "model: ffn % 128 != 0");
+  MS_CHECK_ARG(d.n_layers > 0, "model: n_layers <= 0");
+  MS_CHECK_ARG(d.max_seqs >= 1 && d.max_rows >= 1 && d.max_seqs * d.max_rows <= 16,
+               "model: max_seqs * max_rows must be in [1, 16]");
+  MS_CHECK_ARG(d.max_pos >= 1, "model: max_pos < 1");
+  MS_CHECK_ARG(d.vocab == 0 || d.vocab % 64 == 0, "model: vocab % 64 != 0");
+  auto *m = new ms_model();
+  m->d = d;
+  m->Mmax = d.max_seqs * d.max_rows;
+  m->h_pos.assign(d.max_seqs, 0);
+  const int M = m->Mmax;
+  auto cleanup = [&](int rc) {
+    ms_model_destroy(m);
+    return rc;
+  };
+  size_t max_part = 0;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const ms_layer_desc &ld = layers[l];
+    if (!(ld.n_heads > 0 && ld.n_kv_heads > 0 && ld.n_heads % ld.n_kv_heads == 0 &&
+          ld.q_dim == ld.n_heads * ld.head_dim && ld.kv_dim == ld.n_kv_heads * ld.head_dim &&
+          ld.q_dim % 128 == 0 && ld.kv_dim % 16 == 0 && ld.rot_dim > 0 &&
+          ld.rot_dim % 2 == 0 && ld.rot_dim <= ld.head_dim && ld.cache_len > 0 &&
+          (ld.cache_kind == MS_CACHE_LINEAR || ld.cache_kind == MS_CACHE_CIRCULAR)))
+      return cleanup(fail(MS_E_INVALID, "model: inconsistent layer " + std::to_string(l) +
+                                            " (ShapeGuard: q_dim = n_heads*head_dim, "
+                                            "kv_dim = n_kv*head_dim, q_dim % 128 == 0)"));
+    Layer Ly;
+    Ly.d = ld;
+    const size_t K[7] = {(size_t)d.hidden, (size_t)d.hidden, (size_t)d.hidden,
+                         (size_t)ld.q_dim, (size_t)d.hidden, (size_t)d.hidden,
+                         (size_t)d.ffn};
+    const size_t N[7] = {(size_t)ld.q_dim, (size_t)ld.kv_dim, (size_t)ld.kv_dim,
+                         (size_t)d.hidden, (size_t)d.ffn, (size_t)d.ffn, (size_t)d.hidden};
+    size_t off = 0;
+    for (int i = 0; i < 7; ++i) {
+      Ly.bytes[i] = K[i] * N[i] / 2;
+      Ly.off[i] = off;
+      off += (Ly.bytes[i] + 4095) & ~(size_t)4095;
+    }
+    m->slot_bytes = std::max(m->slot_bytes, off);
+    // rope table id
+    int rid = -1;
+    for (size_t r = 0; r < m->ropes.size(); ++r)
+      if (m->ropes[r].rot == ld.rot_dim && m->ropes[r].theta == ld.theta) rid = (int)r;
+    if (rid < 0) {
+      RopeTab t;
+      t.rot = ld.rot_dim;
+      t.theta = ld.theta;
+      m->ropes.push_back(t);
+      rid = (int)m->ropes.size() - 1;
+    }
+    Ly.rope = rid;
+    const int ncols_qkv = ld.q_dim + 2 * ld.kv_dim;
+    Ly.S_qkv = pick_split(ncols_qkv / 16, d.hidden / 128, 512);
+    Ly.S_o = pick_split(d.hidden / 16, ld.q_dim / 128, 512);
+    Ly.S_d = pick_split(d.hidden / 16, d.ffn / 128, 512);
+    const int span = ld.cache_kind == MS_CACHE_CIRCULAR ? ld.cache_len + d.max_rows - 1
+                                                        : ld.cache_len + d.max_rows;
+    Ly.n_chunks = cdiv(span, kAttnChunk);
+    const int G = ld.n_heads / ld.n_kv_heads;
+    max_part = std::max(max_part, (size_t)d.max_seqs * ld.n_kv_heads * Ly.n_chunks *
+                                      d.max_rows * G * (ld.head_dim + 2));
+    m->qkv_max = std::max(m->qkv_max, ncols_qkv);
+    m->q_max = std::max(m->q_max, ld.q_dim);
+    m->kv_max = std::max(m->kv_max, ld.kv_dim);
+    m->hd_max = std::max(m->hd_max, ld.head_dim);
+    m->L.push_back(Ly);
+  }
+  int rc;
+  const int D = d.hidden, F = d.ffn;
+  if ((rc = dmalloc(m, (void **)&m->x_in, (size_t)M * D * 4)) ||
+      (rc = dmalloc(m, (void **)&m->xn, (size_t)M * D * 4)) ||
+      (rc = dmalloc(m, (void **)&m->x2n, (size_t)M * D * 4)) ||
+      (rc = dmalloc(m, (void **)&m->aA_hi, (size_t)M * D * 2)) ||
+      (rc = dmalloc(m, (void **)&m->aA_lo, (size_t)M * D * 2)) ||
+      (rc = dmalloc(m, (void **)&m->aO_hi, (size_t)M * m->q_max * 2)) ||
+      (rc = dmalloc(m, (void **)&m->aO_lo, (size_t)M * m->q_max * 2)) ||
+      (rc = dmalloc(m, (void **)&m->aF_hi, (size_t)M * F * 2)) ||
+      (rc = dmalloc(m, (void **)&m->aF_lo, (size_t)M * F * 2)))
+    return cleanup(rc);
+  int sq = 1, so = 1, sd = 1;
+  for (auto &Ly : m->L) {
+    sq = std::max(sq, Ly.S_qkv);
+    so = std::max(so, Ly.S_o);
+    sd = std::max(sd, Ly.S_d);
+  }
+  if ((rc = dmalloc(m, (void **)&m->qkv_part, (size_t)sq * M * m->qkv_max * 4)) ||
+      (rc = dmalloc(m, (void **)&m->o_part, (size_t)so * M * D * 4)) ||
+      (rc = dmalloc(m, (void **)&m->down_part, (size_t)sd * M * D * 4)) ||
+      (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
+      (rc = dmalloc(m, (void **)&m->counters, 4096 * 4)) ||
+      (rc = dmalloc(m, (void **)&m->pos, 64 * 4)) ||
+      (rc = dmalloc(m, (void **)&m->tok, 64 * 4)) ||
+      (rc = dmalloc(m, (void **)&m->step, 64 * 4)) ||
+      (rc = dmalloc(m, (void **)&m->ids_hist, (size_t)m->hist_cap * d.max_seqs * 4)))
+    return cleanup(rc);
+  if (hipMemset(m->counters, 0, 4096 * 4) != hipSuccess ||
+      hipMemset(m->pos, 0, 64 * 4) != hipSuccess || hipMemset(m->step, 0, 64 * 4) != hipSuccess ||
+      hipMemset(m->tok, 0, 64 * 4) != hipSuccess)
+    return cleanup(fail(MS_E_HIP, "model: memset failed"));
+  MS_CHECK_ARG(16 + d.max_seqs * 64 < 4096, "model: too many attention counters");
+  // KV caches (zero-initialised like the reference's resized Lists)
+  for (auto &Ly : m->L) {
+    const size_t per_seq = (size_t)Ly.d.cache_len * Ly.d.kv_dim;
+    Ly.cache_seq_stride = per_seq;
+    if ((rc = dmalloc(m, (void **)&Ly.kc, per_seq * d.max_seqs * 4)) ||
+        (rc = dmalloc(m, (void **)&Ly.vc, per_seq * d.max_seqs * 4)))
+      return cleanup(rc);
+    (void)hipMemset(Ly.kc, 0, per_seq * d.max_seqs * 4);
+    (void)hipMemset(Ly.vc, 0, per_seq * d.max_seqs * 4);
+  }
+  // RoPE tables for positions 0..max_pos-1
+  for (auto &t : m->ropes) {
+    std::vector<float> cs, sn;
+    rope_table_host(t.rot, t.theta, 0, d.max_pos, cs, sn);
+    if ((rc = dmalloc(m, (void **)&t.cs, cs.size() * 4)) ||
+        (rc = dmalloc(m, (void **)&t.sn, sn.size() * 4)))
+      return cleanup(rc);
+    (void)hipMemcpy(t.cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
+    (void)hipMemcpy(t.sn, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+  }
+  if (d.vocab > 0) {
+    m->lm_blocks = d.vocab / 64;
+    if ((rc = dmalloc(m, (void **)&m->arg_val, (size_t)m->lm_blocks * M * 4)) ||
+        (rc = dmalloc(m, (void **)&m->arg_idx, (size_t)m->lm_blocks * M * 4)))
+      return cleanup(rc);
+  }
+  if (!d.resident) {
+    for (int s = 0; s < 2; ++s) {
+      if ((rc = dmalloc(m, (void **)&m->slot[s], m->slot_bytes))) return cleanup(rc);
+      (void)hipEventCreateWithFlags(&m->ev_free[s], hipEventDefault);
+      (void)hipEventCreateWithFlags(&m->ev_ready[s], hipEventDefault);
+    }
+  }
+  *out = m;
+  return MS_OK;
+}
+
+extern "C" int ms_model_destroy(ms_model *m) {
+  if (!m) return MS_OK;
+  (void)hipStreamSynchronize(ctx().stream);
+  (void)hipStreamSynchronize(ctx().copy_stream);
+  if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+  for (auto &Ly : m->L)
+    for (int i = 0; i < 7; ++i)
+      if (Ly.h_packed[i]) (void)hipHostFree(Ly.h_packed[i]);
+  for (int s = 0; s < 2; ++s) {
+    if (m->ev_free[s]) (void)hipEventDestroy(m->ev_free[s]);
+    if (m->ev_ready[s]) (void)hipEventDestroy(m->ev_ready[s]);
+  }
+  for (void *p : m->allocs) (void)hipFree(p);
+  delete m;
+  return MS_OK;
+}
+
+extern "C" int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_t *src,
+                                   int src_on_device, float scale) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && src, "set_matrix: null argument");
+  MS_CHECK_ARG(layer >= 0 && layer < (int)m->L.size(), "set_matrix: bad layer");
+  MS_CHECK_ARG(mat >= 0 && mat < 7, "set_matrix: mat must be 0..6");
+  MS_CHECK_ARG(scale > 0.f && std::isfinite(scale),
+               "set_matrix: scale must be > 0 (TensorGuard, stream_runner.mojo:365-367)");
+  Layer &Ly = m->L[layer];
+  const int D = m->d.hidden, F = m->d.ffn;
+  const int K[7] = {D, D, D, Ly.d.q_dim, D, D, F};
+  const int N[7] = {Ly.d.q_dim, Ly.d.kv_dim, Ly.d.kv_dim, D, F, F, D};
+  hipStream_t st = ctx().stream;
+  if (m->d.resident) {
+    if (!Ly.w[mat]) {
+      int rc = dmalloc(m, (void **)&Ly.w[mat], Ly.bytes[mat]);
+      if (rc) return rc;
+    }
+    const uint8_t *dsrc = src;
+    void *tmp = nullptr;
+    if (!src_on_device) {
+      MS_HIP_TRY(hipMalloc(&tmp, Ly.bytes[mat]));
+      MS_HIP_TRY(hipMemcpyAsync(tmp, src, Ly.bytes[mat], hipMemcpyHostToDevice, st));
+      dsrc = static_cast<const uint8_t *>(tmp);
+    }
+    int rc = pack_device(Ly.w[mat], dsrc, K[mat], N[mat], st);
+    if (tmp) {
+      (void)hipStreamSynchronize(st);
+      (void)hipFree(tmp);
+    }
+    if (rc) return rc;
+  } else {
+    MS_CHECK_ARG(!src_on_device, "set_matrix: streaming models take host weights");
+    if (!Ly.h_packed[mat])
+      if (hipHostMalloc((void **)&Ly.h_packed[mat], Ly.bytes[mat], hipHostMallocDefault) !=
+          hipSuccess)
+        return fail(MS_E_NOMEM, "set_matrix: pinned allocation failed");
+    if (int rc = ms_host_q4_pack(Ly.h_packed[mat], src, K[mat], N[mat])) return rc;
+  }
+  Ly.scale[mat] = scale;
+  Ly.set_mask |= 1 << mat;
+  // fp16 range of the activations feeding O and Down (see pow2_prescale):
+  // |v| <= 8*s_v*D, |swiglu| <= |gate||up| <= (8*s_g*D)(8*s_u*D).
+  const double bD = (double)D;
+  if (Ly.set_mask & (1 << 2)) Ly.o_prescale = pow2_prescale(8.0 * Ly.scale[2] * bD);
+  if ((Ly.set_mask & 0x30) == 0x30)
+    Ly.f_prescale = pow2_prescale(64.0 * Ly.scale[4] * Ly.scale[5] * bD * bD);
+  if (m->gexec) {
+    (void)hipGraphExecDestroy(m->gexec);
+    m->gexec = nullptr;
+  }
+  return MS_OK;
+}
+
+extern "C" int ms_model_set_ple(ms_model *m, int layer, float ple) {
+  MS_CHECK_ARG(m && layer >= 0 && layer < (int)m->L.size(), "set_ple: bad layer");
+  MS_CHECK_ARG(ple > 0.f && std::isfinite(ple), "set_ple: PLE scale must be > 0");
+  m->L[layer].ple = ple;
+  if (m->gexec) {
+    (void)hipGraphExecDestroy(m->gexec);
+    m->gexec = nullptr;
+  }
+  return MS_OK;
+}
+
+extern "C" int ms_model_set_lm_head(ms_model *m, const uint8_t *src, int src_on_device,
+                                    float scale, const float *h_gamma) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && src, "set_lm_head: null argument");
+  MS_CHECK_ARG(m->d.vocab > 0, "set_lm_head: model created with vocab = 0");
+  MS_CHECK_ARG(scale > 0.f, "set_lm_head: scale must be > 0");
+  const int D = m->d.hidden, V = m->d.vocab;
+  const size_t bytes = (size_t)D * V / 2;
+  hipStream_t st = ctx().stream;
+  if (!m->lm_w)
+    if (int rc = dmalloc(m, (void **)&m->lm_w, bytes)) return rc;
+  const uint8_t *dsrc = src;
+  void *tmp = nullptr;
+  if (!src_on_device) {
+    MS_HIP_TRY(hipMalloc(&tmp, bytes));
+    MS_HIP_TRY(hipMemcpyAsync(tmp, src, bytes, hipMemcpyHostToDevice, st));
+    dsrc = static_cast<const uint8_t *>(tmp);
+  }
+  int rc = pack_device(m->lm_w, dsrc, D, V, st);
+  if (tmp) {
+    (void)hipStreamSynchronize(st);
+    (void)hipFree(tmp);
+  }
+  if (rc) return rc;
+  if (h_gamma) {
+    if (!m->gamma)
+      if (int r = dmalloc(m, (void **)&m->gamma, (size_t)D * 4)) return r;
+    MS_HIP_TRY(hipMemcpyAsync(m->gamma, h_gamma, (size_t)D * 4, hipMemcpyHostToDevice, st));
+    MS_HIP_TRY(hipStreamSynchronize(st));
+  }
+  m->lm_scale = scale;
+  m->has_lm = true;
+  if (m->gexec) {
+    (void)hipGraphExecDestroy(m->gexec);
+    m->gexec = nullptr;
+  }
+  return MS_OK;
+}
+
+extern "C" int ms_model_reset(ms_model *m) {
+  MS_CHECK_ARG(m, "reset: null model");
+  std::fill(m->h_pos.begin(), m->h_pos.end(), 0);
+  // positions restart at 0; stale cache contents are never read (every read
+  // position < the current position has been rewritten since the reset)
+  return MS_OK;
+}
+
+static int upload_pos(ms_model *m, const int *h_base, int B, hipStream_t st) {
+  int32_t tmp[64];
+  for (int b = 0; b < B; ++b) tmp[b] = h_base[b];
+  MS_HIP_TRY(hipMemcpyAsync(m->pos, tmp, sizeof(int32_t) * B, hipMemcpyHostToDevice, st));
+  MS_HIP_TRY(hipStreamSynchronize(st));
+  return MS_OK;
+}
+
+static int forward_impl(ms_model *m, int first, int count, float *d_x, int B, int T,
+                        const int *h_base, float *d_hidden) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && d_x && h_base, "forward: null argument");
+  MS_CHECK_ARG(B >= 1 && B <= m->d.max_seqs && T >= 1 && T <= m->d.max_rows,
+               "forward: n_seqs/T exceed the model's max_seqs/max_rows");
+  if (int rc = check_ready(m, false)) return rc;
+  if (int rc = check_positions(m, h_base, B, T, 0)) return rc;
+  hipStream_t st = ctx().stream;
+  if (int rc = upload_pos(m, h_base, B, st)) return rc;
+  const int M = B * T, D = m->d.hidden;
+  // input rows -> PLE + pre-norm of the first layer
+  FinArgs f{};
+  f.M = M;
+  f.D = D;
+  f.base = d_x;
+  f.pre_scale = m->L[first].ple;
+  f.normalize = 1;
+  f.xn_out = m->xn;
+  f.a_hi = m->aA_hi;
+  f.a_lo = m->aA_lo;
+  f.a_prescale = 1.f;
+  if (int rc = launch_fin_rows(f, st)) return rc;
+  RunCfg rc{};
+  rc.B = B;
+  rc.T = T;
+  rc.last_fin = LAST_OUTPUT;
+  rc.out_rows = d_x;
+  rc.hidden = d_hidden;
+  rc.first_layer = first;
+  rc.n_layers = count;
+  if (int r = run_layers(m, rc, st)) return r;
+  if (d_hidden) {
+    // the final layer's output also goes to the caller's rows
+    MS_HIP_TRY(hipMemcpyAsync(d_x, d_hidden + (size_t)(count - 1) * M * D,
+                              (size_t)M * D * 4, hipMemcpyDeviceToDevice, st));
+  }
+  MS_HIP_TRY(hipStreamSynchronize(st));
+  for (int b = 0; b < B; ++b) m->h_pos[b] = h_base[b] + T;
+  return MS_OK;
+}
+
+extern "C" int ms_layer_forward(ms_model *m, int layer, float *d_x, int n_seqs, int T,
+                                const int *h_base) {
+  MS_CHECK_ARG(m && layer >= 0 && layer < (int)m->L.size(), "layer_forward: bad layer");
+  return forward_impl(m, layer, 1, d_x, n_seqs, T, h_base, nullptr);
+}
+
+extern "C" int ms_forward(ms_model *m, float *d_x, int n_seqs, int T, const int *h_base,
+                          float *d_hidden) {
+  MS_CHECK_ARG(m, "forward: null model");
+  return forward_impl(m, 0, (int)m->L.size(), d_x, n_seqs, T, h_base, d_hidden);
+}
+
+// ---- decode --------------------------------------------------------------------
+static int enqueue_decode_step(ms_model *m, int B, hipStream_t st) {
+  const int D = m->d.hidden;
+  {
+    ProfScope ps(PC_PREP, (double)D * B / 2, st);
+    if (int rc = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, m->tok, B, m->x_in, st))
+      return rc;
+    FinArgs f{};
+    f.M = B;
+    f.D = D;
+    f.base = m->x_in;
+    f.pre_scale = m->L[0].ple;
+    f.normalize = 1;
+    f.xn_out = m->xn;
+    f.a_hi = m->aA_hi;
+    f.a_lo = m->aA_lo;
+    f.a_prescale = 1.f;
+    if (int rc = launch_fin_rows(f, st)) return rc;
+  }
+  RunCfg rc{};
+  rc.B = B;
+  rc.T = 1;
+  rc.last_fin = LAST_LM;
+  rc.first_layer = 0;
+  rc.n_layers = (int)m->L.size();
+  if (int r = run_layers(m, rc, st)) return r;
+  GemvArgs a{};
+  a.epi = EPI_ARGMAX;
+  a.K = D;
+  a.M = B;
+  a.a_hi = m->aA_hi;
+  a.a_lo = m->aA_lo;
+  a.lda = D;
+  a.out_mul = 1.f;
+  a.seg[0] = GemvSeg{m->lm_w, m->lm_scale, m->d.vocab, 0};
+  a.nseg = 1;
+  a.P = 4;
+  a.S = 1;
+  a.waves = 4;
+  a.out = nullptr;
+  a.arg_val = m->arg_val;
+  a.arg_idx = m->arg_idx;
+  a.ids_out = nullptr;
+  a.tok_state = m->tok;
+  a.pos_state = m->pos;
+  a.ids_hist = m->ids_hist;
+  a.step_ptr = m->step;
+  a.counter = m->counters + 2;
+  ProfScope ps(PC_LM, (double)D * m->d.vocab / 2, st);
+  return launch_gemv(a, st);
+}
+
+extern "C" int ms_decode_begin(ms_model *m, int n_seqs, const int32_t *h_tokens,
+                               const int32_t *h_pos) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && h_tokens && h_pos, "decode_begin: null argument");
+  MS_CHECK_ARG(n_seqs >= 1 && n_seqs <= m->d.max_seqs, "decode_begin: bad n_seqs");
+  MS_CHECK_ARG(m->d.vocab > 0, "decode_begin: model has no LM head");
+  for (int b = 0; b < n_seqs; ++b)
+    MS_CHECK_ARG(h_tokens[b] >= 0 && h_tokens[b] < m->d.vocab, "decode_begin: bad token id");
+  hipStream_t st = ctx().stream;
+  MS_HIP_TRY(hipMemcpyAsync(m->tok, h_tokens, 4 * n_seqs, hipMemcpyHostToDevice, st));
+  MS_HIP_TRY(hipMemcpyAsync(m->pos, h_pos, 4 * n_seqs, hipMemcpyHostToDevice, st));
+  MS_HIP_TRY(hipStreamSynchronize(st));
+  for (int b = 0; b < n_seqs; ++b) m->h_pos[b] = h_pos[b];
+  m->dec_nseq = n_seqs;
+  return MS_OK;
+}
+
+extern "C" int ms_decode_run(ms_model *m, int n_steps, int use_graph, int32_t *h_ids_out) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && n_steps >= 0, "decode_run: bad arguments");
+  MS_CHECK_ARG(m->dec_nseq >= 1, "decode_run: call ms_decode_begin first");
+  if (int rc = check_ready(m, true)) return rc;
+  const int B = m->dec_nseq;
+  if (int rc = check_positions(m, m->h_pos.data(), B, 1, n_steps - 1)) return rc;
+  if (!m->d.resident) use_graph = 0;  // streaming runs eagerly (host-side slot logic)
+  hipStream_t st = ctx().stream;
+  int done = 0;
+  while (done < n_steps) {
+    const int chunk = std::min(n_steps - done, m->hist_cap);
+    MS_HIP_TRY(hipMemsetAsync(m->step, 0, 4, st));
+    if (use_graph) {
+      if (!m->gexec || m->g_nseq != B) {
+        if (m->gexec) {
+          (void)hipGraphExecDestroy(m->gexec);
+          m->gexec = nullptr;
+        }
+        MS_HIP_TRY(hipStreamSynchronize(st));
+        hipGraph_t g;
+        MS_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_decode_step(m, B, st);
+        hipError_t e = hipStreamEndCapture(st, &g);
+        if (rc) return rc;
+        if (e != hipSuccess) return fail(MS_E_HIP, "decode graph capture failed");
+        MS_HIP_TRY(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
+        (void)hipGraphDestroy(g);
+        m->g_nseq = B;
+      }
+      for (int s = 0; s < chunk; ++s) MS_HIP_TRY(hipGraphLaunch(m->gexec, st));
+    } else {
+      for (int s = 0; s < chunk; ++s)
+        if (int rc = enqueue_decode_step(m, B, st)) return rc;
+    }
+    if (h_ids_out)
+      MS_HIP_TRY(hipMemcpyAsync(h_ids_out + (size_t)done * B, m->ids_hist,
+                                (size_t)chunk * B * 4, hipMemcpyDeviceToHost, st));
+    MS_HIP_TRY(hipStreamSynchronize(st));
+    done += chunk;
+  }
+  if (g_prof.on) prof_collect();
+  for (int b = 0; b < B; ++b) m->h_pos[b] += n_steps;
+  return MS_OK;
+}
+
+extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_tokens,
+                          int pos0, int32_t *h_first_id) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && h_tokens && n_tokens >= 1, "prefill: bad arguments");
+  MS_CHECK_ARG(seq >= 0 && seq < m->d.max_seqs, "prefill: bad sequence index");
+  MS_CHECK_ARG(m->d.vocab > 0, "prefill: model has no LM head");
+  if (int rc = check_ready(m, true)) return rc;
+  for (int i = 0; i < n_tokens; ++i)
+    MS_CHECK_ARG(h_tokens[i] >= 0 && h_tokens[i] < m->d.vocab, "prefill: token id out of range");
+  hipStream_t st = ctx().stream;
+  const int D = m->d.hidden;
+  const int T = m->d.max_rows;
+  int32_t *dtok = nullptr;
+  MS_HIP_TRY(hipMallocAsync((void **)&dtok, (size_t)n_tokens * 4, st));
+  MS_HIP_TRY(hipMemcpyAsync(dtok, h_tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, st));
+  int rcode = MS_OK;
+  for (int c0 = 0; c0 < n_tokens && rcode == MS_OK; c0 += T) {
+    const int t = std::min(T, n_tokens - c0);
+    const int base = pos0 + c0;
+    if ((rcode = check_positions(m, &base, 1, t, 0))) break;
+    MS_HIP_TRY(hipMemcpyAsync(m->pos + seq, &base, 4, hipMemcpyHostToDevice, st));
+    if ((rcode = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, dtok + c0, t, m->x_in, st)))
+      break;
+    FinArgs f{};
+    f.M = t;
+    f.D = D;
+    f.base = m->x_in;
+    f.pre_scale = m->L[0].ple;
+    f.normalize = 1;
+    f.xn_out = m->xn;
+    f.a_hi = m->aA_hi;
+    f.a_lo = m->aA_lo;
+    f.a_prescale = 1.f;
+    if ((rcode = launch_fin_rows(f, st))) break;
+    const bool last = c0 + t >= n_tokens;
+    RunCfg rc{};
+    rc.B = 1;
+    rc.T = t;
+    rc.last_fin = last ? LAST_LM : LAST_OUTPUT;
+    rc.out_rows = m->x_in;  // intermediate chunks: output unused
+    rc.seq0 = seq;
+    rc.first_layer = 0;
+    rc.n_layers = (int)m->L.size();
+    if ((rcode = run_layers(m, rc, st))) break;
+    if (last) {
+      // LM head on the last prompt row only
+      GemvArgs a{};
+      a.epi = EPI_ARGMAX;
+      a.K = D;
+      a.M = 1;
+      a.a_hi = m->aA_hi + (size_t)(t - 1) * D;
+      a.a_lo = m->aA_lo + (size_t)(t - 1) * D;
+      a.lda = D;
+      a.out_mul = 1.f;
+      a.seg[0] = GemvSeg{m->lm_w, m->lm_scale, m->d.vocab, 0};
+      a.nseg = 1;
+      a.P = 4;
+      a.S = 1;
+      a.waves = 4;
+      a.arg_val = m->arg_val;
+      a.arg_idx = m->arg_idx;
+      a.ids_out = m->tok + seq;
+      a.counter = m->counters + 2;
+      if ((rcode = launch_gemv(a, st))) break;
+    }
+  }
+  (void)hipFreeAsync(dtok, st);
+  if (rcode) return rcode;
+  int32_t id = 0;
+  MS_HIP_TRY(hipMemcpyAsync(&id, m->tok + seq, 4, hipMemcpyDeviceToHost, st));
+  MS_HIP_TRY(hipStreamSynchronize(st));
+  if (h_first_id) *h_first_id = id;
+  m->h_pos[seq] = pos0 + n_tokens;
+  return MS_OK;
+}
+
+extern "C" int ms_model_stream_stats(ms_model *m, ms_stream_stats *out) {
+  MS_CHECK_ARG(m && out, "stream_stats: null argument");
+  *out = m->stats;
+  return MS_OK;
+}
+
+extern "C" int ms_prof_enable(int on) {
+  g_prof.on = on != 0;
+  for (int i = 0; i < MS_PROF_CLASSES; ++i) {
+    g_prof.launches[i] = 0;
+    g_prof.ms[i] = 0;
+    g_prof.bytes[i] = 0;
+  }
+  return MS_OK;
+}
+
+extern "C" int ms_prof_get(int cls, const char **name, long *launches, double *total_ms,
+                           double *bytes) {
+  MS_CHECK_ARG(cls >= 0 && cls < MS_PROF_CLASSES, "prof_get: bad class");
+  if (g_prof.on && !g_prof.pending.empty()) prof_collect();
+  if (name) *name = kProfNames[cls];
+  if (launches) *launches = g_prof.launches[cls];
+  if (total_ms) *total_ms = g_prof.ms[cls];
+  if (bytes) *bytes = g_prof.bytes[cls];
+  return MS_OK;
+}

@@ -1,0 +1,93 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/ms_gpu.h declares, reports errors instead of crashing before ms_init,
+and its host-side helpers (seeded generator, panel packer) are correct."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+import mojostream_amd as ms
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    txt = open(os.path.join(ROOT, "include", "ms_gpu.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(ms_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_header_function():
+    lib = C.CDLL(ms.LIB_PATH)
+    names = header_functions()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(ms.EXPORTED)
+
+
+def test_calls_before_init_fail_cleanly():
+    p = C.c_void_p()
+    rc = ms.lib().ms_malloc(C.byref(p), 16)
+    assert rc == -3  # MS_E_STATE
+    assert b"ms_init" in ms.lib().ms_last_error()
+
+
+def test_host_generator_is_deterministic_and_uniform():
+    a = ms.host_random_u8(1 << 16, 42, 7)
+    b = ms.host_random_u8(1 << 16, 42, 7)
+    c = ms.host_random_u8(1 << 16, 42, 8)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    lo, hi = a & 15, a >> 4
+    for nib in (lo, hi):  # both nibbles uniform over 0..15
+        h = np.bincount(nib, minlength=16) / nib.size
+        assert np.all(np.abs(h - 1 / 16) < 0.01)
+    assert ms.host_random_u8(13, 1, 2).tolist() == ms.host_random_u8(16, 1, 2)[:13].tolist()
+    s = [ms.host_uniform(42, 1, i, 0.04, 0.15) for i in range(200)]
+    assert min(s) >= 0.04 and max(s) < 0.15
+    n = ms.host_normal(20000, 3, 4)
+    assert abs(n.mean()) < 0.03 and abs(n.std() - 1) < 0.03
+
+
+def panel_pack_reference(q4: np.ndarray, K: int, N: int) -> np.ndarray:
+    """Independent statement of the panel layout: for column n and row k the
+    nibble sits in panel n//16, super-tile k//128, lane (n%16)+16*((k%128)//32),
+    dword (k%32)//8, nibble (e>>1)+4*(e&1) with e = k%8."""
+    out = np.zeros(K * N // 8, np.uint32)
+    W = np.empty((K, N), np.uint32)
+    W[:, 0::2] = q4 & 15
+    W[:, 1::2] = q4 >> 4
+    k = np.arange(K)[:, None]
+    n = np.arange(N)[None, :]
+    lane = (n % 16) + 16 * ((k % 128) // 32)
+    dword = (n // 16) * (K * 2) + (k // 128) * 256 + lane * 4 + (k % 32) // 8
+    e = k % 8
+    q = (e >> 1) + 4 * (e & 1)
+    np.bitwise_or.at(out, dword.ravel(), (W << (4 * q)).ravel().astype(np.uint32))
+    return out.view(np.uint8)
+
+
+def test_host_pack_matches_layout_definition():
+    K, N = 256, 48
+    q4 = ms.host_random_u8(K * N // 2, 5, 5).reshape(K, N // 2)
+    got = np.empty(K * N // 2, np.uint8)
+    ms.check(ms.lib().ms_host_q4_pack(got.ctypes.data, q4.ctypes.data, K, N))
+    assert np.array_equal(got, panel_pack_reference(q4, K, N))
+    assert ms.lib().ms_q4_packed_bytes(K, N) == K * N // 2
+
+
+def test_host_pack_rejects_bad_shapes():
+    buf = np.zeros(1024, np.uint8)
+    assert ms.lib().ms_host_q4_pack(buf.ctypes.data, buf.ctypes.data, 100, 16) == -1
+    assert ms.lib().ms_host_q4_pack(buf.ctypes.data, buf.ctypes.data, 128, 8) == -1
+
+
+def test_arch_presets_match_reference_sizes():
+    e4b = ms.arch_e4b()
+    # per-layer block sizes of sparse_pin.mojo:38-39
+    assert e4b.layer_bytes(0) == 45875200 and e4b.layer_bytes(5) == 52428800
+    assert e4b.weight_bytes() == 1972633600
+    assert [l for l in range(42) if ms.e4b_is_full(l)] == [5, 11, 17, 23, 29, 35, 41]
+    assert ms.arch_14b().weight_bytes() == 6606028800
+    assert ms.arch_demo().weight_bytes() == 304087040
