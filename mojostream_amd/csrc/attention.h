@@ -20,19 +20,22 @@ struct AttnArgs {
   const int32_t *pos;          // base position per sequence [B]
   float *kc, *vc;              // caches [B][cache_len][kv_dim]
   size_t cache_seq_stride;     // floats between sequences
-  int n_chunks, CH;
+  int n_chunks;                // chunks of kAttnChunk keys per (sequence, kv head)
   float *part;                 // [B][n_kv][n_chunks][T*G][hd+2]
-  unsigned *counters;          // [B*n_kv], zero between uses
+  // combine
   float *out;                  // [B*T][q_dim] or null
   _Float16 *out_hi, *out_lo;   // [B*T][q_dim] or null
   float out_prescale;
   int write_cache;
 };
 
-constexpr int kAttnChunk = 32;
-constexpr int kAttnMaxTG = 20;   // T * (n_heads / n_kv)
-constexpr int kAttnLds = 12288;  // floats of q/k/v staging
+constexpr int kAttnChunk = 16;
+constexpr int kAttnMaxTG = 20;    // T * (n_heads / n_kv) per block
+constexpr int kAttnLds = 10240;   // floats of q staging
+constexpr int kAttnMaxChunks = 512;
 
+// Scores + chunk softmax + P.V partials, then the merge of the chunks with the
+// cache append of the rows (two launches).
 int launch_attention(const AttnArgs &a, hipStream_t st);
 int attn_check(const AttnArgs &a);
 

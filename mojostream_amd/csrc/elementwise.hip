@@ -189,7 +189,6 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.S = 1;
   a.ld = ld;
   a.apply_rope = 0;
-  a.CH = kAttnChunk;
   const int span = (L->cache_kind == MS_CACHE_CIRCULAR) ? L->cache_len + T - 1
                                                         : (base + T);
   a.n_chunks = cdiv(span, kAttnChunk);
@@ -202,25 +201,22 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   const int G = a.n_heads / a.n_kv;
   const size_t qkv_f = (size_t)T * ld;
   const size_t part_f = (size_t)a.n_kv * a.n_chunks * T * G * (a.hd + 2);
-  const size_t need = (qkv_f + part_f) * 4 + 64 * 4 + 64;
+  const size_t need = (qkv_f + part_f) * 4 + 64;
   void *buf = nullptr;
   if (int rc = scratch(need, &buf)) return rc;
   float *qkv = static_cast<float *>(buf);
   float *part = qkv + qkv_f;
-  unsigned *cnt = reinterpret_cast<unsigned *>(part + part_f);
-  int32_t *dpos = reinterpret_cast<int32_t *>(cnt + 32);
+  int32_t *dpos = reinterpret_cast<int32_t *>(part + part_f);
   MS_HIP_TRY(hipMemcpy2DAsync(qkv, ld * 4, d_q, L->q_dim * 4, L->q_dim * 4, T,
                               hipMemcpyDeviceToDevice, st));
   MS_HIP_TRY(hipMemcpy2DAsync(qkv + L->q_dim, ld * 4, d_knew, L->kv_dim * 4,
                               L->kv_dim * 4, T, hipMemcpyDeviceToDevice, st));
   MS_HIP_TRY(hipMemcpy2DAsync(qkv + L->q_dim + L->kv_dim, ld * 4, d_vnew, L->kv_dim * 4,
                               L->kv_dim * 4, T, hipMemcpyDeviceToDevice, st));
-  MS_HIP_TRY(hipMemsetAsync(cnt, 0, 32 * sizeof(unsigned), st));
   MS_HIP_TRY(hipMemcpyAsync(dpos, &base, sizeof(int32_t), hipMemcpyHostToDevice, st));
   a.qkv = qkv;
   a.split_stride = qkv_f;
   a.part = part;
-  a.counters = cnt;
   a.pos = dpos;
   if (int rc = launch_attention(a, st)) return rc;
   MS_HIP_TRY(hipStreamSynchronize(st));
@@ -250,8 +246,6 @@ extern "C" int ms_lm_head_argmax(const float *d_x, int M, int D, const uint8_t *
   _Float16 *hi = static_cast<_Float16 *>(buf), *lo = hi + hl;
   float *bv = reinterpret_cast<float *>(lo + hl);
   int32_t *bi = reinterpret_cast<int32_t *>(bv + blocks * M);
-  unsigned *cnt = reinterpret_cast<unsigned *>(bi + blocks * M);
-  MS_HIP_TRY(hipMemsetAsync(cnt, 0, sizeof(unsigned), st));
   // final-norm outputs are bounded by sqrt(D) * max|gamma|; no prescale needed
   if (int rc = launch_split(d_x, M, D, D, 1.0f, hi, lo, D, st)) return rc;
   GemvArgs a{};
@@ -271,9 +265,14 @@ extern "C" int ms_lm_head_argmax(const float *d_x, int M, int D, const uint8_t *
   a.ldo = vocab;
   a.arg_val = bv;
   a.arg_idx = bi;
-  a.ids_out = d_ids;
-  a.counter = cnt;
   if (int rc = launch_gemv(a, st)) return rc;
+  ArgmaxFin f{};
+  f.arg_val = bv;
+  f.arg_idx = bi;
+  f.n_blocks = (int)blocks;
+  f.M = M;
+  f.ids_out = d_ids;
+  if (int rc = launch_argmax_fin(f, st)) return rc;
   MS_HIP_TRY(hipStreamSynchronize(st));
   return MS_OK;
 }

@@ -93,7 +93,6 @@ struct ms_model {
   float *qkv_part = nullptr, *attn_part = nullptr, *o_part = nullptr,
         *down_part = nullptr;
   size_t qkv_part_stride = 0, o_part_stride = 0, d_part_stride = 0;
-  unsigned *counters = nullptr;  // [0] O, [1] Down, [2] LM, [16..] attention
   int32_t *pos = nullptr, *tok = nullptr, *ids_hist = nullptr, *step = nullptr;
   int hist_cap = 1024;
   float *arg_val = nullptr;
@@ -185,47 +184,69 @@ static void prof_collect() {
 // ---- per-layer enqueue --------------------------------------------------------
 struct RunCfg {
   int B, T;                 // sequences, rows per sequence
-  int last_fin;             // what the last Down block does after the final layer
-  float *out_rows;          // LAST_OUTPUT: layer output rows
-  float *hidden;            // optional [L][M][D]
+  const float *in_rows;     // first layer input rows [B*T][D]
+  float *out_rows;          // layer output of the last layer (or null)
+  float *hidden;            // optional [n_layers][B*T][D]
   int first_layer, n_layers;
   int seq0;                 // first sequence (caches / positions offset)
 };
-enum { LAST_OUTPUT = 0, LAST_LM = 1 };
 
-static FinArgs fin_next(ms_model *m, const RunCfg &rc, int l, const float *base,
-                        const float *parts, int n_parts, size_t stride) {
-  FinArgs f{};
-  const int M = rc.B * rc.T;
-  f.M = M;
-  f.D = m->d.hidden;
-  f.base = base;
-  f.parts = parts;
-  f.n_parts = n_parts;
-  f.part_stride = stride;
-  f.a_prescale = 1.f;
-  const int last = rc.first_layer + rc.n_layers - 1;
-  if (rc.hidden && l >= 0)
-    f.hidden_out = rc.hidden + (size_t)(l - rc.first_layer) * M * m->d.hidden;
-  if (l < last) {
-    f.pre_scale = m->L[l + 1].ple;
-    f.normalize = 1;
-    f.xn_out = m->xn;
-    f.a_hi = m->aA_hi;
-    f.a_lo = m->aA_lo;
-  } else if (rc.last_fin == LAST_LM) {
-    f.pre_scale = 1.f;
-    f.normalize = 1;
-    f.gamma = m->gamma;
-    f.a_hi = m->aA_hi;
-    f.a_lo = m->aA_lo;
-  } else {
-    // plain layer output: write into the caller's rows, no normalisation
-    f.pre_scale = 1.f;
-    f.normalize = 0;
-    if (!f.hidden_out) f.hidden_out = rc.out_rows;
+// LDS bytes of a prologue GEMV (mirrors gemv_lds_bytes in q4.hip).
+static size_t prep_lds(int waves, int P, int M, int K, int S) {
+  const int ks = ((K / 128 + S - 1) / S) * 128;
+  return ((size_t)waves * P * 256 + (size_t)P * M * 16) * 4 + (size_t)2 * M * (ks + 8) * 2;
+}
+
+// GEMV whose activation rows come from a row preparation: in the kernel's LDS
+// prologue when it fits, else through the standalone prep kernel.
+static int gemv_prep(ms_model *m, GemvArgs a, const PrepArgs &p, hipStream_t st) {
+  if (prep_lds(a.waves, a.P, a.M, a.K, a.S) <= 150 * 1024) {
+    a.prep = p;
+    a.prep.on = 1;
+    return launch_gemv(a, st);
   }
-  return f;
+  if (int rc = launch_prep_rows(p, a.M, a.K, m->aA_hi, m->aA_lo, st)) return rc;
+  a.prep = PrepArgs{};
+  a.a_hi = m->aA_hi;
+  a.a_lo = m->aA_lo;
+  a.lda = a.K;
+  return launch_gemv(a, st);
+}
+
+// Row preparation of layer l's attention input: the previous layer's output
+// (x2n + down partials) or the call's input rows, times PLE, rmsnorm.
+static PrepArgs attn_in_prep(ms_model *m, const RunCfg &rc, int l) {
+  PrepArgs p{};
+  const int M = rc.B * rc.T, D = m->d.hidden;
+  p.pre_scale = m->L[l].ple;
+  p.xn_out = m->xn;
+  if (l == rc.first_layer) {
+    p.base = rc.in_rows;
+  } else {
+    p.base = m->x2n;
+    p.parts = m->down_part;
+    p.n_parts = m->L[l - 1].S_d;
+    p.part_stride = (size_t)M * D;
+    if (rc.hidden) p.hid_out = rc.hidden + (size_t)(l - 1 - rc.first_layer) * M * D;
+  }
+  return p;
+}
+
+// The last layer's output x2n + down partials, optionally normalised for the
+// LM head (final norm with gamma, rmsnorm_weighted_inplace kernels.mojo:598-613).
+static PrepArgs final_prep(ms_model *m, const RunCfg &rc) {
+  PrepArgs p{};
+  const int M = rc.B * rc.T, D = m->d.hidden;
+  const int last = rc.first_layer + rc.n_layers - 1;
+  p.base = m->x2n;
+  p.parts = m->down_part;
+  p.n_parts = m->L[last].S_d;
+  p.part_stride = (size_t)M * D;
+  p.pre_scale = 1.f;
+  p.gamma = m->gamma;
+  p.hid_out = rc.out_rows;
+  if (rc.hidden) p.hid_out2 = rc.hidden + (size_t)(rc.n_layers - 1) * M * D;
+  return p;
 }
 
 static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
@@ -235,15 +256,12 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
   const int D = m->d.hidden, F = m->d.ffn;
   const int ld = d.q_dim + 2 * d.kv_dim;
 
-  // 1. QKV
+  // 1. PLE + pre-norm (prologue) and the fused Q|K|V projection
   {
     GemvArgs a{};
     a.epi = EPI_STORE;
     a.K = D;
     a.M = M;
-    a.a_hi = m->aA_hi;
-    a.a_lo = m->aA_lo;
-    a.lda = D;
     a.out_mul = 1.f;
     a.seg[0] = GemvSeg{Ly.w[0], Ly.scale[0], d.q_dim, 0};
     a.seg[1] = GemvSeg{Ly.w[1], Ly.scale[1], d.kv_dim, d.q_dim};
@@ -256,9 +274,9 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.ldo = ld;
     a.split_stride = (size_t)M * ld;
     ProfScope ps(PC_QKV, (double)D * ld / 2, st);
-    if (int rc2 = launch_gemv(a, st)) return rc2;
+    if (int rc2 = gemv_prep(m, a, attn_in_prep(m, rc, l), st)) return rc2;
   }
-  // 2. attention
+  // 2. attention (chunks + merge/cache append)
   {
     AttnArgs a{};
     a.B = rc.B;
@@ -284,19 +302,18 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.kc = Ly.kc + (size_t)rc.seq0 * Ly.cache_seq_stride;
     a.vc = Ly.vc + (size_t)rc.seq0 * Ly.cache_seq_stride;
     a.cache_seq_stride = Ly.cache_seq_stride;
-    a.CH = kAttnChunk;
     a.n_chunks = Ly.n_chunks;
     a.part = m->attn_part;
-    a.counters = m->counters + 16;
     a.out = nullptr;
     a.out_hi = m->aO_hi;
     a.out_lo = m->aO_lo;
     a.out_prescale = Ly.o_prescale;
     a.write_cache = 1;
+    // KV bytes read at the current position are counted by bench.py
     ProfScope ps(PC_ATTN, 0.0, st);
     if (int rc2 = launch_attention(a, st)) return rc2;
   }
-  // 3. O projection; last block: residual + post-attention norm
+  // 3. O projection -> split-K partials
   {
     GemvArgs a{};
     a.epi = EPI_STORE;
@@ -314,33 +331,15 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.out = m->o_part;
     a.ldo = D;
     a.split_stride = (size_t)M * D;
-    a.counter = m->counters + 0;
-    a.fin_kind = 1;
-    FinArgs &f = a.fin;
-    f.M = M;
-    f.D = D;
-    f.base = m->xn;
-    f.parts = m->o_part;
-    f.n_parts = Ly.S_o;
-    f.part_stride = (size_t)M * D;
-    f.pre_scale = 1.f;
-    f.normalize = 1;
-    f.xn_out = m->x2n;
-    f.a_hi = m->aA_hi;
-    f.a_lo = m->aA_lo;
-    f.a_prescale = 1.f;
     ProfScope ps(PC_O, (double)d.q_dim * D / 2, st);
     if (int rc2 = launch_gemv(a, st)) return rc2;
   }
-  // 4. Gate + Up with SwiGLU epilogue
+  // 4. residual + post-attention norm (prologue), Gate|Up, SwiGLU epilogue
   {
     GemvArgs a{};
     a.epi = EPI_SWIGLU;
     a.K = D;
     a.M = M;
-    a.a_hi = m->aA_hi;
-    a.a_lo = m->aA_lo;
-    a.lda = D;
     a.out_mul = 1.f;
     a.seg[0] = GemvSeg{Ly.w[4], Ly.scale[4], F, 0};
     a.seg[1] = GemvSeg{Ly.w[5], Ly.scale[5], F, 0};
@@ -353,10 +352,17 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.sw_lo = m->aF_lo;
     a.ldo_sw = F;
     a.sw_prescale = Ly.f_prescale;
+    PrepArgs p{};
+    p.base = m->xn;
+    p.parts = m->o_part;
+    p.n_parts = Ly.S_o;
+    p.part_stride = (size_t)M * D;
+    p.pre_scale = 1.f;
+    p.xn_out = m->x2n;
     ProfScope ps(PC_GATEUP, (double)D * F, st);
-    if (int rc2 = launch_gemv(a, st)) return rc2;
+    if (int rc2 = gemv_prep(m, a, p, st)) return rc2;
   }
-  // 5. Down; last block: residual, then the next layer's PLE + norm
+  // 5. Down projection -> split-K partials (summed by the next consumer)
   {
     GemvArgs a{};
     a.epi = EPI_STORE;
@@ -374,26 +380,75 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.out = m->down_part;
     a.ldo = D;
     a.split_stride = (size_t)M * D;
-    a.counter = m->counters + 1;
-    a.fin_kind = 1;
-    a.fin = fin_next(m, rc, l, m->x2n, m->down_part, Ly.S_d, (size_t)M * D);
     ProfScope ps(PC_DOWN, (double)F * D / 2, st);
     if (int rc2 = launch_gemv(a, st)) return rc2;
   }
   return MS_OK;
 }
 
+// LM head over rows `row0..row0+M-1` of the last layer's output, then the
+// greedy id per row.
+static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const ArgmaxFin &fin,
+                      hipStream_t st) {
+  const int D = m->d.hidden;
+  PrepArgs p = final_prep(m, rc);
+  p.base += (size_t)row0 * D;
+  p.parts += (size_t)row0 * D;
+  if (p.hid_out) p.hid_out += (size_t)row0 * D;
+  if (p.hid_out2) p.hid_out2 += (size_t)row0 * D;
+  GemvArgs a{};
+  a.epi = EPI_ARGMAX;
+  a.K = D;
+  a.M = M;
+  a.out_mul = 1.f;
+  a.seg[0] = GemvSeg{m->lm_w, m->lm_scale, m->d.vocab, 0};
+  a.nseg = 1;
+  a.P = 4;
+  a.S = 1;
+  a.waves = 4;
+  a.out = nullptr;
+  a.arg_val = m->arg_val;
+  a.arg_idx = m->arg_idx;
+  {
+    // one prep block per row (the head has thousands of blocks, so a per-block
+    // prologue would re-read the residual rows thousands of times)
+    ProfScope ps(PC_LM, (double)D * m->d.vocab / 2, st);
+    if (int r = launch_prep_rows(p, M, D, m->aA_hi, m->aA_lo, st)) return r;
+    a.a_hi = m->aA_hi;
+    a.a_lo = m->aA_lo;
+    a.lda = D;
+    if (int r = launch_gemv(a, st)) return r;
+  }
+  ArgmaxFin f = fin;
+  f.arg_val = m->arg_val;
+  f.arg_idx = m->arg_idx;
+  f.n_blocks = m->lm_blocks;
+  f.M = M;
+  ProfScope ps(PC_OTHER, 0.0, st);
+  return launch_argmax_fin(f, st);
+}
+
+// Output rows of the last layer without an LM head.
+static int enqueue_output(ms_model *m, const RunCfg &rc, hipStream_t st) {
+  PrepArgs p = final_prep(m, rc);
+  p.gamma = nullptr;
+  ProfScope ps(PC_OTHER, 0.0, st);
+  return launch_prep_rows(p, rc.B * rc.T, m->d.hidden, nullptr, nullptr, st);
+}
+
 // ---- streaming: two HBM slots filled on the copy stream ----------------------
-static int stream_prefetch(ms_model *m, int l, hipStream_t st) {
+// Copies layer l's packed weights into slot l%2 once the layer that used the
+// slot before has finished; a/b bracket the copies on the copy stream.
+static int stream_prefetch(ms_model *m, int l, hipEvent_t a, hipEvent_t b) {
   const int s = l & 1;
   Layer &Ly = m->L[l];
-  // the slot is free once the layer that used it two steps ago has finished
   MS_HIP_TRY(hipStreamWaitEvent(ctx().copy_stream, m->ev_free[s], 0));
+  MS_HIP_TRY(hipEventRecord(a, ctx().copy_stream));
   for (int i = 0; i < 7; ++i)
     MS_HIP_TRY(hipMemcpyAsync(m->slot[s] + Ly.off[i], Ly.h_packed[i], Ly.bytes[i],
                               hipMemcpyHostToDevice, ctx().copy_stream));
+  MS_HIP_TRY(hipEventRecord(b, ctx().copy_stream));
   MS_HIP_TRY(hipEventRecord(m->ev_ready[s], ctx().copy_stream));
-  (void)st;
   return MS_OK;
 }
 
@@ -416,9 +471,7 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
     std::vector<hipEvent_t> cp0, cp1, w0, w1;
     for (int l = l0; l < l1; ++l) {
       hipEvent_t a = mk(), b = mk();
-      MS_HIP_TRY(hipEventRecord(a, ctx().copy_stream));
-      if (int r = stream_prefetch(m, l, st)) return r;
-      MS_HIP_TRY(hipEventRecord(b, ctx().copy_stream));
+      if (int r = stream_prefetch(m, l, a, b)) return r;
       cp0.push_back(a);
       cp1.push_back(b);
       const int s = l & 1;
@@ -579,17 +632,14 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
       (rc = dmalloc(m, (void **)&m->o_part, (size_t)so * M * D * 4)) ||
       (rc = dmalloc(m, (void **)&m->down_part, (size_t)sd * M * D * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
-      (rc = dmalloc(m, (void **)&m->counters, 4096 * 4)) ||
       (rc = dmalloc(m, (void **)&m->pos, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->tok, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->step, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->ids_hist, (size_t)m->hist_cap * d.max_seqs * 4)))
     return cleanup(rc);
-  if (hipMemset(m->counters, 0, 4096 * 4) != hipSuccess ||
-      hipMemset(m->pos, 0, 64 * 4) != hipSuccess || hipMemset(m->step, 0, 64 * 4) != hipSuccess ||
+  if (hipMemset(m->pos, 0, 64 * 4) != hipSuccess || hipMemset(m->step, 0, 64 * 4) != hipSuccess ||
       hipMemset(m->tok, 0, 64 * 4) != hipSuccess)
     return cleanup(fail(MS_E_HIP, "model: memset failed"));
-  MS_CHECK_ARG(16 + d.max_seqs * 64 < 4096, "model: too many attention counters");
   // KV caches (zero-initialised like the reference's resized Lists)
   for (auto &Ly : m->L) {
     const size_t per_seq = (size_t)Ly.d.cache_len * Ly.d.kv_dim;
@@ -774,33 +824,16 @@ static int forward_impl(ms_model *m, int first, int count, float *d_x, int B, in
   if (int rc = check_positions(m, h_base, B, T, 0)) return rc;
   hipStream_t st = ctx().stream;
   if (int rc = upload_pos(m, h_base, B, st)) return rc;
-  const int M = B * T, D = m->d.hidden;
-  // input rows -> PLE + pre-norm of the first layer
-  FinArgs f{};
-  f.M = M;
-  f.D = D;
-  f.base = d_x;
-  f.pre_scale = m->L[first].ple;
-  f.normalize = 1;
-  f.xn_out = m->xn;
-  f.a_hi = m->aA_hi;
-  f.a_lo = m->aA_lo;
-  f.a_prescale = 1.f;
-  if (int rc = launch_fin_rows(f, st)) return rc;
   RunCfg rc{};
   rc.B = B;
   rc.T = T;
-  rc.last_fin = LAST_OUTPUT;
+  rc.in_rows = d_x;
   rc.out_rows = d_x;
   rc.hidden = d_hidden;
   rc.first_layer = first;
   rc.n_layers = count;
   if (int r = run_layers(m, rc, st)) return r;
-  if (d_hidden) {
-    // the final layer's output also goes to the caller's rows
-    MS_HIP_TRY(hipMemcpyAsync(d_x, d_hidden + (size_t)(count - 1) * M * D,
-                              (size_t)M * D * 4, hipMemcpyDeviceToDevice, st));
-  }
+  if (int r = enqueue_output(m, rc, st)) return r;
   MS_HIP_TRY(hipStreamSynchronize(st));
   for (int b = 0; b < B; ++b) m->h_pos[b] = h_base[b] + T;
   return MS_OK;
@@ -825,49 +858,20 @@ static int enqueue_decode_step(ms_model *m, int B, hipStream_t st) {
     ProfScope ps(PC_PREP, (double)D * B / 2, st);
     if (int rc = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, m->tok, B, m->x_in, st))
       return rc;
-    FinArgs f{};
-    f.M = B;
-    f.D = D;
-    f.base = m->x_in;
-    f.pre_scale = m->L[0].ple;
-    f.normalize = 1;
-    f.xn_out = m->xn;
-    f.a_hi = m->aA_hi;
-    f.a_lo = m->aA_lo;
-    f.a_prescale = 1.f;
-    if (int rc = launch_fin_rows(f, st)) return rc;
   }
   RunCfg rc{};
   rc.B = B;
   rc.T = 1;
-  rc.last_fin = LAST_LM;
+  rc.in_rows = m->x_in;
   rc.first_layer = 0;
   rc.n_layers = (int)m->L.size();
   if (int r = run_layers(m, rc, st)) return r;
-  GemvArgs a{};
-  a.epi = EPI_ARGMAX;
-  a.K = D;
-  a.M = B;
-  a.a_hi = m->aA_hi;
-  a.a_lo = m->aA_lo;
-  a.lda = D;
-  a.out_mul = 1.f;
-  a.seg[0] = GemvSeg{m->lm_w, m->lm_scale, m->d.vocab, 0};
-  a.nseg = 1;
-  a.P = 4;
-  a.S = 1;
-  a.waves = 4;
-  a.out = nullptr;
-  a.arg_val = m->arg_val;
-  a.arg_idx = m->arg_idx;
-  a.ids_out = nullptr;
-  a.tok_state = m->tok;
-  a.pos_state = m->pos;
-  a.ids_hist = m->ids_hist;
-  a.step_ptr = m->step;
-  a.counter = m->counters + 2;
-  ProfScope ps(PC_LM, (double)D * m->d.vocab / 2, st);
-  return launch_gemv(a, st);
+  ArgmaxFin f{};
+  f.tok_state = m->tok;
+  f.pos_state = m->pos;
+  f.ids_hist = m->ids_hist;
+  f.step = m->step;
+  return enqueue_lm(m, rc, 0, B, f, st);
 }
 
 extern "C" int ms_decode_begin(ms_model *m, int n_seqs, const int32_t *h_tokens,
@@ -956,47 +960,19 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
     MS_HIP_TRY(hipMemcpyAsync(m->pos + seq, &base, 4, hipMemcpyHostToDevice, st));
     if ((rcode = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, dtok + c0, t, m->x_in, st)))
       break;
-    FinArgs f{};
-    f.M = t;
-    f.D = D;
-    f.base = m->x_in;
-    f.pre_scale = m->L[0].ple;
-    f.normalize = 1;
-    f.xn_out = m->xn;
-    f.a_hi = m->aA_hi;
-    f.a_lo = m->aA_lo;
-    f.a_prescale = 1.f;
-    if ((rcode = launch_fin_rows(f, st))) break;
-    const bool last = c0 + t >= n_tokens;
     RunCfg rc{};
     rc.B = 1;
     rc.T = t;
-    rc.last_fin = last ? LAST_LM : LAST_OUTPUT;
-    rc.out_rows = m->x_in;  // intermediate chunks: output unused
+    rc.in_rows = m->x_in;
     rc.seq0 = seq;
     rc.first_layer = 0;
     rc.n_layers = (int)m->L.size();
     if ((rcode = run_layers(m, rc, st))) break;
-    if (last) {
+    if (c0 + t >= n_tokens) {
       // LM head on the last prompt row only
-      GemvArgs a{};
-      a.epi = EPI_ARGMAX;
-      a.K = D;
-      a.M = 1;
-      a.a_hi = m->aA_hi + (size_t)(t - 1) * D;
-      a.a_lo = m->aA_lo + (size_t)(t - 1) * D;
-      a.lda = D;
-      a.out_mul = 1.f;
-      a.seg[0] = GemvSeg{m->lm_w, m->lm_scale, m->d.vocab, 0};
-      a.nseg = 1;
-      a.P = 4;
-      a.S = 1;
-      a.waves = 4;
-      a.arg_val = m->arg_val;
-      a.arg_idx = m->arg_idx;
-      a.ids_out = m->tok + seq;
-      a.counter = m->counters + 2;
-      if ((rcode = launch_gemv(a, st))) break;
+      ArgmaxFin f{};
+      f.ids_out = m->tok + seq;
+      if ((rcode = enqueue_lm(m, rc, t - 1, 1, f, st))) break;
     }
   }
   (void)hipFreeAsync(dtok, st);

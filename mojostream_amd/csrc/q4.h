@@ -21,32 +21,27 @@ enum GemvEpilogue {
   EPI_ARGMAX = 3,      // LM head: logits (optional) + per-block argmax
 };
 
-// Row finalisation run by the last block of a GEMV (or by a prep kernel).
-// x = (base ? base : 0) + sum_{s<n_parts} parts[s]; hidden_out <- x;
-// x *= pre_scale; x = x / rms(x) * (gamma ? gamma : 1);
-// xn_out <- x (fp32); a_hi/a_lo <- split(x * a_prescale).
-struct FinArgs {
-  int M, D;
-  const float *base;    // [M][D] or null
-  const float *parts;   // [n_parts][M][D] or null
+// Optional GEMV prologue: every block rebuilds the activation rows it needs
+// in LDS.  x = base + sum_{s<n_parts} parts[s]; y = rmsnorm(x * pre_scale)
+// (* gamma); the block keeps fp16 hi/lo of y for its K range.  Block 0 also
+// stores x (the previous layer's output) and y (the residual base).
+struct PrepArgs {
+  int on;
+  const float *base;    // [M][K] or null
+  const float *parts;   // [n_parts][M][K] or null
   int n_parts;
   size_t part_stride;   // floats between split slices
-  float *hidden_out;    // [M][D] or null (x before scaling/normalisation)
-  float pre_scale;      // PLE of the next layer, or 1
-  int normalize;        // 0: skip the rmsnorm (plain residual output)
-  const float *gamma;   // final norm weights or null
-  float *xn_out;        // [M][D] or null
-  _Float16 *a_hi, *a_lo;  // [M][D] or null
-  float a_prescale;     // power of two
+  float pre_scale;      // PLE of this layer (1 for the post-attention norm)
+  const float *gamma;   // final-norm weights or null
+  float *xn_out;        // block 0: y [M][K] or null
+  float *hid_out;       // block 0: x [M][K] or null
+  float *hid_out2;      // block 0: second copy of x or null
 };
-
-// Arguments of the fused attention-block finalisation (see attention.hip).
-struct AttnArgs;
 
 struct GemvArgs {
   int epi;                        // GemvEpilogue
   int K, M;
-  const _Float16 *a_hi, *a_lo;  // activations [M][lda] (hi/lo fp16 split)
+  const _Float16 *a_hi, *a_lo;  // activations [M][lda] (hi/lo fp16 split), unless prep.on
   int lda;
   float out_mul;                 // undoes the activation pre-scale
   GemvSeg seg[3];
@@ -61,28 +56,35 @@ struct GemvArgs {
   _Float16 *sw_hi, *sw_lo;        // [M][ldo_sw]
   int ldo_sw;
   float sw_prescale;
-  // EPI_ARGMAX
+  // EPI_ARGMAX: per-block maximum and its first index, per row
   float *arg_val;                 // [blocks][M]
   int32_t *arg_idx;               // [blocks][M]
-  int32_t *ids_out;               // [M] final ids (last block)
-  int32_t *tok_state;             // optional: next-token state [M]
-  int32_t *pos_state;             // optional: positions [M], incremented
-  int32_t *ids_hist;              // optional: history [step][M]
-  const int32_t *step_ptr;        // optional: step counter for ids_hist
-  // last-block finalisation
-  unsigned *counter;              // null: none
-  int fin_kind;                   // 0 none, 1 rows (FinArgs)
-  FinArgs fin;
+  PrepArgs prep;
+};
+
+// Final argmax over the LM head's per-block maxima (greedy branch of
+// temperature_sampling, lm_head.mojo:224-230) and decode-state update.
+struct ArgmaxFin {
+  const float *arg_val;
+  const int32_t *arg_idx;
+  int n_blocks, M;
+  int32_t *ids_out;     // [M] or null
+  int32_t *tok_state;   // [M] or null: next input token
+  int32_t *pos_state;   // [M] or null: incremented
+  int32_t *ids_hist;    // [cap][M] or null
+  int32_t *step;        // step counter (with ids_hist)
 };
 
 int launch_gemv(const GemvArgs &a, hipStream_t st);
 // fp32 rows -> hi/lo fp16 (times prescale)
 int launch_split(const float *x, int M, int K, int ldx, float prescale,
                  _Float16 *hi, _Float16 *lo, int ldo, hipStream_t st);
-int launch_fin_rows(const FinArgs &f, hipStream_t st);
 int launch_sum_parts(float *out, const float *parts, int S, size_t n, hipStream_t st);
 int pack_device(uint8_t *dst, const uint8_t *src, int K, int N, hipStream_t st);
-
-__device__ void fin_rows_block(const FinArgs &f);
+int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st);
+// Standalone row preparation (same math as the GEMV prologue) writing the
+// fp16 hi/lo split to global memory: used where the consumer is not a GEMV.
+int launch_prep_rows(const PrepArgs &p, int M, int K, _Float16 *hi, _Float16 *lo,
+                     hipStream_t st);
 
 }  // namespace ms

@@ -108,7 +108,7 @@ int launch_split(const float *x, int M, int K, int ldx, float prescale,
 }
 
 // ------------------------------------------------------------------------------
-// row finalisation (residual sum + rmsnorm + hi/lo split) by one block
+// block reductions
 // ------------------------------------------------------------------------------
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -116,8 +116,9 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
+// Sum over the block; every thread returns the total.  sh: >= 16 floats.
 __device__ float block_sum(float v, float *sh) {
-  const int lane = threadIdx.x % 64, w = threadIdx.x / 64, nw = blockDim.x / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   v = wave_sum(v);
   __syncthreads();
   if (lane == 0) sh[w] = v;
@@ -127,56 +128,63 @@ __device__ float block_sum(float v, float *sh) {
   return t;
 }
 
-constexpr int kFinMaxPerThread = 40;  // D <= 40 * blockDim.x
+// ------------------------------------------------------------------------------
+// row preparation (residual sum + PLE + rmsnorm), shared by the GEMV prologue
+// and the standalone kernel.  Order of the fp32 operations follows the
+// reference: x = x + proj (gemma4_e4b.mojo:522,538), x *= ple (kernels.mojo:
+// 506-516), x *= 1/sqrt(mean(x^2)+1e-6) (:474-489), * gamma (:598-613).
+// ------------------------------------------------------------------------------
+__device__ inline float prep_x(const PrepArgs &p, int K, int m, int k) {
+  const size_t idx = (size_t)m * K + k;
+  float x = p.base ? p.base[idx] : 0.f;
+  for (int s = 0; s < p.n_parts; ++s) x = x + p.parts[s * p.part_stride + idx];
+  return x;
+}
 
-__device__ void fin_rows_block(const FinArgs &f) {
+__device__ float prep_inv_rms(const PrepArgs &p, int K, int m, float *sh) {
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    const float x = prep_x(p, K, m, k) * p.pre_scale;
+    ss += x * x;
+  }
+  ss = block_sum(ss, sh);
+  return 1.0f / sqrtf(ss / (float)K + 1e-6f);
+}
+
+// Normalised value of (m, k); block `writer` also stores the fp32 outputs.
+__device__ inline float prep_y(const PrepArgs &p, int K, int m, int k, float inv,
+                               bool writer) {
+  const float x = prep_x(p, K, m, k);
+  float y = (x * p.pre_scale) * inv;
+  if (p.gamma) y = y * p.gamma[k];
+  if (writer) {
+    const size_t idx = (size_t)m * K + k;
+    if (p.hid_out) p.hid_out[idx] = x;
+    if (p.hid_out2) p.hid_out2[idx] = x;
+    if (p.xn_out) p.xn_out[idx] = y;
+  }
+  return y;
+}
+
+__global__ __launch_bounds__(256) void k_prep_rows(PrepArgs p, int K, _Float16 *hi,
+                                                   _Float16 *lo) {
   __shared__ float sh[16];
-  const int tid = threadIdx.x, nt = blockDim.x;
-  for (int m = 0; m < f.M; ++m) {
-    float v[kFinMaxPerThread];
-    float ss = 0.f;
-#pragma unroll
-    for (int k = 0; k < kFinMaxPerThread; ++k) {
-      const int c = tid + k * nt;
-      if (c < f.D) {
-        const size_t idx = (size_t)m * f.D + c;
-        float x = f.base ? f.base[idx] : 0.f;
-        for (int s = 0; s < f.n_parts; ++s) x = x + f.parts[s * f.part_stride + idx];
-        if (f.hidden_out) f.hidden_out[idx] = x;
-        x = x * f.pre_scale;
-        v[k] = x;
-        ss += x * x;
-      }
-    }
-    float inv = 1.f;
-    if (f.normalize) {
-      ss = block_sum(ss, sh);
-      inv = 1.0f / sqrtf(ss / (float)f.D + 1e-6f);
-    }
-#pragma unroll
-    for (int k = 0; k < kFinMaxPerThread; ++k) {
-      const int c = tid + k * nt;
-      if (c < f.D) {
-        const size_t idx = (size_t)m * f.D + c;
-        float y = v[k] * inv;
-        if (f.gamma) y = y * f.gamma[c];
-        if (f.xn_out) f.xn_out[idx] = y;
-        if (f.a_hi) {
-          _Float16 h, l;
-          split_hi_lo(y * f.a_prescale, &h, &l);
-          f.a_hi[idx] = h;
-          f.a_lo[idx] = l;
-        }
-      }
+  const int m = blockIdx.x;
+  const float inv = prep_inv_rms(p, K, m, sh);
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    const float y = prep_y(p, K, m, k, inv, true);
+    if (hi) {
+      _Float16 h, l;
+      split_hi_lo(y, &h, &l);
+      hi[(size_t)m * K + k] = h;
+      lo[(size_t)m * K + k] = l;
     }
   }
 }
 
-__global__ void k_fin_rows(FinArgs f) { fin_rows_block(f); }
-
-int launch_fin_rows(const FinArgs &f, hipStream_t st) {
-  MS_CHECK_ARG(f.D <= kFinMaxPerThread * 256, "row finalisation: D too large");
-  hipLaunchKernelGGL(k_fin_rows, dim3(1), dim3(256), 0, st, f);
+int launch_prep_rows(const PrepArgs &p, int M, int K, _Float16 *hi, _Float16 *lo,
+                     hipStream_t st) {
+  hipLaunchKernelGGL(k_prep_rows, dim3(M), dim3(256), 0, st, p, K, hi, lo);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }
@@ -193,6 +201,9 @@ __device__ inline uint32_t and_or(uint32_t d, uint32_t m, uint32_t c) {
 __device__ inline half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 
 // 8 nibbles -> 8 exact fp16 values (nibble - 8) in MFMA element order.
+// fp16 1024 + n has n in the low mantissa bits, so the nibble is OR-ed into
+// 0x6400 (bits 0-3: n, bits 4-7: 16n) and an exact fp16 add/FMA removes the
+// offset.  fp16 has 10 mantissa bits, hence the >> 8 for the upper nibbles.
 __device__ inline half8_t q4_to_half8(uint32_t d, uint32_t magic) {
   const uint32_t d8 = d >> 8;
   half2_t v0 = as_h2(and_or(d, 0x000F000Fu, magic));   // 1024 + n
@@ -223,12 +234,12 @@ __device__ inline void gemv_slot(const GemvArgs &a, int pg, int p,
   }
   int panel = pg * a.P + p;
   for (int si = 0; si < a.nseg; ++si) {
-    const GemvSeg &s = a.seg[si];
-    const int np = s.n_cols / 16;
+    const GemvSeg &sg = a.seg[si];
+    const int np = sg.n_cols / 16;
     if (panel < np) {
-      *w = s.w + (size_t)panel * a.K * 8;
-      *scale = s.scale;
-      *col = s.out_col0 + panel * 16;
+      *w = sg.w + (size_t)panel * a.K * 8;
+      *scale = sg.scale;
+      *col = sg.out_col0 + panel * 16;
       return;
     }
     panel -= np;
@@ -242,15 +253,28 @@ __device__ inline void gemv_slot(const GemvArgs &a, int pg, int p,
 // lane j + 16*(i/4), element i%4).
 __device__ inline int dfrag(int i, int j) { return (j + 16 * (i >> 2)) * 4 + (i & 3); }
 
-template <int MODE, int P>
+// LDS bytes of the GEMV for a given configuration.
+__host__ __device__ inline size_t gemv_lds_bytes(int waves, int P, int M, int ks, bool prep) {
+  size_t b = ((size_t)waves * P * 256 + (size_t)P * M * 16) * 4;
+  if (prep) b += (size_t)2 * M * (ks + 8) * 2;
+  return b;
+}
+
+// MODE 0: M <= 8, hi rows 0..M-1 and lo rows M..2M-1 share one MFMA.
+// MODE 1: M <= 16, separate hi and lo MFMAs.
+// PREP: activations built by the block in LDS (PrepArgs).
+template <int MODE, int P, bool PREP>
 __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
-  extern __shared__ float red[];  // [waves][P][256]
+  extern __shared__ float red[];  // [waves][P][256], vals [P][M][16], A hi/lo
+  __shared__ float sh[16];
+  constexpr int U = (MODE == 0) ? 4 : 2;  // super-tiles in flight per wave
   const int W = a.waves;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int KG = a.K / kSuperK;
   const int s = blockIdx.x % a.S;
   const int pg = blockIdx.x / a.S;
   const int G0 = (int)((long)KG * s / a.S), G1 = (int)((long)KG * (s + 1) / a.S);
+  const int M = a.M;
 
   const uint8_t *wp[P];
   float wsc[P];
@@ -258,13 +282,48 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 #pragma unroll
   for (int p = 0; p < P; ++p) gemv_slot(a, pg, p, &wp[p], &wsc[p], &col[p]);
 
+  const int ks = (G1 - G0) * kSuperK;
+  const int ldl = ks + 8;
+  _Float16 *lds_hi = reinterpret_cast<_Float16 *>(red + (size_t)W * P * 256 + P * M * 16);
+  _Float16 *lds_lo = lds_hi + (size_t)M * ldl;
+
+  if (PREP) {
+    const int k0 = G0 * kSuperK;
+    const bool writer = blockIdx.x == 0;
+    for (int m = 0; m < M; ++m) {
+      const float inv = prep_inv_rms(a.prep, a.K, m, sh);
+      const int kb = writer ? 0 : k0, ke = writer ? a.K : k0 + ks;
+      for (int k = kb + (int)threadIdx.x; k < ke; k += blockDim.x) {
+        const float y = prep_y(a.prep, a.K, m, k, inv, writer);
+        if (k >= k0 && k < k0 + ks) {
+          _Float16 h, l;
+          split_hi_lo(y, &h, &l);
+          lds_hi[(size_t)m * ldl + (k - k0)] = h;
+          lds_lo[(size_t)m * ldl + (k - k0)] = l;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // A-fragment source rows for this lane (row i of the 16-row MFMA operand)
   const int i = lane & 15, g = lane >> 4;
   const _Float16 *arow = nullptr, *arow_lo = nullptr;
-  if (MODE == 0) {
-    if (i < a.M) arow = a.a_hi + (size_t)i * a.lda;
-    else if (i < 2 * a.M) arow = a.a_lo + (size_t)(i - a.M) * a.lda;
+  int astride = 0;  // offset of super-tile G relative to its base, in halves
+  if (PREP) {
+    if (MODE == 0) {
+      if (i < M) arow = lds_hi + (size_t)i * ldl;
+      else if (i < 2 * M) arow = lds_lo + (size_t)(i - M) * ldl;
+    } else if (i < M) {
+      arow = lds_hi + (size_t)i * ldl;
+      arow_lo = lds_lo + (size_t)i * ldl;
+    }
+    astride = -G0 * kSuperK;
   } else {
-    if (i < a.M) {
+    if (MODE == 0) {
+      if (i < M) arow = a.a_hi + (size_t)i * a.lda;
+      else if (i < 2 * M) arow = a.a_lo + (size_t)(i - M) * a.lda;
+    } else if (i < M) {
       arow = a.a_hi + (size_t)i * a.lda;
       arow_lo = a.a_lo + (size_t)i * a.lda;
     }
@@ -276,27 +335,40 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 #pragma unroll
   for (int p = 0; p < P; ++p) acc[p] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int G = G0 + wave; G < G1; G += W) {
-    half8_t af[4], afl[4];
-    const int kofs = G * kSuperK + 32 * g;
+  for (int G = G0 + wave; G < G1; G += U * W) {
+    uint4 q[U][P];
+    half8_t af[U][4];
+    half8_t afl[MODE == 1 ? U : 1][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      af[t] = arow ? load_h8(arow + kofs + 8 * t) : half8_t{};
-      if (MODE == 1) afl[t] = arow_lo ? load_h8(arow_lo + kofs + 8 * t) : half8_t{};
+    for (int u = 0; u < U; ++u) {
+      const int Gu = G + u * W;
+      if (Gu < G1) {
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          q[u][p] = *reinterpret_cast<const uint4 *>(wp[p] + (size_t)Gu * 1024 + lane * 16);
+        const int kofs = Gu * kSuperK + astride + 32 * g;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          af[u][t] = arow ? load_h8(arow + kofs + 8 * t) : half8_t{};
+          if (MODE == 1) afl[u][t] = arow_lo ? load_h8(arow_lo + kofs + 8 * t) : half8_t{};
+        }
+      }
     }
-    uint4 q[P];
 #pragma unroll
-    for (int p = 0; p < P; ++p)
-      q[p] = *reinterpret_cast<const uint4 *>(wp[p] + (size_t)G * 1024 + lane * 16);
+    for (int u = 0; u < U; ++u) {
+      const int Gu = G + u * W;
+      if (Gu < G1) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const uint32_t dw[4] = {q[p].x, q[p].y, q[p].z, q[p].w};
+        for (int p = 0; p < P; ++p) {
+          const uint32_t dw[4] = {q[u][p].x, q[u][p].y, q[u][p].z, q[u][p].w};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const half8_t b = q4_to_half8(dw[t], magic);
-        acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], b, acc[p], 0, 0, 0);
-        if (MODE == 1)
-          acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afl[t], b, acc[p], 0, 0, 0);
+          for (int t = 0; t < 4; ++t) {
+            const half8_t b = q4_to_half8(dw[t], magic);
+            acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u][t], b, acc[p], 0, 0, 0);
+            if (MODE == 1)
+              acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afl[u][t], b, acc[p], 0, 0, 0);
+          }
+        }
       }
     }
   }
@@ -312,15 +384,15 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   __syncthreads();
 
   // reduce over waves: value of (slot p, row m, column j) -> vals[p][m][j]
-  const int n_out = P * a.M * 16;
+  const int n_out = P * M * 16;
   float *vals = red + (size_t)W * P * 256;
   for (int o = threadIdx.x; o < n_out; o += blockDim.x) {
-    const int p = o / (a.M * 16), m = (o / 16) % a.M, j = o % 16;
+    const int p = o / (M * 16), m = (o / 16) % M, j = o % 16;
     float v = 0.f;
     for (int w = 0; w < W; ++w) {
       const float *r = red + ((size_t)w * P + p) * 256;
       v += r[dfrag(m, j)];
-      if (MODE == 0) v += r[dfrag(m + a.M, j)];
+      if (MODE == 0) v += r[dfrag(m + M, j)];
     }
     vals[o] = v * (wsc[p] * a.out_mul);
   }
@@ -328,7 +400,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 
   if (a.epi == EPI_STORE || a.epi == EPI_ACCUMULATE) {
     for (int o = threadIdx.x; o < n_out; o += blockDim.x) {
-      const int p = o / (a.M * 16), m = (o / 16) % a.M, j = o % 16;
+      const int p = o / (M * 16), m = (o / 16) % M, j = o % 16;
       if (!wp[p]) continue;
       if (a.epi == EPI_STORE)
         a.out[(size_t)s * a.split_stride + (size_t)m * a.ldo + col[p] + j] = vals[o];
@@ -338,9 +410,9 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   } else if (a.epi == EPI_SWIGLU) {
     // slot 0 = gate, slot 1 = up (same columns): swiglu_inplace
     // (kernels.mojo:519-532) fused into the producer.
-    for (int o = threadIdx.x; o < a.M * 16; o += blockDim.x) {
+    for (int o = threadIdx.x; o < M * 16; o += blockDim.x) {
       const int m = o / 16, j = o % 16;
-      const float gt = vals[o], up = vals[a.M * 16 + o];
+      const float gt = vals[o], up = vals[M * 16 + o];
       const float y = up * gt * (1.0f / (1.0f + expf(-gt)));
       const size_t idx = (size_t)m * a.ldo_sw + col[0] + j;
       if (a.out) a.out[(size_t)m * a.ldo + col[0] + j] = y;
@@ -352,58 +424,74 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   } else if (a.epi == EPI_ARGMAX) {
     // logits (optional) and the block's first index of the maximum per row
     for (int o = threadIdx.x; o < n_out; o += blockDim.x) {
-      const int p = o / (a.M * 16), m = (o / 16) % a.M, j = o % 16;
+      const int p = o / (M * 16), m = (o / 16) % M, j = o % 16;
       if (a.out) a.out[(size_t)m * a.ldo + col[p] + j] = vals[o];
     }
-    if (threadIdx.x < a.M) {
+    if ((int)threadIdx.x < M) {
       const int m = threadIdx.x;
       float bv = -INFINITY;
       int bi = 0x7fffffff;
       for (int p = 0; p < P; ++p)
         for (int j = 0; j < 16; ++j) {
-          const float v = vals[(p * a.M + m) * 16 + j];
+          const float v = vals[(p * M + m) * 16 + j];
           const int idx = col[p] + j;
-          if (v > bv || (v == bv && idx < bi)) { bv = v; bi = idx; }
+          if (v > bv || (v == bv && idx < bi)) {
+            bv = v;
+            bi = idx;
+          }
         }
-      a.arg_val[(size_t)blockIdx.x * a.M + m] = bv;
-      a.arg_idx[(size_t)blockIdx.x * a.M + m] = bi;
+      a.arg_val[(size_t)blockIdx.x * M + m] = bv;
+      a.arg_idx[(size_t)blockIdx.x * M + m] = bi;
     }
   }
+}
 
-  if (a.counter == nullptr) return;
-  // ---- last block of the grid runs the dependent finalisation ----
-  __shared__ int is_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0)
-    is_last = (atomicAdd(a.counter, 1u) == gridDim.x - 1) ? 1 : 0;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  if (a.epi == EPI_ARGMAX) {
-    if (threadIdx.x < a.M) {
-      const int m = threadIdx.x;
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      // blocks in increasing column order; strict '>' keeps the lowest index
-      // (temperature_sampling greedy branch, lm_head.mojo:224-230)
-      for (int b = 0; b < (int)gridDim.x; ++b) {
-        const float v = a.arg_val[(size_t)b * a.M + m];
-        const int idx = a.arg_idx[(size_t)b * a.M + m];
-        if (v > bv || (v == bv && idx < bi)) { bv = v; bi = idx; }
+// Greedy id per row from the per-block maxima; blocks are visited in increasing
+// column order and ties keep the lowest index (lm_head.mojo:224-230).
+__global__ __launch_bounds__(256) void k_argmax_fin(ArgmaxFin f) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  for (int m = 0; m < f.M; ++m) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int b = threadIdx.x; b < f.n_blocks; b += blockDim.x) {
+      const float v = f.arg_val[(size_t)b * f.M + m];
+      const int idx = f.arg_idx[(size_t)b * f.M + m];
+      if (v > bv || (v == bv && idx < bi)) {
+        bv = v;
+        bi = idx;
       }
-      if (a.ids_out) a.ids_out[m] = bi;
-      if (a.tok_state) a.tok_state[m] = bi;
-      if (a.pos_state) a.pos_state[m] += 1;
-      if (a.ids_hist) a.ids_hist[(size_t)(*a.step_ptr) * a.M + m] = bi;
     }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int o = blockDim.x / 2; o > 0; o >>= 1) {
+      if ((int)threadIdx.x < o) {
+        const float v = sv[threadIdx.x + o];
+        const int idx = si[threadIdx.x + o];
+        if (v > sv[threadIdx.x] || (v == sv[threadIdx.x] && idx < si[threadIdx.x])) {
+          sv[threadIdx.x] = v;
+          si[threadIdx.x] = idx;
+        }
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      const int id = si[0];
+      if (f.ids_out) f.ids_out[m] = id;
+      if (f.tok_state) f.tok_state[m] = id;
+      if (f.pos_state) f.pos_state[m] += 1;
+      if (f.ids_hist) f.ids_hist[(size_t)(*f.step) * f.M + m] = id;
+    }
+    __syncthreads();
   }
-  if (a.fin_kind == 1) fin_rows_block(a.fin);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    if (a.ids_hist && a.step_ptr) atomicAdd((int *)a.step_ptr, 1);
-    atomicExch(a.counter, 0u);
-  }
+  if (threadIdx.x == 0 && f.ids_hist) *f.step += 1;
+}
+
+int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st) {
+  hipLaunchKernelGGL(k_argmax_fin, dim3(1), dim3(256), 0, st, f);
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
 }
 
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
@@ -414,8 +502,8 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_CHECK_ARG(a.epi != EPI_ACCUMULATE || a.S == 1, "GEMV: accumulate needs S=1");
   MS_CHECK_ARG(a.epi != EPI_SWIGLU || (a.S == 1 && a.P == 2 && a.nseg == 2),
                "GEMV: SwiGLU epilogue needs S=1, P=2, two segments");
-  MS_CHECK_ARG(a.epi != EPI_ARGMAX || (a.S == 1 && a.counter),
-               "GEMV: argmax epilogue needs S=1 and a counter");
+  MS_CHECK_ARG(a.epi != EPI_ARGMAX || (a.S == 1 && a.arg_val && a.arg_idx),
+               "GEMV: argmax epilogue needs S=1 and block-max buffers");
   long n_panels = 0;
   for (int i = 0; i < a.nseg; ++i) {
     MS_CHECK_ARG(a.seg[i].n_cols % 16 == 0, "GEMV: segment width % 16 != 0");
@@ -426,26 +514,28 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   }
   const long groups = (a.epi == EPI_SWIGLU) ? a.seg[0].n_cols / 16 : n_panels / a.P;
   const long blocks = groups * a.S;
-  const size_t shmem = ((size_t)a.waves * a.P * 256 + (size_t)a.P * a.M * 16) * 4;
+  const int KG = a.K / kSuperK;
+  const int ks_max = ((KG + a.S - 1) / a.S) * kSuperK;
+  const bool prep = a.prep.on != 0;
+  const size_t shmem = gemv_lds_bytes(a.waves, a.P, a.M, ks_max, prep);
+  MS_CHECK_ARG(shmem <= 160 * 1024 - 256, "GEMV: LDS budget exceeded (use the prep kernel)");
   const bool packed = a.M <= 8;
-#define MS_GEMV_CASE(MODE, PP)                                                  \
-  hipLaunchKernelGGL((k_gemv<MODE, PP>), dim3(blocks), dim3(64 * a.waves), shmem, \
+#define MS_GEMV_CASE(MODE, PP, PR)                                                \
+  hipLaunchKernelGGL((k_gemv<MODE, PP, PR>), dim3(blocks), dim3(64 * a.waves), shmem, \
                      st, a)
-  if (packed) {
-    switch (a.P) {
-      case 1: MS_GEMV_CASE(0, 1); break;
-      case 2: MS_GEMV_CASE(0, 2); break;
-      case 4: MS_GEMV_CASE(0, 4); break;
-      default: return fail(MS_E_INVALID, "GEMV: P must be 1, 2 or 4");
-    }
-  } else {
-    switch (a.P) {
-      case 1: MS_GEMV_CASE(1, 1); break;
-      case 2: MS_GEMV_CASE(1, 2); break;
-      case 4: MS_GEMV_CASE(1, 4); break;
-      default: return fail(MS_E_INVALID, "GEMV: P must be 1, 2 or 4");
-    }
+#define MS_GEMV_P(MODE, PR)                                                       \
+  switch (a.P) {                                                                   \
+    case 1: MS_GEMV_CASE(MODE, 1, PR); break;                                      \
+    case 2: MS_GEMV_CASE(MODE, 2, PR); break;                                      \
+    case 4: MS_GEMV_CASE(MODE, 4, PR); break;                                      \
+    default: return fail(MS_E_INVALID, "GEMV: P must be 1, 2 or 4");               \
   }
+  if (packed) {
+    if (prep) { MS_GEMV_P(0, true) } else { MS_GEMV_P(0, false) }
+  } else {
+    if (prep) { MS_GEMV_P(1, true) } else { MS_GEMV_P(1, false) }
+  }
+#undef MS_GEMV_P
 #undef MS_GEMV_CASE
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
