@@ -9,9 +9,9 @@
 //
 // Two launches:
 //  k_attn_chunks   one block per (sequence, kv head, 16-key chunk, row group):
-//                  q (after RoPE) for the kv head's G query heads staged in LDS,
-//                  the chunk's V rows prefetched into registers while the
-//                  scores are computed, then (max, sum, o[hd]) per (row, head).
+//                  the chunk's K and V rows and q (after RoPE) for the kv
+//                  head's G query heads staged in LDS with every load issued
+//                  up front, then (max, sum, o[hd]) per (row, head).
 //  k_attn_combine  one block per (sequence, row, kv head): merges the chunks
 //                  (log-sum-exp rescaling), writes the O-projection input
 //                  (fp32 and fp16 hi/lo) and appends the row's K (after RoPE)
@@ -26,29 +26,37 @@
 
 namespace ms {
 
+// Sum of the split-K partials of q|k|v element (row, col).  All loads are
+// unconditional (absent splits alias split 0) so they are issued together.
 __device__ inline float qkv_val(const AttnArgs &a, int row, int col) {
   const size_t idx = (size_t)row * a.ld + col;
-  float x = a.qkv[idx];
-  for (int s = 1; s < a.S; ++s) x = x + a.qkv[(size_t)s * a.split_stride + idx];
+  float v[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) v[s] = a.qkv[(size_t)(s < a.S ? s : 0) * a.split_stride + idx];
+  float x = v[0];
+#pragma unroll
+  for (int s = 1; s < 4; ++s)
+    if (s < a.S) x = x + v[s];
   return x;
 }
 
 // Element d of a head starting at column c0 of row `row`, rotated by RoPE at
 // position pos (apply_rope_inplace, kernels.mojo:579-595; pairs (i, i+rot/2)
-// over the first rot dims).
+// over the first rot dims).  Branch-free: the pair element and the table
+// entries are loaded for every d (clamped into range) and selected afterwards.
 __device__ inline float rope_val(const AttnArgs &a, int row, int c0, int d, int pos) {
-  const float x = qkv_val(a, row, c0 + d);
-  if (!a.apply_rope || d >= a.rot) return x;
   const int half = a.rot >> 1;
-  const int i = d < half ? d : d - half;
-  const float cv = a.cos_t[(size_t)pos * half + i];
-  const float sv = a.sin_t[(size_t)pos * half + i];
-  if (d < half) {
-    const float y = qkv_val(a, row, c0 + d + half);
-    return x * cv - y * sv;
-  }
-  const float y = qkv_val(a, row, c0 + d - half);
-  return y * sv + x * cv;
+  const bool rot = a.apply_rope && d < a.rot;
+  const int dd = d < a.rot ? d : 0;
+  const int i = dd < half ? dd : dd - half;
+  const int pd = dd < half ? dd + half : dd - half;
+  const float x = qkv_val(a, row, c0 + d);
+  const float y = qkv_val(a, row, c0 + pd);
+  const size_t ti = a.apply_rope ? (size_t)pos * half + i : 0;
+  const float cv = a.apply_rope ? a.cos_t[ti] : 1.f;
+  const float sv = a.apply_rope ? a.sin_t[ti] : 0.f;
+  const float r = (dd < half) ? x * cv - y * sv : y * sv + x * cv;
+  return rot ? r : x;
 }
 
 __device__ inline void key_range(const AttnArgs &a, int p, int *lo, int *hi) {
@@ -75,12 +83,28 @@ __device__ inline int row_group(const AttnArgs &a, int *RG) {
   return TR;
 }
 
+__device__ inline float block_reduce(float v, float *sh, bool is_max) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float u = __shfl_xor(v, o, 64);
+    v = is_max ? fmaxf(v, u) : v + u;
+  }
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  float t = sh[0];
+  for (int i = 1; i < nw; ++i) t = is_max ? fmaxf(t, sh[i]) : t + sh[i];
+  return t;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
   extern __shared__ float lds[];
   constexpr int CH = kAttnChunk;
-  constexpr int DPT = (HD + 255) / 256;  // P.V dims per thread
+  constexpr int F4 = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
   constexpr int NV = HD / 64;            // float4 per thread per key (scores)
+  constexpr int DPT = (HD + 255) / 256;  // P.V dims per thread
   const int G = a.n_heads / a.n_kv;
   int RG;
   const int TR = row_group(a, &RG);
@@ -104,36 +128,56 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
   const int TG = nr * G;
   const int nk = min(CH, kmax - c0 + 1);
 
-  float *sq = lds;                     // [TG][HD] rotated queries
-  float *ss = lds + kAttnLds;          // [TG][CH] scores -> probabilities
+  float *sk = lds;                     // [CH][HD] keys of the chunk
+  float *sv = sk + CH * HD;            // [CH][HD] values
+  float *sq = sv + CH * HD;            // [TG][HD] rotated queries
+  float *ss = sq + kAttnLds;           // [TG][CH] scores -> probabilities
   float *sm = ss + kAttnMaxTG * CH;    // [TG]
   float *sl = sm + kAttnMaxTG;         // [TG]
   const float *kcache = a.kc + (size_t)b * a.cache_seq_stride;
   const float *vcache = a.vc + (size_t)b * a.cache_seq_stride;
 
-  // V rows of the chunk -> registers (independent of the scores)
-  float vreg[CH][DPT];
+  // cache rows of the chunk -> LDS, all loads in flight at once
+  float4 kr[F4], vr[F4];
 #pragma unroll
-  for (int k = 0; k < CH; ++k)
-#pragma unroll
-    for (int j = 0; j < DPT; ++j) {
-      const int d = tid + 256 * j;
-      const int kp = c0 + k;
-      float v = 0.f;
-      if (k < nk && d < HD) {
-        if (kp >= base)
-          v = qkv_val(a, b * a.T + (kp - base), a.q_dim + a.kv_dim + h * HD + d);
-        else
-          v = vcache[(size_t)cache_slot(a, kp) * a.kv_dim + h * HD + d];
-      }
-      vreg[k][j] = v;
+  for (int j = 0; j < F4; ++j) {
+    const int f = tid + 256 * j;            // float4 index in [CH][HD/4]
+    const int k = f / (HD / 4), d4 = f % (HD / 4);
+    const int kp = c0 + k;
+    if (k < nk && kp < base) {
+      const size_t off = (size_t)cache_slot(a, kp) * a.kv_dim + h * HD + 4 * d4;
+      kr[j] = *reinterpret_cast<const float4 *>(kcache + off);
+      vr[j] = *reinterpret_cast<const float4 *>(vcache + off);
+    } else {
+      kr[j] = float4{0.f, 0.f, 0.f, 0.f};
+      vr[j] = float4{0.f, 0.f, 0.f, 0.f};
     }
-
+  }
   // rotated q for rows r0..r0+nr-1, query heads h*G..h*G+G-1
+#pragma unroll 4
   for (int e = tid; e < TG * HD; e += 256) {
     const int tg = e / HD, d = e % HD;
     const int t = r0 + tg / G, g = tg % G;
     sq[e] = rope_val(a, b * a.T + t, (h * G + g) * HD, d, base + t);
+  }
+  // slots of this call's rows are filled below; every other slot (cache rows,
+  // and zeros past the chunk end so that 0 * v stays finite) is written here
+#pragma unroll
+  for (int j = 0; j < F4; ++j) {
+    const int f = tid + 256 * j;
+    const int k = f / (HD / 4);
+    if (!(k < nk && c0 + k >= base)) {
+      reinterpret_cast<float4 *>(sk)[f] = kr[j];
+      reinterpret_cast<float4 *>(sv)[f] = vr[j];
+    }
+  }
+  // rows of this call that fall in the chunk: fresh K (after RoPE) and V
+  const int kin0 = max(c0, base), kin1 = min(c0 + nk, base + a.T);
+  for (int e = tid; e < (kin1 - kin0) * HD; e += 256) {
+    const int kp = kin0 + e / HD, d = e % HD;
+    const int row = b * a.T + (kp - base);
+    sk[(kp - c0) * HD + d] = rope_val(a, row, a.q_dim + h * HD, d, kp);
+    sv[(kp - c0) * HD + d] = qkv_val(a, row, a.q_dim + a.kv_dim + h * HD + d);
   }
   __syncthreads();
 
@@ -144,31 +188,15 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < kAttnMaxTG; ++i) acc[i] = 0.f;
   if (kk < nk) {
-    float4 kv[NV];
-    if (kp >= base) {
-      const int row = b * a.T + (kp - base);
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int d = dg * 4 + 64 * i;
-        kv[i] = float4{rope_val(a, row, a.q_dim + h * HD, d, kp),
-                       rope_val(a, row, a.q_dim + h * HD, d + 1, kp),
-                       rope_val(a, row, a.q_dim + h * HD, d + 2, kp),
-                       rope_val(a, row, a.q_dim + h * HD, d + 3, kp)};
-      }
-    } else {
-      const float *krow = kcache + (size_t)cache_slot(a, kp) * a.kv_dim + h * HD;
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        kv[i] = *reinterpret_cast<const float4 *>(krow + dg * 4 + 64 * i);
-    }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int d = dg * 4 + 64 * i;
+      const float4 kv = *reinterpret_cast<const float4 *>(sk + kk * HD + d);
 #pragma unroll
       for (int t = 0; t < kAttnMaxTG; ++t)
         if (t < TG) {
           const float4 qq = *reinterpret_cast<const float4 *>(sq + t * HD + d);
-          acc[t] += qq.x * kv[i].x + qq.y * kv[i].y + qq.z * kv[i].z + qq.w * kv[i].w;
+          acc[t] += qq.x * kv.x + qq.y * kv.y + qq.z * kv.z + qq.w * kv.w;
         }
     }
   }
@@ -197,8 +225,8 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
     for (int k = 0; k < CH; ++k) m = fmaxf(m, ss[tid * CH + k]);
     float l = 0.f;
     for (int k = 0; k < CH; ++k) {
-      const float s = ss[tid * CH + k];
-      const float p = (s == -INFINITY) ? 0.f : expf(s - m);
+      const float sc = ss[tid * CH + k];
+      const float p = (sc == -INFINITY) ? 0.f : expf(sc - m);
       ss[tid * CH + k] = p;
       l += p;
     }
@@ -214,7 +242,7 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
     for (int t = 0; t < TG; ++t) {
       float o = 0.f;
 #pragma unroll
-      for (int k = 0; k < CH; ++k) o += ss[t * CH + k] * vreg[k][j];
+      for (int k = 0; k < CH; ++k) o += ss[t * CH + k] * sv[k * HD + d];
       const int row_t = r0 + t / G, g = t % G;
       float *pp = a.part + ((((size_t)b * a.n_kv + h) * a.n_chunks + c) * a.T * G +
                             (size_t)row_t * G + g) * (HD + 2);
@@ -230,6 +258,7 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
   extern __shared__ float wsh[];  // [G][n_active] chunk weights
+  __shared__ float sh[16];
   const int G = a.n_heads / a.n_kv;
   int bid = blockIdx.x;
   const int h = bid % a.n_kv;
@@ -245,19 +274,30 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
   const size_t cstride = (size_t)a.T * G * (HD + 2);
   const float *p0 = a.part + (((size_t)b * a.n_kv + h) * a.n_chunks * a.T * G +
                               (size_t)t * G) * (HD + 2);
-  if (tid < G) {
-    const float *pg = p0 + (size_t)tid * (HD + 2);
-    float M = -INFINITY;
-    for (int cc = 0; cc < n_active; ++cc) M = fmaxf(M, pg[cc * cstride + HD]);
-    float L = 0.f;
-    for (int cc = 0; cc < n_active; ++cc) {
-      const float m = pg[cc * cstride + HD];
-      const float w = (m == -INFINITY) ? 0.f : expf(m - M);
-      wsh[tid * n_active + cc] = w;
-      L += pg[cc * cstride + HD + 1] * w;
+  // chunk weights exp(m_c - M) / L per query head, chunks spread over threads
+  for (int g = 0; g < G; ++g) {
+    const float *pg = p0 + (size_t)g * (HD + 2);
+    float mloc[2], lloc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int cc = tid + 256 * j;
+      mloc[j] = cc < n_active ? pg[cc * cstride + HD] : -INFINITY;
+      lloc[j] = cc < n_active ? pg[cc * cstride + HD + 1] : 0.f;
     }
+    const float M = block_reduce(fmaxf(mloc[0], mloc[1]), sh, true);
+    float wl[2], part = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      wl[j] = (mloc[j] == -INFINITY) ? 0.f : expf(mloc[j] - M);
+      part += lloc[j] * wl[j];
+    }
+    const float L = block_reduce(part, sh, false);
     const float inv = 1.0f / L;
-    for (int cc = 0; cc < n_active; ++cc) wsh[tid * n_active + cc] *= inv;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int cc = tid + 256 * j;
+      if (cc < n_active) wsh[g * n_active + cc] = wl[j] * inv;
+    }
   }
   __syncthreads();
   const int row = b * a.T + t;
@@ -265,6 +305,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
     const int g = e / HD, d = e % HD;
     const float *pg = p0 + (size_t)g * (HD + 2) + d;
     float o = 0.f;
+#pragma unroll 8
     for (int cc = 0; cc < n_active; ++cc) o += pg[cc * cstride] * wsh[g * n_active + cc];
     const size_t oi = (size_t)row * a.q_dim + (h * G + g) * HD + d;
     if (a.out) a.out[oi] = o;
@@ -301,6 +342,8 @@ int attn_check(const AttnArgs &a) {
   MS_CHECK_ARG(a.rot % 2 == 0 && a.rot <= a.hd, "attention: bad rotary width");
   MS_CHECK_ARG(a.cache_len > 0, "attention: empty cache");
   MS_CHECK_ARG(a.n_chunks <= kAttnMaxChunks, "attention: too many key chunks");
+  MS_CHECK_ARG(a.S >= 1 && a.S <= 4, "attention: at most 4 split-K partials");
+  MS_CHECK_ARG((size_t)G * a.n_chunks * 4 <= 64 * 1024, "attention: combine LDS budget");
   return MS_OK;
 }
 
@@ -310,7 +353,8 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
   const int TR = std::max(1, std::min(a.T, kAttnMaxTG / G));
   const int RG = (a.T + TR - 1) / TR;
   const long blocks = (long)a.B * a.n_kv * a.n_chunks * RG;
-  const size_t shmem = (size_t)(kAttnLds + kAttnMaxTG * kAttnChunk + 2 * kAttnMaxTG) * 4;
+  const size_t shmem =
+      (size_t)(2 * kAttnChunk * a.hd + kAttnLds + kAttnMaxTG * kAttnChunk + 2 * kAttnMaxTG) * 4;
   const long cblocks = (long)a.B * a.T * a.n_kv;
   const size_t cshmem = (size_t)G * a.n_chunks * 4;
 #define MS_ATTN(HDV)                                                                      \

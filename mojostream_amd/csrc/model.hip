@@ -131,7 +131,7 @@ static float pow2_prescale(double bound) {
 
 static int pick_split(int panels, int KG, int target_blocks) {
   int S = 1;
-  while ((long)panels * S < target_blocks && S * 2 <= KG) S *= 2;
+  while ((long)panels * S < target_blocks && S * 2 <= KG && S < 4) S *= 2;
   return S;
 }
 

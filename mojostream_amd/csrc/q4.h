@@ -19,6 +19,8 @@ enum GemvEpilogue {
                        // up*gate*sigmoid(gate) -> f16 hi/lo (times act_scale)
                        // and optionally fp32 into out
   EPI_ARGMAX = 3,      // LM head: logits (optional) + per-block argmax
+  EPI_RESID = 4,       // S=1, P=1: x = resid + value -> out [M][ldo] and the
+                       // block's sum of squares per row -> ss_out[m][block]
 };
 
 // Optional GEMV prologue: every block rebuilds the activation rows it needs
@@ -27,6 +29,12 @@ enum GemvEpilogue {
 // stores x (the previous layer's output) and y (the residual base).
 struct PrepArgs {
   int on;
+  // Reduced-row mode (xsum set): x = xsum[m][k] was summed by a producer,
+  // which also left n_ss partial sums of (x*pre_scale)^2 per row in ss.
+  const float *xsum;    // [M][K] or null
+  const float *ss;      // [M][n_ss]
+  int n_ss;
+  // Direct mode: x = base + sum of split partials.
   const float *base;    // [M][K] or null
   const float *parts;   // [n_parts][M][K] or null
   int n_parts;
@@ -59,6 +67,9 @@ struct GemvArgs {
   // EPI_ARGMAX: per-block maximum and its first index, per row
   float *arg_val;                 // [blocks][M]
   int32_t *arg_idx;               // [blocks][M]
+  // EPI_RESID
+  const float *resid;             // [M][ldo]
+  float *ss_out;                  // [M][n_blocks]
   PrepArgs prep;
 };
 
@@ -86,5 +97,8 @@ int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st);
 // fp16 hi/lo split to global memory: used where the consumer is not a GEMV.
 int launch_prep_rows(const PrepArgs &p, int M, int K, _Float16 *hi, _Float16 *lo,
                      hipStream_t st);
+// Residual sum of a row: xsum = base + sum parts (also into hid_out/hid_out2)
+// and per-256-column partial sums of (xsum*pre_scale)^2 -> ss [M][ceil(K/256)].
+int launch_rowsum(const PrepArgs &p, int M, int K, float *xsum, float *ss, hipStream_t st);
 
 }  // namespace ms

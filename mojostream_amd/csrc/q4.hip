@@ -134,56 +134,100 @@ __device__ float block_sum(float v, float *sh) {
 // reference: x = x + proj (gemma4_e4b.mojo:522,538), x *= ple (kernels.mojo:
 // 506-516), x *= 1/sqrt(mean(x^2)+1e-6) (:474-489), * gamma (:598-613).
 // ------------------------------------------------------------------------------
-__device__ inline float prep_x(const PrepArgs &p, int K, int m, int k) {
-  const size_t idx = (size_t)m * K + k;
-  float x = p.base ? p.base[idx] : 0.f;
-  for (int s = 0; s < p.n_parts; ++s) x = x + p.parts[s * p.part_stride + idx];
-  return x;
-}
+constexpr int kPrepMaxPer = 20;  // K <= kPrepMaxPer * blockDim.x
 
-__device__ float prep_inv_rms(const PrepArgs &p, int K, int m, float *sh) {
+// Builds activation row m: every thread loads all of its elements (base and
+// every split partial) before any use, so the row costs one memory round trip.
+// Outputs: the normalised values stay in registers (y[]); block `writer`
+// stores x and y; elements with k in [k0, k0+ks) go to LDS as fp16 hi/lo
+// (or to global hi/lo when gl_hi is set).
+__device__ void prep_row(const PrepArgs &p, int K, int m, bool writer, int k0, int ks,
+                         _Float16 *lds_hi, _Float16 *lds_lo, int ldl, _Float16 *gl_hi,
+                         _Float16 *gl_lo, float *sh) {
+  const int nt = blockDim.x, tid = threadIdx.x;
+  // Branch-free loads: indices are clamped into the row and absent split
+  // slices alias slice 0, so every load is unconditional and in bounds and the
+  // compiler keeps a whole half-row of them in flight; values are masked after.
+  constexpr int HP = kPrepMaxPer / 2;
+  float v[kPrepMaxPer], gm[kPrepMaxPer];
   float ss = 0.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) {
-    const float x = prep_x(p, K, m, k) * p.pre_scale;
-    ss += x * x;
+  const float *bp = p.base ? p.base : p.parts;
+  const float *gp = p.gamma ? p.gamma : bp;
+  const float *ps[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    ps[s] = p.parts ? p.parts + (s < p.n_parts ? s : 0) * p.part_stride : bp;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    float xb[HP], xp[4][HP], xg[HP];
+#pragma unroll
+    for (int i = 0; i < HP; ++i) {
+      const int k = min(tid + (hh * HP + i) * nt, K - 1);
+      const size_t idx = (size_t)m * K + k;
+      xb[i] = bp[idx];
+      xg[i] = gp[p.gamma ? k : idx];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xp[s][i] = ps[s][idx];
+    }
+#pragma unroll
+    for (int i = 0; i < HP; ++i) {
+      const int k = tid + (hh * HP + i) * nt;
+      float x = p.base ? xb[i] : 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (s < p.n_parts) x = x + xp[s][i];
+      if (p.n_parts > 4) {
+        const size_t idx = (size_t)m * K + min(k, K - 1);
+        for (int s = 4; s < p.n_parts; ++s) x = x + p.parts[s * p.part_stride + idx];
+      }
+      v[hh * HP + i] = (k < K) ? x : 0.f;
+      gm[hh * HP + i] = p.gamma ? xg[i] : 1.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPrepMaxPer; ++i) {
+    const float xs = v[i] * p.pre_scale;
+    ss += xs * xs;  // zero for k >= K
   }
   ss = block_sum(ss, sh);
-  return 1.0f / sqrtf(ss / (float)K + 1e-6f);
-}
-
-// Normalised value of (m, k); block `writer` also stores the fp32 outputs.
-__device__ inline float prep_y(const PrepArgs &p, int K, int m, int k, float inv,
-                               bool writer) {
-  const float x = prep_x(p, K, m, k);
-  float y = (x * p.pre_scale) * inv;
-  if (p.gamma) y = y * p.gamma[k];
-  if (writer) {
-    const size_t idx = (size_t)m * K + k;
-    if (p.hid_out) p.hid_out[idx] = x;
-    if (p.hid_out2) p.hid_out2[idx] = x;
-    if (p.xn_out) p.xn_out[idx] = y;
+  const float inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+#pragma unroll
+  for (int i = 0; i < kPrepMaxPer; ++i) {
+    const int k = tid + i * nt;
+    if (k < K) {
+      const float x = v[i];
+      float y = (x * p.pre_scale) * inv;
+      if (p.gamma) y = y * gm[i];
+      const size_t idx = (size_t)m * K + k;
+      if (writer) {
+        if (p.hid_out) p.hid_out[idx] = x;
+        if (p.hid_out2) p.hid_out2[idx] = x;
+        if (p.xn_out) p.xn_out[idx] = y;
+      }
+      if (k >= k0 && k < k0 + ks) {
+        _Float16 h, l;
+        split_hi_lo(y, &h, &l);
+        if (gl_hi) {
+          gl_hi[idx] = h;
+          gl_lo[idx] = l;
+        } else {
+          lds_hi[(size_t)m * ldl + (k - k0)] = h;
+          lds_lo[(size_t)m * ldl + (k - k0)] = l;
+        }
+      }
+    }
   }
-  return y;
 }
 
 __global__ __launch_bounds__(256) void k_prep_rows(PrepArgs p, int K, _Float16 *hi,
                                                    _Float16 *lo) {
   __shared__ float sh[16];
-  const int m = blockIdx.x;
-  const float inv = prep_inv_rms(p, K, m, sh);
-  for (int k = threadIdx.x; k < K; k += blockDim.x) {
-    const float y = prep_y(p, K, m, k, inv, true);
-    if (hi) {
-      _Float16 h, l;
-      split_hi_lo(y, &h, &l);
-      hi[(size_t)m * K + k] = h;
-      lo[(size_t)m * K + k] = l;
-    }
-  }
+  prep_row(p, K, blockIdx.x, true, 0, hi ? K : 0, nullptr, nullptr, 0, hi, lo, sh);
 }
 
 int launch_prep_rows(const PrepArgs &p, int M, int K, _Float16 *hi, _Float16 *lo,
                      hipStream_t st) {
+  MS_CHECK_ARG(K <= kPrepMaxPer * 256, "prep: row too long");
   hipLaunchKernelGGL(k_prep_rows, dim3(M), dim3(256), 0, st, p, K, hi, lo);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -264,7 +308,7 @@ __host__ __device__ inline size_t gemv_lds_bytes(int waves, int P, int M, int ks
 // MODE 1: M <= 16, separate hi and lo MFMAs.
 // PREP: activations built by the block in LDS (PrepArgs).
 template <int MODE, int P, bool PREP>
-__global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   extern __shared__ float red[];  // [waves][P][256], vals [P][M][16], A hi/lo
   __shared__ float sh[16];
   constexpr int U = (MODE == 0) ? 4 : 2;  // super-tiles in flight per wave
@@ -289,20 +333,9 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 
   if (PREP) {
     const int k0 = G0 * kSuperK;
-    const bool writer = blockIdx.x == 0;
-    for (int m = 0; m < M; ++m) {
-      const float inv = prep_inv_rms(a.prep, a.K, m, sh);
-      const int kb = writer ? 0 : k0, ke = writer ? a.K : k0 + ks;
-      for (int k = kb + (int)threadIdx.x; k < ke; k += blockDim.x) {
-        const float y = prep_y(a.prep, a.K, m, k, inv, writer);
-        if (k >= k0 && k < k0 + ks) {
-          _Float16 h, l;
-          split_hi_lo(y, &h, &l);
-          lds_hi[(size_t)m * ldl + (k - k0)] = h;
-          lds_lo[(size_t)m * ldl + (k - k0)] = l;
-        }
-      }
-    }
+    for (int m = 0; m < M; ++m)
+      prep_row(a.prep, a.K, m, blockIdx.x == 0, k0, ks, lds_hi, lds_lo, ldl, nullptr, nullptr,
+               sh);
     __syncthreads();
   }
 
@@ -448,9 +481,9 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 
 // Greedy id per row from the per-block maxima; blocks are visited in increasing
 // column order and ties keep the lowest index (lm_head.mojo:224-230).
-__global__ __launch_bounds__(256) void k_argmax_fin(ArgmaxFin f) {
-  __shared__ float sv[256];
-  __shared__ int si[256];
+__global__ __launch_bounds__(1024) void k_argmax_fin(ArgmaxFin f) {
+  __shared__ float sv[1024];
+  __shared__ int si[1024];
   for (int m = 0; m < f.M; ++m) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
@@ -489,7 +522,7 @@ __global__ __launch_bounds__(256) void k_argmax_fin(ArgmaxFin f) {
 }
 
 int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st) {
-  hipLaunchKernelGGL(k_argmax_fin, dim3(1), dim3(256), 0, st, f);
+  hipLaunchKernelGGL(k_argmax_fin, dim3(1), dim3(1024), 0, st, f);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }
@@ -497,7 +530,7 @@ int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st) {
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_CHECK_ARG(a.M >= 1 && a.M <= 16, "GEMV: 1 <= M <= 16");
   MS_CHECK_ARG(a.K % kSuperK == 0, "GEMV: K % 128 != 0");
-  MS_CHECK_ARG(a.waves == 4 || a.waves == 8, "GEMV: waves must be 4 or 8");
+  MS_CHECK_ARG(a.waves == 4, "GEMV: 4 waves per block");
   MS_CHECK_ARG(a.S >= 1 && a.S <= a.K / kSuperK, "GEMV: bad K split");
   MS_CHECK_ARG(a.epi != EPI_ACCUMULATE || a.S == 1, "GEMV: accumulate needs S=1");
   MS_CHECK_ARG(a.epi != EPI_SWIGLU || (a.S == 1 && a.P == 2 && a.nseg == 2),
@@ -519,6 +552,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   const bool prep = a.prep.on != 0;
   const size_t shmem = gemv_lds_bytes(a.waves, a.P, a.M, ks_max, prep);
   MS_CHECK_ARG(shmem <= 160 * 1024 - 256, "GEMV: LDS budget exceeded (use the prep kernel)");
+  MS_CHECK_ARG(!prep || a.K <= kPrepMaxPer * 64 * a.waves, "GEMV: prologue row too long");
   const bool packed = a.M <= 8;
 #define MS_GEMV_CASE(MODE, PP, PR)                                                \
   hipLaunchKernelGGL((k_gemv<MODE, PP, PR>), dim3(blocks), dim3(64 * a.waves), shmem, \
