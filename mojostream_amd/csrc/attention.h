@@ -9,11 +9,8 @@ struct AttnArgs {
   int q_dim, kv_dim, hd, n_heads, n_kv, rot;
   int cache_kind, cache_len, clamp;
   float scale;              // 1/sqrt(head_dim)
-  // q|k|v source: split-K partial sums [S][B*T][ld]; q at column 0,
-  // k at q_dim, v at q_dim + kv_dim
+  // q|k|v rows [B*T][ld]: q at column 0, k at q_dim, v at q_dim + kv_dim
   const float *qkv;
-  int S;
-  size_t split_stride;
   int ld;
   int apply_rope;
   const float *cos_t, *sin_t;  // [positions][rot/2]
@@ -23,9 +20,7 @@ struct AttnArgs {
   int n_chunks;                // chunks of kAttnChunk keys per (sequence, kv head)
   float *part;                 // [B][n_kv][n_chunks][T*G][hd+2]
   // combine
-  float *out;                  // [B*T][q_dim] or null
-  _Float16 *out_hi, *out_lo;   // [B*T][q_dim] or null
-  float out_prescale;
+  float *out;                  // [B*T][q_dim]
   int write_cache;
 };
 

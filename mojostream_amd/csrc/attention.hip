@@ -12,9 +12,9 @@
 //                  the chunk's K and V rows and q (after RoPE) for the kv
 //                  head's G query heads staged in LDS with every load issued
 //                  up front, then (max, sum, o[hd]) per (row, head).
-//  k_attn_combine  one block per (sequence, row, kv head): merges the chunks
+//  k_attn_combine  one block per (sequence, row, query head): merges the chunks
 //                  (log-sum-exp rescaling), writes the O-projection input
-//                  (fp32 and fp16 hi/lo) and appends the row's K (after RoPE)
+//                  rows (fp32) and appends the row's K (after RoPE)
 //                  and V to the cache.  It runs after every chunk block has
 //                  read the cache, so rows that wrap the circular window never
 //                  overwrite a key another row still needs.
@@ -26,18 +26,9 @@
 
 namespace ms {
 
-// Sum of the split-K partials of q|k|v element (row, col).  All loads are
-// unconditional (absent splits alias split 0) so they are issued together.
+// q|k|v element (row, col) of the fused projection output.
 __device__ inline float qkv_val(const AttnArgs &a, int row, int col) {
-  const size_t idx = (size_t)row * a.ld + col;
-  float v[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) v[s] = a.qkv[(size_t)(s < a.S ? s : 0) * a.split_stride + idx];
-  float x = v[0];
-#pragma unroll
-  for (int s = 1; s < 4; ++s)
-    if (s < a.S) x = x + v[s];
-  return x;
+  return a.qkv[(size_t)row * a.ld + col];
 }
 
 // Element d of a head starting at column c0 of row `row`, rotated by RoPE at
@@ -84,7 +75,9 @@ __device__ inline int row_group(const AttnArgs &a, int *RG) {
 }
 
 __device__ inline float block_reduce(float v, float *sh, bool is_max) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // 256-thread blocks (a blockDim read would load the dispatch packet)
+  constexpr int nw = 4;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float u = __shfl_xor(v, o, 64);
@@ -255,16 +248,22 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
   }
 }
 
+// One block per (sequence, row, query head): chunk weights exp(m_c - M) / L,
+// then o[d] = sum_c w_c * o_c[d] with every chunk's load of a 16-chunk group
+// in flight together.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
-  extern __shared__ float wsh[];  // [G][n_active] chunk weights
+  extern __shared__ float wsh[];  // [n_active] chunk weights
   __shared__ float sh[16];
+  constexpr int DPT = (HD + 255) / 256;
+  constexpr int CG = 16;  // chunk loads in flight per dim
   const int G = a.n_heads / a.n_kv;
   int bid = blockIdx.x;
-  const int h = bid % a.n_kv;
-  bid /= a.n_kv;
+  const int hq = bid % a.n_heads;
+  bid /= a.n_heads;
   const int t = bid % a.T;
   const int b = bid / a.T;
+  const int h = hq / G, g = hq % G;
   const int tid = threadIdx.x;
   const int base = a.pos[b];
   int kmin, kmax, dummy;
@@ -272,51 +271,52 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
   key_range(a, base + a.T - 1, &dummy, &kmax);
   const int n_active = (kmax - kmin) / kAttnChunk + 1;
   const size_t cstride = (size_t)a.T * G * (HD + 2);
-  const float *p0 = a.part + (((size_t)b * a.n_kv + h) * a.n_chunks * a.T * G +
-                              (size_t)t * G) * (HD + 2);
-  // chunk weights exp(m_c - M) / L per query head, chunks spread over threads
-  for (int g = 0; g < G; ++g) {
-    const float *pg = p0 + (size_t)g * (HD + 2);
-    float mloc[2], lloc[2];
+  const float *pg = a.part + (((size_t)b * a.n_kv + h) * a.n_chunks * a.T * G +
+                              (size_t)t * G + g) * (HD + 2);
+  float mloc[2], lloc[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int cc = tid + 256 * j;
-      mloc[j] = cc < n_active ? pg[cc * cstride + HD] : -INFINITY;
-      lloc[j] = cc < n_active ? pg[cc * cstride + HD + 1] : 0.f;
+  for (int j = 0; j < 2; ++j) {
+    const int cc = min(tid + 256 * j, n_active - 1);
+    mloc[j] = pg[cc * cstride + HD];
+    lloc[j] = pg[cc * cstride + HD + 1];
+    if (tid + 256 * j >= n_active) {
+      mloc[j] = -INFINITY;
+      lloc[j] = 0.f;
     }
-    const float M = block_reduce(fmaxf(mloc[0], mloc[1]), sh, true);
-    float wl[2], part = 0.f;
+  }
+  const float M = block_reduce(fmaxf(mloc[0], mloc[1]), sh, true);
+  float wl[2], part = 0.f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      wl[j] = (mloc[j] == -INFINITY) ? 0.f : expf(mloc[j] - M);
-      part += lloc[j] * wl[j];
-    }
-    const float L = block_reduce(part, sh, false);
-    const float inv = 1.0f / L;
+  for (int j = 0; j < 2; ++j) {
+    wl[j] = (mloc[j] == -INFINITY) ? 0.f : expf(mloc[j] - M);
+    part += lloc[j] * wl[j];
+  }
+  const float L = block_reduce(part, sh, false);
+  const float inv = 1.0f / L;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int cc = tid + 256 * j;
-      if (cc < n_active) wsh[g * n_active + cc] = wl[j] * inv;
-    }
+  for (int j = 0; j < 2; ++j) {
+    const int cc = tid + 256 * j;
+    if (cc < n_active) wsh[cc] = wl[j] * inv;
   }
   __syncthreads();
   const int row = b * a.T + t;
-  for (int e = tid; e < G * HD; e += 256) {
-    const int g = e / HD, d = e % HD;
-    const float *pg = p0 + (size_t)g * (HD + 2) + d;
-    float o = 0.f;
-#pragma unroll 8
-    for (int cc = 0; cc < n_active; ++cc) o += pg[cc * cstride] * wsh[g * n_active + cc];
-    const size_t oi = (size_t)row * a.q_dim + (h * G + g) * HD + d;
-    if (a.out) a.out[oi] = o;
-    if (a.out_hi) {
-      _Float16 hh, ll;
-      split_hi_lo(o * a.out_prescale, &hh, &ll);
-      a.out_hi[oi] = hh;
-      a.out_lo[oi] = ll;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = tid + 256 * j;
+    if (d < HD) {
+      float o = 0.f;
+      for (int c0 = 0; c0 < n_active; c0 += CG) {
+        float v[CG];
+#pragma unroll
+        for (int u = 0; u < CG; ++u) v[u] = pg[(size_t)min(c0 + u, n_active - 1) * cstride + d];
+#pragma unroll
+        for (int u = 0; u < CG; ++u)
+          if (c0 + u < n_active) o += v[u] * wsh[c0 + u];
+      }
+      a.out[(size_t)row * a.q_dim + hq * HD + d] = o;
     }
   }
-  if (a.write_cache) {
+  if (a.write_cache && g == 0) {
     // write_kv_sliding / write_kv_full (gemma4_e4b.mojo:211-249)
     const int p = base + t;
     if (!(a.cache_kind == MS_CACHE_LINEAR && p >= a.cache_len)) {
@@ -342,21 +342,21 @@ int attn_check(const AttnArgs &a) {
   MS_CHECK_ARG(a.rot % 2 == 0 && a.rot <= a.hd, "attention: bad rotary width");
   MS_CHECK_ARG(a.cache_len > 0, "attention: empty cache");
   MS_CHECK_ARG(a.n_chunks <= kAttnMaxChunks, "attention: too many key chunks");
-  MS_CHECK_ARG(a.S >= 1 && a.S <= 4, "attention: at most 4 split-K partials");
-  MS_CHECK_ARG((size_t)G * a.n_chunks * 4 <= 64 * 1024, "attention: combine LDS budget");
+  MS_CHECK_ARG(a.ld >= a.q_dim + 2 * a.kv_dim, "attention: q|k|v row stride too small");
   return MS_OK;
 }
 
 int launch_attention(const AttnArgs &a, hipStream_t st) {
   if (int rc = attn_check(a)) return rc;
+  MS_CHECK_ARG(a.qkv && a.part && a.pos && a.out, "attention: missing buffers");
   const int G = a.n_heads / a.n_kv;
   const int TR = std::max(1, std::min(a.T, kAttnMaxTG / G));
   const int RG = (a.T + TR - 1) / TR;
   const long blocks = (long)a.B * a.n_kv * a.n_chunks * RG;
   const size_t shmem =
       (size_t)(2 * kAttnChunk * a.hd + kAttnLds + kAttnMaxTG * kAttnChunk + 2 * kAttnMaxTG) * 4;
-  const long cblocks = (long)a.B * a.T * a.n_kv;
-  const size_t cshmem = (size_t)G * a.n_chunks * 4;
+  const long cblocks = (long)a.B * a.T * a.n_heads;
+  const size_t cshmem = (size_t)a.n_chunks * 4;
 #define MS_ATTN(HDV)                                                                      \
   hipLaunchKernelGGL(k_attn_chunks<HDV>, dim3(blocks), dim3(256), shmem, st, a);       \
   hipLaunchKernelGGL(k_attn_combine<HDV>, dim3(cblocks), dim3(256), cshmem, st, a)

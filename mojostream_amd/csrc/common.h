@@ -68,6 +68,10 @@ __host__ __device__ inline uint64_t rand_word(uint64_t seed, uint64_t stream,
 // v_mfma_f32_16x16x32_f16 (B[k][j]: lane j + 16*(k/8), element k%8) with MFMA
 // k-block t of super-tile G mapped to rows 128G + 32*(l/16) + 8t + e.
 constexpr int kPanelCols = 16;
+// Threads per block of the simple 1-D kernels.  Device code uses this
+// constant rather than blockDim, whose value is loaded from the dispatch packet.
+constexpr int kBlock = 256;
+
 constexpr int kSuperK = 128;
 __host__ __device__ inline size_t panel_offset(int K, int nb, int G, int lane) {
   return (size_t)nb * (size_t)K * 8 + (size_t)G * 1024 + (size_t)lane * 16;

@@ -15,26 +15,26 @@ __global__ void k_rmsnorm(float *x, const float *gamma, int cols) {
   __shared__ float sh[16];
   float *rp = x + (size_t)blockIdx.x * cols;
   float ss = 0.f;
-  for (int i = threadIdx.x; i < cols; i += blockDim.x) ss += rp[i] * rp[i];
+  for (int i = threadIdx.x; i < cols; i += kBlock) ss += rp[i] * rp[i];
   // block reduction
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = ss;
   __syncthreads();
   float t = 0.f;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += sh[w];
+  for (int w = 0; w < (kBlock >> 6); ++w) t += sh[w];
   const float inv = 1.0f / sqrtf(t / (float)cols + 1e-6f);
-  for (int i = threadIdx.x; i < cols; i += blockDim.x)
+  for (int i = threadIdx.x; i < cols; i += kBlock)
     rp[i] = gamma ? rp[i] * inv * gamma[i] : rp[i] * inv;
 }
 
 __global__ void k_scale(float *x, size_t n, float s) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
   if (i < n) x[i] = x[i] * s;
 }
 
 // swiglu_inplace (kernels.mojo:519-532): up = up * gate * sigmoid(gate)
 __global__ void k_swiglu(const float *gate, float *up, size_t n) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= n) return;
   const float g = gate[i];
   up[i] = up[i] * g * (1.0f / (1.0f + expf(-g)));
@@ -46,7 +46,7 @@ __global__ void k_rope(float *x, int rows, int row_stride, int n_heads, int head
                        int rot, const float *cs, const float *sn) {
   const int half = rot / 2;
   const long total = (long)rows * n_heads * half;
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long i = (long)blockIdx.x * kBlock + threadIdx.x;
   if (i >= total) return;
   const int r = (int)(i / ((long)n_heads * half));
   const int hh = (int)((i / half) % n_heads);
@@ -61,7 +61,7 @@ __global__ void k_rope(float *x, int rows, int row_stride, int n_heads, int head
 // get_token_embedding Q4 branch (lm_head.mojo:186-195) from the panel layout.
 __global__ void k_embed(const uint8_t *w, int D, int vocab, float scale,
                         const int32_t *tokens, int n, float *out) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int i = blockIdx.x * kBlock + threadIdx.x;
   if (i >= n * D) return;
   const int r = i / D, k = i % D;
   const int tok = tokens[r];
@@ -75,7 +75,7 @@ __global__ void k_embed(const uint8_t *w, int D, int vocab, float scale,
 
 int launch_embed(const uint8_t *w, int D, int vocab, float scale, const int32_t *tokens,
                  int n, float *out, hipStream_t st) {
-  hipLaunchKernelGGL(k_embed, dim3(cdiv((long)n * D, 256)), dim3(256), 0, st, w, D,
+  hipLaunchKernelGGL(k_embed, dim3(cdiv((long)n * D, kBlock)), dim3(kBlock), 0, st, w, D,
                      vocab, scale, tokens, n, out);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -107,7 +107,7 @@ using namespace ms;
 extern "C" int ms_rmsnorm(float *d_x, int rows, int cols) {
   if (int rc = require_init()) return rc;
   MS_CHECK_ARG(rows > 0 && cols > 0, "rmsnorm: bad shape");
-  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, ctx().stream, d_x,
+  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kBlock), 0, ctx().stream, d_x,
                      (const float *)nullptr, cols);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -116,7 +116,7 @@ extern "C" int ms_rmsnorm(float *d_x, int rows, int cols) {
 extern "C" int ms_rmsnorm_weighted(float *d_x, const float *d_gamma, int rows, int cols) {
   if (int rc = require_init()) return rc;
   MS_CHECK_ARG(rows > 0 && cols > 0, "rmsnorm_weighted: bad shape");
-  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, ctx().stream, d_x, d_gamma,
+  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kBlock), 0, ctx().stream, d_x, d_gamma,
                      cols);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -125,7 +125,7 @@ extern "C" int ms_rmsnorm_weighted(float *d_x, const float *d_gamma, int rows, i
 extern "C" int ms_ple_scale(float *d_x, size_t n, float s) {
   if (int rc = require_init()) return rc;
   if (!n) return MS_OK;
-  hipLaunchKernelGGL(k_scale, dim3(cdiv((long)n, 256)), dim3(256), 0, ctx().stream, d_x,
+  hipLaunchKernelGGL(k_scale, dim3(cdiv((long)n, kBlock)), dim3(kBlock), 0, ctx().stream, d_x,
                      n, s);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -134,7 +134,7 @@ extern "C" int ms_ple_scale(float *d_x, size_t n, float s) {
 extern "C" int ms_swiglu(const float *d_gate, float *d_up, size_t n) {
   if (int rc = require_init()) return rc;
   if (!n) return MS_OK;
-  hipLaunchKernelGGL(k_swiglu, dim3(cdiv((long)n, 256)), dim3(256), 0, ctx().stream,
+  hipLaunchKernelGGL(k_swiglu, dim3(cdiv((long)n, kBlock)), dim3(kBlock), 0, ctx().stream,
                      d_gate, d_up, n);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -155,7 +155,7 @@ extern "C" int ms_rope(float *d_x, int rows, int row_stride, int n_heads, int he
   MS_HIP_TRY(hipMemcpyAsync(dcs, cs.data(), nb, hipMemcpyHostToDevice, ctx().stream));
   MS_HIP_TRY(hipMemcpyAsync(dsn, sn.data(), nb, hipMemcpyHostToDevice, ctx().stream));
   const long total = (long)rows * n_heads * (rot_dim / 2);
-  hipLaunchKernelGGL(k_rope, dim3(cdiv(total, 256)), dim3(256), 0, ctx().stream, d_x, rows,
+  hipLaunchKernelGGL(k_rope, dim3(cdiv(total, kBlock)), dim3(kBlock), 0, ctx().stream, d_x, rows,
                      row_stride, n_heads, head_stride, rot_dim, dcs, dsn);
   MS_HIP_TRY(hipGetLastError());
   MS_HIP_TRY(hipStreamSynchronize(ctx().stream));  // scratch may be reused
@@ -186,7 +186,6 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.cache_len = L->cache_len;
   a.clamp = L->clamp_reads;
   a.scale = 1.0f / sqrtf((float)L->head_dim);
-  a.S = 1;
   a.ld = ld;
   a.apply_rope = 0;
   const int span = (L->cache_kind == MS_CACHE_CIRCULAR) ? L->cache_len + T - 1
@@ -215,7 +214,6 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
                               L->kv_dim * 4, T, hipMemcpyDeviceToDevice, st));
   MS_HIP_TRY(hipMemcpyAsync(dpos, &base, sizeof(int32_t), hipMemcpyHostToDevice, st));
   a.qkv = qkv;
-  a.split_stride = qkv_f;
   a.part = part;
   a.pos = dpos;
   if (int rc = launch_attention(a, st)) return rc;
@@ -234,32 +232,33 @@ extern "C" int ms_embed_q4(const uint8_t *d_packed, int D, int vocab, float scal
 extern "C" int ms_lm_head_argmax(const float *d_x, int M, int D, const uint8_t *d_packed,
                                  int vocab, float scale, float *d_logits, int32_t *d_ids) {
   if (int rc = require_init()) return rc;
-  MS_CHECK_ARG(M >= 1 && M <= 16, "lm_head: 1 <= M <= 16");
-  MS_CHECK_ARG(D % 128 == 0 && vocab % 64 == 0, "lm_head: D % 128, vocab % 64");
+  MS_CHECK_ARG(M >= 1 && M <= kGemvMaxM, "lm_head: 1 <= M <= 16");
+  MS_CHECK_ARG(D % 128 == 0 && D <= kQuantMaxK && vocab % 64 == 0,
+               "lm_head: D % 128 (D <= 16384), vocab % 64");
   hipStream_t st = ctx().stream;
   const int P = 4;
   const long blocks = vocab / 16 / P;
-  const size_t hl = (size_t)M * D;
-  const size_t need = hl * 2 * 2 + (size_t)blocks * M * 8 + 64;
+  const size_t qb = (quant_rows_bytes(M, D) + 255) & ~(size_t)255;
+  const size_t need = qb + (size_t)blocks * M * 8 + 64;
   void *buf = nullptr;
   if (int rc = scratch(need, &buf)) return rc;
-  _Float16 *hi = static_cast<_Float16 *>(buf), *lo = hi + hl;
-  float *bv = reinterpret_cast<float *>(lo + hl);
+  const QuantRows q = quant_rows_view(buf, M, D);
+  float *bv = reinterpret_cast<float *>(static_cast<uint8_t *>(buf) + qb);
   int32_t *bi = reinterpret_cast<int32_t *>(bv + blocks * M);
-  // final-norm outputs are bounded by sqrt(D) * max|gamma|; no prescale needed
-  if (int rc = launch_split(d_x, M, D, D, 1.0f, hi, lo, D, st)) return rc;
+  RowSrc r{};
+  r.x = d_x;
+  r.ld = D;
+  r.pre_scale = 1.f;
+  if (int rc = launch_quant_rows(r, M, D, q, st)) return rc;
   GemvArgs a{};
   a.epi = EPI_ARGMAX;
+  a.asrc = AS_QUANT;
   a.K = D;
   a.M = M;
-  a.a_hi = hi;
-  a.a_lo = lo;
-  a.lda = D;
-  a.out_mul = 1.0f;
+  a.q = q;
   a.seg[0] = GemvSeg{d_packed, scale, vocab, 0};
   a.nseg = 1;
   a.P = P;
-  a.S = 1;
   a.waves = 4;
   a.out = d_logits;
   a.ldo = vocab;

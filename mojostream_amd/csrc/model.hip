@@ -1,18 +1,17 @@
 // The Gemma-4 per-token layer loop on one MI355X.
 //
 // Per layer (e4b_forward_layer gemma4_e4b.mojo:459-540; gemma4_forward_layer
-// main.mojo:538-613) five launches on one stream:
-//   1. QKV GEMV   x_norm -> q|k|v split-K partials (Q, K, V fused, 3 scales)
-//   2. attention  partial sums + RoPE + causal GQA over the cache; the last
-//                 block per (seq, kv head) merges chunks, writes the O input
-//                 (fp16 hi/lo) and appends K/V to the cache
-//   3. O GEMV     -> partials; last block: x2 = x_norm + attn.Wo,
-//                 x2n = rmsnorm(x2), GateUp input
-//   4. GateUp     gate and up panels of the same columns in one block;
-//                 epilogue up*gate*sigmoid(gate) -> Down input
-//   5. Down GEMV  -> partials; last block: x_out = x2n + ffn.Wd (the layer
-//                 output), then PLE scale + rmsnorm of the next layer's input
-//                 (or the final weighted norm for the LM head).
+// main.mojo:538-613) six launches on one stream, each consumer reading one
+// fp32 row array (no split-K partials between kernels):
+//   1. QKV GEMV   prologue: xn = rmsnorm(ple * x) in LDS (block 0 stores xn);
+//                 Q, K, V fused (3 segments, 3 scales) -> qkv rows
+//   2. attention  chunk partials (RoPE, causal GQA over the cache), then one
+//                 merge block per query head: O input (fp16 hi/lo), K/V append
+//   3. O GEMV     A staged in LDS; epilogue x2 = xn + attn.Wo
+//   4. GateUp     prologue: x2n = rmsnorm(x2) (block 0 stores x2n); gate and
+//                 up panels of the same columns in one block; epilogue
+//                 up*gate*sigmoid(gate) -> Down input (fp16 hi/lo)
+//   5. Down GEMV  A staged in LDS; epilogue x_out = x2n + ffn.Wd
 // The residual adds to the normalized stream, as in the reference
 // (gemma4_e4b.mojo:520-538, gen_reference.py:160-172).
 //
@@ -48,8 +47,7 @@ struct Layer {
   float *kc = nullptr, *vc = nullptr;
   size_t cache_seq_stride = 0;
   int rope = 0;
-  float o_prescale = 1.f, f_prescale = 1.f;
-  int S_qkv = 1, S_o = 1, S_d = 1, n_chunks = 1;
+  int n_chunks = 1;
 };
 
 // profiling classes
@@ -87,12 +85,15 @@ struct ms_model {
   float *gamma = nullptr;
   bool has_lm = false;
   // workspaces
-  float *x_in = nullptr, *xn = nullptr, *x2n = nullptr;
-  _Float16 *aA_hi = nullptr, *aA_lo = nullptr, *aO_hi = nullptr, *aO_lo = nullptr,
-           *aF_hi = nullptr, *aF_lo = nullptr;
-  float *qkv_part = nullptr, *attn_part = nullptr, *o_part = nullptr,
-        *down_part = nullptr;
-  size_t qkv_part_stride = 0, o_part_stride = 0, d_part_stride = 0;
+  // rows between kernels: x_in (embeddings), xs (layer output), xn and x2n
+  // (normalised attention / FFN inputs, the residual bases), x2 (after O)
+  float *x_in = nullptr, *xs = nullptr, *xn = nullptr, *x2 = nullptr, *x2n = nullptr;
+  // O-projection input (attention output) and Down input (SwiGLU output)
+  float *aO = nullptr, *aF = nullptr;
+  // quantized activation rows for projections whose rows do not fit in LDS
+  void *quant = nullptr;
+  int quant_k = 0;
+  float *qkv = nullptr, *attn_part = nullptr;
   int32_t *pos = nullptr, *tok = nullptr, *ids_hist = nullptr, *step = nullptr;
   int hist_cap = 1024;
   float *arg_val = nullptr;
@@ -120,19 +121,6 @@ static int dmalloc(ms_model *m, void **p, size_t bytes) {
     return fail(MS_E_NOMEM, "model: out of device memory");
   m->allocs.push_back(*p);
   return MS_OK;
-}
-
-static float pow2_prescale(double bound) {
-  // largest power of two p <= 1 with bound * p <= 32768 (fp16 max 65504)
-  int e = 0;
-  while (bound * std::ldexp(1.0, -e) > 32768.0 && e < 60) ++e;
-  return (float)std::ldexp(1.0, -e);
-}
-
-static int pick_split(int panels, int KG, int target_blocks) {
-  int S = 1;
-  while ((long)panels * S < target_blocks && S * 2 <= KG && S < 4) S *= 2;
-  return S;
 }
 
 // ---- profiling helpers -------------------------------------------------------
@@ -191,62 +179,26 @@ struct RunCfg {
   int seq0;                 // first sequence (caches / positions offset)
 };
 
-// LDS bytes of a prologue GEMV (mirrors gemv_lds_bytes in q4.hip).
-static size_t prep_lds(int waves, int P, int M, int K, int S) {
-  const int ks = ((K / 128 + S - 1) / S) * 128;
-  return ((size_t)waves * P * 256 + (size_t)P * M * 16) * 4 + (size_t)2 * M * (ks + 8) * 2;
-}
-
-// GEMV whose activation rows come from a row preparation: in the kernel's LDS
-// prologue when it fits, else through the standalone prep kernel.
-static int gemv_prep(ms_model *m, GemvArgs a, const PrepArgs &p, hipStream_t st) {
-  if (prep_lds(a.waves, a.P, a.M, a.K, a.S) <= 150 * 1024) {
-    a.prep = p;
-    a.prep.on = 1;
-    return launch_gemv(a, st);
-  }
-  if (int rc = launch_prep_rows(p, a.M, a.K, m->aA_hi, m->aA_lo, st)) return rc;
-  a.prep = PrepArgs{};
-  a.a_hi = m->aA_hi;
-  a.a_lo = m->aA_lo;
-  a.lda = a.K;
+// Launch a projection of rows r: quantized in the kernel's prologue with
+// `waves` waves per block when the limb rows fit in LDS, else by the quant
+// kernel into m->quant first (the GEMV then reads them from global memory).
+static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipStream_t st) {
+  constexpr size_t kLdsLimit = 150 * 1024;
+  a.asrc = AS_ROWS;
+  a.rows = r;
+  a.waves = waves;
+  if (a.K <= 8 * 2 * 64 * waves && gemv_lds_need(a) <= kLdsLimit) return launch_gemv(a, st);
+  a.asrc = AS_QUANT;
+  a.rows = RowSrc{};
+  a.q = quant_rows_view(m->quant, a.M, a.K);
+  a.waves = 4;
+  if (int rc = launch_quant_rows(r, a.M, a.K, a.q, st)) return rc;
   return launch_gemv(a, st);
 }
 
-// Row preparation of layer l's attention input: the previous layer's output
-// (x2n + down partials) or the call's input rows, times PLE, rmsnorm.
-static PrepArgs attn_in_prep(ms_model *m, const RunCfg &rc, int l) {
-  PrepArgs p{};
-  const int M = rc.B * rc.T, D = m->d.hidden;
-  p.pre_scale = m->L[l].ple;
-  p.xn_out = m->xn;
-  if (l == rc.first_layer) {
-    p.base = rc.in_rows;
-  } else {
-    p.base = m->x2n;
-    p.parts = m->down_part;
-    p.n_parts = m->L[l - 1].S_d;
-    p.part_stride = (size_t)M * D;
-    if (rc.hidden) p.hid_out = rc.hidden + (size_t)(l - 1 - rc.first_layer) * M * D;
-  }
-  return p;
-}
-
-// The last layer's output x2n + down partials, optionally normalised for the
-// LM head (final norm with gamma, rmsnorm_weighted_inplace kernels.mojo:598-613).
-static PrepArgs final_prep(ms_model *m, const RunCfg &rc) {
-  PrepArgs p{};
-  const int M = rc.B * rc.T, D = m->d.hidden;
-  const int last = rc.first_layer + rc.n_layers - 1;
-  p.base = m->x2n;
-  p.parts = m->down_part;
-  p.n_parts = m->L[last].S_d;
-  p.part_stride = (size_t)M * D;
-  p.pre_scale = 1.f;
-  p.gamma = m->gamma;
-  p.hid_out = rc.out_rows;
-  if (rc.hidden) p.hid_out2 = rc.hidden + (size_t)(rc.n_layers - 1) * M * D;
-  return p;
+// Rows entering layer l: the previous layer's output or the call's input rows.
+static const float *layer_input(ms_model *m, const RunCfg &rc, int l) {
+  return l == rc.first_layer ? rc.in_rows : m->xs;
 }
 
 static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
@@ -256,25 +208,28 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
   const int D = m->d.hidden, F = m->d.ffn;
   const int ld = d.q_dim + 2 * d.kv_dim;
 
-  // 1. PLE + pre-norm (prologue) and the fused Q|K|V projection
+  // 1. x = rmsnorm(ple * x) in the prologue, fused Q|K|V projection
+  //    (gemma4_e4b.mojo:473-487)
   {
+    RowSrc r{};
+    r.x = layer_input(m, rc, l);
+    r.ld = D;
+    r.pre_scale = Ly.ple;
+    r.norm = 1;
+    r.y_out = m->xn;
     GemvArgs a{};
     a.epi = EPI_STORE;
     a.K = D;
     a.M = M;
-    a.out_mul = 1.f;
     a.seg[0] = GemvSeg{Ly.w[0], Ly.scale[0], d.q_dim, 0};
     a.seg[1] = GemvSeg{Ly.w[1], Ly.scale[1], d.kv_dim, d.q_dim};
     a.seg[2] = GemvSeg{Ly.w[2], Ly.scale[2], d.kv_dim, d.q_dim + d.kv_dim};
     a.nseg = 3;
     a.P = 1;
-    a.S = Ly.S_qkv;
-    a.waves = 4;
-    a.out = m->qkv_part;
+    a.out = m->qkv;
     a.ldo = ld;
-    a.split_stride = (size_t)M * ld;
     ProfScope ps(PC_QKV, (double)D * ld / 2, st);
-    if (int rc2 = gemv_prep(m, a, attn_in_prep(m, rc, l), st)) return rc2;
+    if (int rc2 = launch_proj(m, a, r, 8, st)) return rc2;
   }
   // 2. attention (chunks + merge/cache append)
   {
@@ -291,9 +246,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.cache_len = d.cache_len;
     a.clamp = d.clamp_reads;
     a.scale = 1.0f / sqrtf((float)d.head_dim);
-    a.qkv = m->qkv_part;
-    a.S = Ly.S_qkv;
-    a.split_stride = (size_t)M * ld;
+    a.qkv = m->qkv;
     a.ld = ld;
     a.apply_rope = 1;
     a.cos_t = m->ropes[Ly.rope].cs;
@@ -304,84 +257,71 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.cache_seq_stride = Ly.cache_seq_stride;
     a.n_chunks = Ly.n_chunks;
     a.part = m->attn_part;
-    a.out = nullptr;
-    a.out_hi = m->aO_hi;
-    a.out_lo = m->aO_lo;
-    a.out_prescale = Ly.o_prescale;
+    a.out = m->aO;
     a.write_cache = 1;
     // KV bytes read at the current position are counted by bench.py
     ProfScope ps(PC_ATTN, 0.0, st);
     if (int rc2 = launch_attention(a, st)) return rc2;
   }
-  // 3. O projection -> split-K partials
+  // 3. x2 = x + attn . Wo (residual epilogue)
   {
+    RowSrc r{};
+    r.x = m->aO;
+    r.ld = d.q_dim;
+    r.pre_scale = 1.f;
     GemvArgs a{};
-    a.epi = EPI_STORE;
+    a.epi = EPI_RESID;
     a.K = d.q_dim;
     a.M = M;
-    a.a_hi = m->aO_hi;
-    a.a_lo = m->aO_lo;
-    a.lda = d.q_dim;
-    a.out_mul = 1.0f / Ly.o_prescale;
     a.seg[0] = GemvSeg{Ly.w[3], Ly.scale[3], D, 0};
     a.nseg = 1;
     a.P = 1;
-    a.S = Ly.S_o;
-    a.waves = 4;
-    a.out = m->o_part;
+    a.out = m->x2;
     a.ldo = D;
-    a.split_stride = (size_t)M * D;
+    a.resid = m->xn;
     ProfScope ps(PC_O, (double)d.q_dim * D / 2, st);
-    if (int rc2 = launch_gemv(a, st)) return rc2;
+    if (int rc2 = launch_proj(m, a, r, 4, st)) return rc2;
   }
-  // 4. residual + post-attention norm (prologue), Gate|Up, SwiGLU epilogue
+  // 4. x2n = rmsnorm(x2) in the prologue, Gate|Up, SwiGLU epilogue
   {
+    RowSrc r{};
+    r.x = m->x2;
+    r.ld = D;
+    r.pre_scale = 1.f;
+    r.norm = 1;
+    r.y_out = m->x2n;
     GemvArgs a{};
     a.epi = EPI_SWIGLU;
     a.K = D;
     a.M = M;
-    a.out_mul = 1.f;
     a.seg[0] = GemvSeg{Ly.w[4], Ly.scale[4], F, 0};
     a.seg[1] = GemvSeg{Ly.w[5], Ly.scale[5], F, 0};
     a.nseg = 2;
     a.P = 2;
-    a.S = 1;
-    a.waves = 4;
-    a.out = nullptr;
-    a.sw_hi = m->aF_hi;
-    a.sw_lo = m->aF_lo;
+    a.sw_out = m->aF;
     a.ldo_sw = F;
-    a.sw_prescale = Ly.f_prescale;
-    PrepArgs p{};
-    p.base = m->xn;
-    p.parts = m->o_part;
-    p.n_parts = Ly.S_o;
-    p.part_stride = (size_t)M * D;
-    p.pre_scale = 1.f;
-    p.xn_out = m->x2n;
     ProfScope ps(PC_GATEUP, (double)D * F, st);
-    if (int rc2 = gemv_prep(m, a, p, st)) return rc2;
+    if (int rc2 = launch_proj(m, a, r, 4, st)) return rc2;
   }
-  // 5. Down projection -> split-K partials (summed by the next consumer)
+  // 5. x_out = x2n + ffn . Wd (residual epilogue): the layer output
   {
+    RowSrc r{};
+    r.x = m->aF;
+    r.ld = F;
+    r.pre_scale = 1.f;
     GemvArgs a{};
-    a.epi = EPI_STORE;
+    a.epi = EPI_RESID;
     a.K = F;
     a.M = M;
-    a.a_hi = m->aF_hi;
-    a.a_lo = m->aF_lo;
-    a.lda = F;
-    a.out_mul = 1.0f / Ly.f_prescale;
     a.seg[0] = GemvSeg{Ly.w[6], Ly.scale[6], D, 0};
     a.nseg = 1;
     a.P = 1;
-    a.S = Ly.S_d;
-    a.waves = 4;
-    a.out = m->down_part;
+    a.out = m->xs;
     a.ldo = D;
-    a.split_stride = (size_t)M * D;
+    a.resid = m->x2n;
+    if (rc.hidden) a.out2 = rc.hidden + (size_t)(l - rc.first_layer) * M * D;
     ProfScope ps(PC_DOWN, (double)F * D / 2, st);
-    if (int rc2 = launch_gemv(a, st)) return rc2;
+    if (int rc2 = launch_proj(m, a, r, 16, st)) return rc2;
   }
   return MS_OK;
 }
@@ -391,33 +331,32 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
 static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const ArgmaxFin &fin,
                       hipStream_t st) {
   const int D = m->d.hidden;
-  PrepArgs p = final_prep(m, rc);
-  p.base += (size_t)row0 * D;
-  p.parts += (size_t)row0 * D;
-  if (p.hid_out) p.hid_out += (size_t)row0 * D;
-  if (p.hid_out2) p.hid_out2 += (size_t)row0 * D;
+  // final norm with gamma (apply_final_norm lm_head.mojo:119-130,
+  // rmsnorm_weighted_inplace kernels.mojo:598-613) fused into the quantization
+  RowSrc r{};
+  r.x = m->xs + (size_t)row0 * D;
+  r.ld = D;
+  r.pre_scale = 1.f;
+  r.norm = 1;
+  r.gamma = m->gamma;
+  if (rc.out_rows) r.x_out = rc.out_rows + (size_t)row0 * D;
   GemvArgs a{};
   a.epi = EPI_ARGMAX;
+  a.asrc = AS_QUANT;
   a.K = D;
   a.M = M;
-  a.out_mul = 1.f;
+  a.q = quant_rows_view(m->quant, M, D);
   a.seg[0] = GemvSeg{m->lm_w, m->lm_scale, m->d.vocab, 0};
   a.nseg = 1;
   a.P = 4;
-  a.S = 1;
   a.waves = 4;
   a.out = nullptr;
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
   {
-    // one prep block per row (the head has thousands of blocks, so a per-block
-    // prologue would re-read the residual rows thousands of times)
     ProfScope ps(PC_LM, (double)D * m->d.vocab / 2, st);
-    if (int r = launch_prep_rows(p, M, D, m->aA_hi, m->aA_lo, st)) return r;
-    a.a_hi = m->aA_hi;
-    a.a_lo = m->aA_lo;
-    a.lda = D;
-    if (int r = launch_gemv(a, st)) return r;
+    if (int r2 = launch_quant_rows(r, M, D, a.q, st)) return r2;
+    if (int r2 = launch_gemv(a, st)) return r2;
   }
   ArgmaxFin f = fin;
   f.arg_val = m->arg_val;
@@ -430,10 +369,10 @@ static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const Argm
 
 // Output rows of the last layer without an LM head.
 static int enqueue_output(ms_model *m, const RunCfg &rc, hipStream_t st) {
-  PrepArgs p = final_prep(m, rc);
-  p.gamma = nullptr;
-  ProfScope ps(PC_OTHER, 0.0, st);
-  return launch_prep_rows(p, rc.B * rc.T, m->d.hidden, nullptr, nullptr, st);
+  if (!rc.out_rows) return MS_OK;
+  const size_t n = (size_t)rc.B * rc.T * m->d.hidden;
+  MS_HIP_TRY(hipMemcpyAsync(rc.out_rows, m->xs, n * 4, hipMemcpyDeviceToDevice, st));
+  return MS_OK;
 }
 
 // ---- streaming: two HBM slots filled on the copy stream ----------------------
@@ -595,9 +534,6 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
     }
     Ly.rope = rid;
     const int ncols_qkv = ld.q_dim + 2 * ld.kv_dim;
-    Ly.S_qkv = pick_split(ncols_qkv / 16, d.hidden / 128, 512);
-    Ly.S_o = pick_split(d.hidden / 16, ld.q_dim / 128, 512);
-    Ly.S_d = pick_split(d.hidden / 16, d.ffn / 128, 512);
     const int span = ld.cache_kind == MS_CACHE_CIRCULAR ? ld.cache_len + d.max_rows - 1
                                                         : ld.cache_len + d.max_rows;
     Ly.n_chunks = cdiv(span, kAttnChunk);
@@ -606,6 +542,7 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
                                       d.max_rows * G * (ld.head_dim + 2));
     m->qkv_max = std::max(m->qkv_max, ncols_qkv);
     m->q_max = std::max(m->q_max, ld.q_dim);
+    m->quant_k = std::max(m->quant_k, std::max(std::max(d.hidden, d.ffn), ld.q_dim));
     m->kv_max = std::max(m->kv_max, ld.kv_dim);
     m->hd_max = std::max(m->hd_max, ld.head_dim);
     m->L.push_back(Ly);
@@ -613,24 +550,15 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   int rc;
   const int D = d.hidden, F = d.ffn;
   if ((rc = dmalloc(m, (void **)&m->x_in, (size_t)M * D * 4)) ||
+      (rc = dmalloc(m, (void **)&m->xs, (size_t)M * D * 4)) ||
       (rc = dmalloc(m, (void **)&m->xn, (size_t)M * D * 4)) ||
+      (rc = dmalloc(m, (void **)&m->x2, (size_t)M * D * 4)) ||
       (rc = dmalloc(m, (void **)&m->x2n, (size_t)M * D * 4)) ||
-      (rc = dmalloc(m, (void **)&m->aA_hi, (size_t)M * D * 2)) ||
-      (rc = dmalloc(m, (void **)&m->aA_lo, (size_t)M * D * 2)) ||
-      (rc = dmalloc(m, (void **)&m->aO_hi, (size_t)M * m->q_max * 2)) ||
-      (rc = dmalloc(m, (void **)&m->aO_lo, (size_t)M * m->q_max * 2)) ||
-      (rc = dmalloc(m, (void **)&m->aF_hi, (size_t)M * F * 2)) ||
-      (rc = dmalloc(m, (void **)&m->aF_lo, (size_t)M * F * 2)))
+      (rc = dmalloc(m, (void **)&m->aO, (size_t)M * m->q_max * 4)) ||
+      (rc = dmalloc(m, (void **)&m->aF, (size_t)M * F * 4)) ||
+      (rc = dmalloc(m, &m->quant, quant_rows_bytes(M, m->quant_k))))
     return cleanup(rc);
-  int sq = 1, so = 1, sd = 1;
-  for (auto &Ly : m->L) {
-    sq = std::max(sq, Ly.S_qkv);
-    so = std::max(so, Ly.S_o);
-    sd = std::max(sd, Ly.S_d);
-  }
-  if ((rc = dmalloc(m, (void **)&m->qkv_part, (size_t)sq * M * m->qkv_max * 4)) ||
-      (rc = dmalloc(m, (void **)&m->o_part, (size_t)so * M * D * 4)) ||
-      (rc = dmalloc(m, (void **)&m->down_part, (size_t)sd * M * D * 4)) ||
+  if ((rc = dmalloc(m, (void **)&m->qkv, (size_t)M * m->qkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
       (rc = dmalloc(m, (void **)&m->pos, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->tok, 64 * 4)) ||
@@ -735,12 +663,6 @@ extern "C" int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_
   }
   Ly.scale[mat] = scale;
   Ly.set_mask |= 1 << mat;
-  // fp16 range of the activations feeding O and Down (see pow2_prescale):
-  // |v| <= 8*s_v*D, |swiglu| <= |gate||up| <= (8*s_g*D)(8*s_u*D).
-  const double bD = (double)D;
-  if (Ly.set_mask & (1 << 2)) Ly.o_prescale = pow2_prescale(8.0 * Ly.scale[2] * bD);
-  if ((Ly.set_mask & 0x30) == 0x30)
-    Ly.f_prescale = pow2_prescale(64.0 * Ly.scale[4] * Ly.scale[5] * bD * bD);
   if (m->gexec) {
     (void)hipGraphExecDestroy(m->gexec);
     m->gexec = nullptr;

@@ -1,4 +1,4 @@
-// Q4 GEMV/GEMM interfaces shared between translation units.
+// Q4 GEMV interfaces shared between translation units.
 #pragma once
 #include "common.h"
 
@@ -13,64 +13,63 @@ struct GemvSeg {
 };
 
 enum GemvEpilogue {
-  EPI_STORE = 0,       // out[s][m][col] = value (s = K split)
-  EPI_ACCUMULATE = 1,  // out[m][col] += value (S must be 1)
+  EPI_STORE = 0,       // out[m][col] = value
+  EPI_ACCUMULATE = 1,  // out[m][col] += value
   EPI_SWIGLU = 2,      // seg0 = gate, seg1 = up, same panel per block:
-                       // up*gate*sigmoid(gate) -> f16 hi/lo (times act_scale)
-                       // and optionally fp32 into out
+                       // sw_out[m][col] = up*gate*sigmoid(gate)
   EPI_ARGMAX = 3,      // LM head: logits (optional) + per-block argmax
-  EPI_RESID = 4,       // S=1, P=1: x = resid + value -> out [M][ldo] and the
-                       // block's sum of squares per row -> ss_out[m][block]
+  EPI_RESID = 4,       // out[m][col] = resid[m][col] + value (and out2)
 };
 
-// Optional GEMV prologue: every block rebuilds the activation rows it needs
-// in LDS.  x = base + sum_{s<n_parts} parts[s]; y = rmsnorm(x * pre_scale)
-// (* gamma); the block keeps fp16 hi/lo of y for its K range.  Block 0 also
-// stores x (the previous layer's output) and y (the residual base).
-struct PrepArgs {
-  int on;
-  // Reduced-row mode (xsum set): x = xsum[m][k] was summed by a producer,
-  // which also left n_ss partial sums of (x*pre_scale)^2 per row in ss.
-  const float *xsum;    // [M][K] or null
-  const float *ss;      // [M][n_ss]
-  int n_ss;
-  // Direct mode: x = base + sum of split partials.
-  const float *base;    // [M][K] or null
-  const float *parts;   // [n_parts][M][K] or null
-  int n_parts;
-  size_t part_stride;   // floats between split slices
-  float pre_scale;      // PLE of this layer (1 for the post-attention norm)
-  const float *gamma;   // final-norm weights or null
-  float *xn_out;        // block 0: y [M][K] or null
-  float *hid_out;       // block 0: x [M][K] or null
-  float *hid_out2;      // block 0: second copy of x or null
+// Activation rows enter the MFMA as four signed int8 limbs of a per-row
+// fixed-point value X = rint(y * 2^s), |X| < 2^30:  y * 2^s = sum_l limb_l 2^(8l).
+// The weights enter as their raw nibbles n (0..15), so the integer dot product
+// sum_k X_k (n_k - 8) = sum_k X_k n_k - 8 sum_k X_k is exact; it is scaled by
+// 2^-s and the tensor scale once per output.
+enum GemvASource {
+  AS_ROWS = 0,   // prologue: every block quantizes the fp32 rows into LDS
+  AS_QUANT = 1,  // limbs prepared in global memory by launch_quant_rows
+};
+
+// fp32 rows and the transform applied before quantization:
+// y = x * pre_scale; if norm: y *= 1/sqrt(mean(y^2) + 1e-6); if gamma: y *= gamma.
+struct RowSrc {
+  const float *x;      // [M][ld]
+  int ld;
+  float pre_scale;
+  int norm;
+  const float *gamma;  // or null
+  float *y_out;        // y [M][K] (written once: block 0 or the quant kernel) or null
+  float *x_out;        // copy of x [M][K] (same writer) or null
+};
+
+// Quantized rows in global memory: limb l of row m at
+// limbs[(4m + l) * K + limb position of k] (MFMA fragment order per 128-row
+// super-tile), shift[m] = s, xsum[m] = sum_k X_k.
+struct QuantRows {
+  int8_t *limbs;
+  int32_t *shift;
+  long long *xsum;
 };
 
 struct GemvArgs {
-  int epi;                        // GemvEpilogue
+  int epi;        // GemvEpilogue
+  int asrc;       // GemvASource
   int K, M;
-  const _Float16 *a_hi, *a_lo;  // activations [M][lda] (hi/lo fp16 split), unless prep.on
-  int lda;
-  float out_mul;                 // undoes the activation pre-scale
+  RowSrc rows;    // AS_ROWS
+  QuantRows q;    // AS_QUANT
   GemvSeg seg[3];
   int nseg;
-  int P;                          // panels per block (EPI_SWIGLU: 2)
-  int S;                          // K splits
-  int waves;                      // waves per block (4 or 8)
-  float *out;                     // EPI_STORE: [S][M][ldo]
+  int P;          // panels per block (EPI_SWIGLU: 2, gate and up)
+  int waves;      // waves per block
+  float *out;     // [M][ldo]
   int ldo;
-  size_t split_stride;
-  // EPI_SWIGLU
-  _Float16 *sw_hi, *sw_lo;        // [M][ldo_sw]
+  float *sw_out;  // EPI_SWIGLU: [M][ldo_sw]
   int ldo_sw;
-  float sw_prescale;
-  // EPI_ARGMAX: per-block maximum and its first index, per row
-  float *arg_val;                 // [blocks][M]
-  int32_t *arg_idx;               // [blocks][M]
-  // EPI_RESID
-  const float *resid;             // [M][ldo]
-  float *ss_out;                  // [M][n_blocks]
-  PrepArgs prep;
+  float *arg_val;    // EPI_ARGMAX: [blocks][M]
+  int32_t *arg_idx;  // EPI_ARGMAX: [blocks][M]
+  const float *resid;  // EPI_RESID: [M][ldo]
+  float *out2;         // EPI_RESID: optional second copy [M][ldo]
 };
 
 // Final argmax over the LM head's per-block maxima (greedy branch of
@@ -86,19 +85,19 @@ struct ArgmaxFin {
   int32_t *step;        // step counter (with ids_hist)
 };
 
+constexpr int kGemvMaxM = 16;
+constexpr int kQuantMaxK = 16384;  // longest row a 1024-thread block quantizes
+
 int launch_gemv(const GemvArgs &a, hipStream_t st);
-// fp32 rows -> hi/lo fp16 (times prescale)
-int launch_split(const float *x, int M, int K, int ldx, float prescale,
-                 _Float16 *hi, _Float16 *lo, int ldo, hipStream_t st);
-int launch_sum_parts(float *out, const float *parts, int S, size_t n, hipStream_t st);
+// LDS bytes a GEMV launch needs.
+size_t gemv_lds_need(const GemvArgs &a);
+// Quantize M rows of length K (one block per row) into q.
+int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st);
+// Device bytes of a QuantRows buffer for M rows of length K (limbs, shifts, sums).
+size_t quant_rows_bytes(int M, int K);
+// Carve a QuantRows view out of one buffer of quant_rows_bytes(M, K).
+QuantRows quant_rows_view(void *buf, int M, int K);
 int pack_device(uint8_t *dst, const uint8_t *src, int K, int N, hipStream_t st);
 int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st);
-// Standalone row preparation (same math as the GEMV prologue) writing the
-// fp16 hi/lo split to global memory: used where the consumer is not a GEMV.
-int launch_prep_rows(const PrepArgs &p, int M, int K, _Float16 *hi, _Float16 *lo,
-                     hipStream_t st);
-// Residual sum of a row: xsum = base + sum parts (also into hid_out/hid_out2)
-// and per-256-column partial sums of (xsum*pre_scale)^2 -> ss [M][ceil(K/256)].
-int launch_rowsum(const PrepArgs &p, int M, int K, float *xsum, float *ss, hipStream_t st);
 
 }  // namespace ms

@@ -2,12 +2,12 @@
 // MFMA GEMV used for decode (M <= 16 rows) with fused epilogues.
 //
 // Reference: matmul_q4_bpack_raw (kernels.mojo:201-267) computes
-// C += A . deq(W) with w = (nibble-8)*scale.  Here the nibble becomes the exact
-// fp16 value (nibble-8) with one v_and_or_b32 and one packed-fp16 op per pair,
-// the activation row is split into fp16 hi+lo (error ~2^-22), and
-// v_mfma_f32_16x16x32_f16 accumulates in fp32; the per-tensor scale is applied
-// once per output.  For M <= 8 the hi rows and lo rows share one MFMA (rows
-// 0..M-1 hi, M..2M-1 lo), so one MFMA covers 512 weights for any M <= 8.
+// C += A . deq(W) with w = (nibble-8)*scale.  Here the weight nibbles go into
+// v_mfma_i32_16x16x64_i8 as they are (three bit operations per eight weights),
+// each activation row as four int8 limbs of a 31-bit fixed-point value with a
+// per-row power-of-two scale, so the dot product sum X*(n-8) is exact integer
+// arithmetic; it is scaled by 2^-s and the tensor scale once per output.  For
+// M <= 4 the 4M limb rows share one MFMA, so one MFMA covers 1024 weights.
 #include "q4.h"
 
 #include <cmath>
@@ -21,7 +21,7 @@ namespace ms {
 __global__ void k_pack(uint32_t *__restrict__ dst, const uint8_t *__restrict__ src,
                        int K, int N) {
   const size_t total = (size_t)K * N / 8;
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= total) return;
   const size_t per_panel = (size_t)K * 2;  // dwords per panel
   const int nb = (int)(i / per_panel);
@@ -52,7 +52,7 @@ static int check_q4_shape(int K, int N) {
 __global__ void k_dequant_rowmajor(float *__restrict__ out,
                                    const uint8_t *__restrict__ w, size_t nbytes,
                                    float scale) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= nbytes) return;
   const uint8_t b = w[i];
   // (nibble - 8) * scale: one exact int->fp32 conversion and one rounded
@@ -65,7 +65,7 @@ __global__ void k_dequant_packed(float *__restrict__ out,
                                  const uint32_t *__restrict__ w, int K, int N,
                                  float scale) {
   const size_t total = (size_t)K * N / 8;
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= total) return;
   const size_t per_panel = (size_t)K * 2;
   const int nb = (int)(i / per_panel);
@@ -84,41 +84,58 @@ __global__ void k_dequant_packed(float *__restrict__ out,
 }
 
 // ------------------------------------------------------------------------------
-// activation split
+// helpers
 // ------------------------------------------------------------------------------
-__global__ void k_split(const float *__restrict__ x, int M, int K, int ldx,
-                        float prescale, _Float16 *__restrict__ hi,
-                        _Float16 *__restrict__ lo, int ldo) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= M * K) return;
-  const int m = i / K, k = i % K;
-  _Float16 h, l;
-  split_hi_lo(x[(size_t)m * ldx + k] * prescale, &h, &l);
-  hi[(size_t)m * ldo + k] = h;
-  lo[(size_t)m * ldo + k] = l;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Global-memory loads through an explicit global pointer: generic (flat)
+// loads also count against the LDS wait counter, so an LDS wait would stall
+// on them.
+template <class T>
+__device__ inline T ldg(const void *p) {
+  return *(const __attribute__((address_space(1))) T *)p;
+}
+template <>
+__device__ inline float4 ldg<float4>(const void *p) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 v = *(const __attribute__((address_space(1))) f32x4 *)p;
+  return float4{v.x, v.y, v.z, v.w};
 }
 
-int launch_split(const float *x, int M, int K, int ldx, float prescale,
-                 _Float16 *hi, _Float16 *lo, int ldo, hipStream_t st) {
-  const int n = M * K;
-  hipLaunchKernelGGL(k_split, dim3(cdiv(n, 256)), dim3(256), 0, st, x, M, K, ldx,
-                     prescale, hi, lo, ldo);
-  MS_HIP_TRY(hipGetLastError());
-  return MS_OK;
+// A uniform value passed through an opaque register move: the compiler can no
+// longer turn selects between such values back into an indexed memory access
+// (which would put them in scratch memory or re-read the argument struct).
+template <class T>
+__device__ inline T launder(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
 }
 
-// ------------------------------------------------------------------------------
-// block reductions
-// ------------------------------------------------------------------------------
 __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
 
-// Sum over the block; every thread returns the total.  sh: >= 16 floats.
-__device__ float block_sum(float v, float *sh) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+// Block reductions over NT threads; every thread returns the result.
+// sh: >= 32 entries.  The block size is a template constant: reading blockDim
+// loads it from the dispatch packet, and waiting for that load would also wait
+// for every weight load already in flight.
+template <int NT>
+__device__ inline float block_sum(float v, float *sh) {
+  constexpr int nw = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   v = wave_sum(v);
   __syncthreads();
   if (lane == 0) sh[w] = v;
@@ -127,279 +144,501 @@ __device__ float block_sum(float v, float *sh) {
   for (int i = 0; i < nw; ++i) t += sh[i];
   return t;
 }
+template <int NT>
+__device__ inline float block_max(float v, float *sh) {
+  constexpr int nw = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  float t = sh[0];
+  for (int i = 1; i < nw; ++i) t = fmaxf(t, sh[i]);
+  return t;
+}
+template <int NT>
+__device__ inline double block_sum_d(double v, double *sh) {
+  constexpr int nw = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_sum_d(v);
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int i = 0; i < nw; ++i) t += sh[i];
+  return t;
+}
 
 // ------------------------------------------------------------------------------
-// row preparation (residual sum + PLE + rmsnorm), shared by the GEMV prologue
-// and the standalone kernel.  Order of the fp32 operations follows the
-// reference: x = x + proj (gemma4_e4b.mojo:522,538), x *= ple (kernels.mojo:
-// 506-516), x *= 1/sqrt(mean(x^2)+1e-6) (:474-489), * gamma (:598-613).
+// Row quantization.
+//
+// Element order of the limb rows (MFMA fragment order): inside a 128-row
+// super-tile, lane group g of the B operand holds rows 32g..32g+31 of its
+// column, dword t = rows 8t..8t+7 with row e in nibble (e>>1) + 4(e&1).  The
+// B fragment of MFMA h (two per super-tile) is the four dwords
+// [d & 0x0F0F0F0F, (d >> 4) & 0x0F0F0F0F] of dwords t = 2h and 2h+1, so byte b
+// of the low/high word holds rows e = {0,4,1,5} / {2,6,3,7}.  The A limbs are
+// stored in that same order: an 8-row group t of lane group g lands at byte
+// 128G + 32g + 16(t>>1) + 8(t&1), low word then high word.
 // ------------------------------------------------------------------------------
-constexpr int kPrepMaxPer = 20;  // K <= kPrepMaxPer * blockDim.x
+__device__ inline int limb_pos8(int k) {
+  return (k >> 7) * 128 + ((k >> 5) & 3) * 32 + ((k >> 4) & 1) * 16 + ((k >> 3) & 1) * 8;
+}
 
-// Builds activation row m: every thread loads all of its elements (base and
-// every split partial) before any use, so the row costs one memory round trip.
-// Outputs: the normalised values stay in registers (y[]); block `writer`
-// stores x and y; elements with k in [k0, k0+ks) go to LDS as fp16 hi/lo
-// (or to global hi/lo when gl_hi is set).
-__device__ void prep_row(const PrepArgs &p, int K, int m, bool writer, int k0, int ks,
-                         _Float16 *lds_hi, _Float16 *lds_lo, int ldl, _Float16 *gl_hi,
-                         _Float16 *gl_lo, float *sh) {
-  const int nt = blockDim.x, tid = threadIdx.x;
-  // Branch-free loads: indices are clamped into the row and absent split
-  // slices alias slice 0, so every load is unconditional and in bounds and the
-  // compiler keeps a whole half-row of them in flight; values are masked after.
-  constexpr int HP = kPrepMaxPer / 2;
-  float v[kPrepMaxPer], gm[kPrepMaxPer];
-  float ss = 0.f;
-  const float *bp = p.base ? p.base : p.parts;
-  const float *gp = p.gamma ? p.gamma : bp;
-  const float *ps[4];
+// X = rint(v * mul) for eight consecutive rows; limb l of the group as its
+// low/high words.  Returns sum X.
+//
+// For |X| < 2^30 the bytes of E = (X + 0x80808080) ^ 0x80808080 are the four
+// balanced limbs of X: X + 0x80808080 = sum_l u_l 2^(8l) with bytes u_l, so
+// X = sum_l (u_l - 128) 2^(8l), and u_l - 128 as a signed byte is u_l ^ 0x80.
+// The low word of limb l takes byte l of rows {0,4,1,5}, the high word rows
+// {2,6,3,7}.
+__device__ inline uint32_t byte_gather(uint32_t a, uint32_t b, uint32_t c, uint32_t d, int l) {
+  const int sh = 8 * l;
+  return ((a >> sh) & 0xFFu) | (((b >> sh) & 0xFFu) << 8) | (((c >> sh) & 0xFFu) << 16) |
+         (((d >> sh) & 0xFFu) << 24);
+}
+
+__device__ inline long long quant8(const float (&v)[8], float mul, uint32_t (&lo)[4],
+                                   uint32_t (&hi)[4]) {
+  uint32_t E[8];
+  long long xs = 0;
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-    ps[s] = p.parts ? p.parts + (s < p.n_parts ? s : 0) * p.part_stride : bp;
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    float xb[HP], xp[4][HP], xg[HP];
-#pragma unroll
-    for (int i = 0; i < HP; ++i) {
-      const int k = min(tid + (hh * HP + i) * nt, K - 1);
-      const size_t idx = (size_t)m * K + k;
-      xb[i] = bp[idx];
-      xg[i] = gp[p.gamma ? k : idx];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) xp[s][i] = ps[s][idx];
-    }
-#pragma unroll
-    for (int i = 0; i < HP; ++i) {
-      const int k = tid + (hh * HP + i) * nt;
-      float x = p.base ? xb[i] : 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        if (s < p.n_parts) x = x + xp[s][i];
-      if (p.n_parts > 4) {
-        const size_t idx = (size_t)m * K + min(k, K - 1);
-        for (int s = 4; s < p.n_parts; ++s) x = x + p.parts[s * p.part_stride + idx];
-      }
-      v[hh * HP + i] = (k < K) ? x : 0.f;
-      gm[hh * HP + i] = p.gamma ? xg[i] : 1.f;
-    }
+  for (int e = 0; e < 8; ++e) {
+    const int x = (int)rintf(v[e] * mul);
+    xs += x;
+    E[e] = ((uint32_t)x + 0x80808080u) ^ 0x80808080u;
   }
 #pragma unroll
-  for (int i = 0; i < kPrepMaxPer; ++i) {
-    const float xs = v[i] * p.pre_scale;
-    ss += xs * xs;  // zero for k >= K
+  for (int l = 0; l < 4; ++l) {
+    lo[l] = byte_gather(E[0], E[4], E[1], E[5], l);
+    hi[l] = byte_gather(E[2], E[6], E[3], E[7], l);
   }
-  ss = block_sum(ss, sh);
-  const float inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+  return xs;
+}
+
+// Per-row shift s with max|y| * 2^s < 2^30.
+__device__ inline int row_shift(float amax) {
+  if (!(amax > 0.f)) return 0;
+  int ex;
+  (void)frexpf(amax, &ex);  // amax < 2^ex
+  return 30 - ex;
+}
+
+// One row through NT threads, NG 8-row groups per thread (K <= 8 * NG * NT).
+template <int NT, int NG, bool GAM>
+struct RowRegs {
+  float v[NG][8];
+  float g[GAM ? NG : 1][8];
+};
+
+// Issue the loads of row m.  Threads past the end of the row load nothing (a
+// clamped duplicate address would send every idle thread of every block to
+// the same cache line).
+template <int NT, int NG, bool GAM>
+__device__ inline void row_load(const RowSrc &r, int K, int m, RowRegs<NT, NG, GAM> &R) {
+  const int nq = K >> 3;
 #pragma unroll
-  for (int i = 0; i < kPrepMaxPer; ++i) {
-    const int k = tid + i * nt;
-    if (k < K) {
-      const float x = v[i];
-      float y = (x * p.pre_scale) * inv;
-      if (p.gamma) y = y * gm[i];
-      const size_t idx = (size_t)m * K + k;
-      if (writer) {
-        if (p.hid_out) p.hid_out[idx] = x;
-        if (p.hid_out2) p.hid_out2[idx] = x;
-        if (p.xn_out) p.xn_out[idx] = y;
-      }
-      if (k >= k0 && k < k0 + ks) {
-        _Float16 h, l;
-        split_hi_lo(y, &h, &l);
-        if (gl_hi) {
-          gl_hi[idx] = h;
-          gl_lo[idx] = l;
-        } else {
-          lds_hi[(size_t)m * ldl + (k - k0)] = h;
-          lds_lo[(size_t)m * ldl + (k - k0)] = l;
-        }
+  for (int gi = 0; gi < NG; ++gi) {
+    const int q = (int)threadIdx.x + gi * NT;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) R.v[gi][e] = 0.f;
+    if (GAM) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) R.g[gi][e] = 0.f;
+    }
+    if (q < nq) {
+      const float *p = r.x + (size_t)m * r.ld + 8 * q;
+      const float4 a = ldg<float4>(p), b = ldg<float4>(p + 4);
+      R.v[gi][0] = a.x; R.v[gi][1] = a.y; R.v[gi][2] = a.z; R.v[gi][3] = a.w;
+      R.v[gi][4] = b.x; R.v[gi][5] = b.y; R.v[gi][6] = b.z; R.v[gi][7] = b.w;
+      if (GAM) {
+        const float4 c = ldg<float4>(r.gamma + 8 * q), d = ldg<float4>(r.gamma + 8 * q + 4);
+        R.g[gi][0] = c.x; R.g[gi][1] = c.y; R.g[gi][2] = c.z; R.g[gi][3] = c.w;
+        R.g[gi][4] = d.x; R.g[gi][5] = d.y; R.g[gi][6] = d.z; R.g[gi][7] = d.w;
       }
     }
   }
 }
 
-__global__ __launch_bounds__(256) void k_prep_rows(PrepArgs p, int K, _Float16 *hi,
-                                                   _Float16 *lo) {
-  __shared__ float sh[16];
-  prep_row(p, K, blockIdx.x, true, 0, hi ? K : 0, nullptr, nullptr, 0, hi, lo, sh);
+// Sum of squares and maximum |value| over the block in one reduction pass.
+// sh: >= 2 * 16 floats.
+template <int NT>
+__device__ inline void block_sum_max(float &ss, float &mx, float *sh) {
+  constexpr int nw = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  ss = wave_sum(ss);
+  mx = wave_max(mx);
+  __syncthreads();
+  if (lane == 0) {
+    sh[w] = ss;
+    sh[16 + w] = mx;
+  }
+  __syncthreads();
+  float t = 0.f, u = 0.f;
+#pragma unroll
+  for (int i = 0; i < nw; ++i) {
+    t += sh[i];
+    u = fmaxf(u, sh[16 + i]);
+  }
+  ss = t;
+  mx = u;
 }
 
-int launch_prep_rows(const PrepArgs &p, int M, int K, _Float16 *hi, _Float16 *lo,
-                     hipStream_t st) {
-  MS_CHECK_ARG(K <= kPrepMaxPer * 256, "prep: row too long");
-  hipLaunchKernelGGL(k_prep_rows, dim3(M), dim3(256), 0, st, p, K, hi, lo);
+// Transform (x * pre_scale, rmsnorm, gamma: rmsnorm_inplace kernels.mojo:474-489,
+// ple_scale_inplace :506-516, rmsnorm_weighted_inplace :598-613), optional
+// fp32 stores by `writer`, quantization and limb stores: limb l of row m goes
+// to dst + (4m + l) * ld_dst + limb position.  Returns the row shift s and the
+// calling wave's part of sum X (summed over the waves by the caller).
+template <int NT, int NG, bool GAM>
+__device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
+                                  RowRegs<NT, NG, GAM> &R, int8_t *dst, size_t ld_dst,
+                                  float *sh, int *s_out, double *xs_wave) {
+  const int nq = K >> 3;
+  float y[NG][8];
+  float ss = 0.f, mx = 0.f;
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y[gi][e] = R.v[gi][e] * r.pre_scale;
+      ss += y[gi][e] * y[gi][e];
+      mx = fmaxf(mx, fabsf(y[gi][e]));
+    }
+  // one reduction for the norm and the maximum (max|y * inv| = max|y| * inv)
+  block_sum_max<NT>(ss, mx, sh);
+  float inv = 1.f;
+  if (r.norm) {
+    inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[gi][e] = y[gi][e] * inv;
+  }
+  float amax = mx * inv;
+  if (GAM) {
+    float gm = 0.f;
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[gi][e] = y[gi][e] * R.g[gi][e];
+        gm = fmaxf(gm, fabsf(y[gi][e]));
+      }
+    float dummy = 0.f;
+    block_sum_max<NT>(dummy, gm, sh);
+    amax = gm;
+  } else {
+    // mx * inv can round below the largest |y * inv|; one ulp of headroom
+    amax = amax * (1.0f + 1.0f / 4194304.0f);
+  }
+  const int s = row_shift(amax);
+  const float mul = ldexpf(1.0f, s);
+  long long xs = 0;
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const int q = (int)threadIdx.x + gi * NT;
+    if (q >= nq) continue;
+    if (writer) {
+      const size_t o = (size_t)m * K + 8 * q;
+      if (r.y_out) {
+        *reinterpret_cast<float4 *>(r.y_out + o) = float4{y[gi][0], y[gi][1], y[gi][2], y[gi][3]};
+        *reinterpret_cast<float4 *>(r.y_out + o + 4) = float4{y[gi][4], y[gi][5], y[gi][6], y[gi][7]};
+      }
+      if (r.x_out) {
+        *reinterpret_cast<float4 *>(r.x_out + o) =
+            float4{R.v[gi][0], R.v[gi][1], R.v[gi][2], R.v[gi][3]};
+        *reinterpret_cast<float4 *>(r.x_out + o + 4) =
+            float4{R.v[gi][4], R.v[gi][5], R.v[gi][6], R.v[gi][7]};
+      }
+    }
+    uint32_t lo[4], hi[4];
+    xs += quant8(y[gi], mul, lo, hi);
+    const int pos = limb_pos8(8 * q);
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+      *reinterpret_cast<uint2 *>(dst + (size_t)(4 * m + l) * ld_dst + pos) = uint2{lo[l], hi[l]};
+  }
+  *s_out = s;
+  *xs_wave = wave_sum_d((double)xs);  // |sum| < 2^44: exact in double
+}
+
+template <bool GAM>
+__global__ __launch_bounds__(1024) void k_quant_rows(RowSrc r, int K, QuantRows q) {
+  __shared__ float sh[32];
+  __shared__ double shd[16];
+  RowRegs<1024, 2, GAM> R;
+  const int m = blockIdx.x;
+  row_load<1024, 2, GAM>(r, K, m, R);
+  int s;
+  double xw;
+  row_finish<1024, 2, GAM>(r, K, m, true, R, q.limbs, K, sh, &s, &xw);
+  if ((threadIdx.x & 63) == 0) shd[threadIdx.x >> 6] = xw;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < 16; ++w) t += shd[w];
+    q.shift[m] = s;
+    q.xsum[m] = (long long)t;
+  }
+}
+
+size_t quant_rows_bytes(int M, int K) {
+  return (size_t)4 * M * K + (size_t)M * 4 + 64 + (size_t)M * 8 + 64;
+}
+
+QuantRows quant_rows_view(void *buf, int M, int K) {
+  QuantRows q;
+  uint8_t *b = static_cast<uint8_t *>(buf);
+  q.limbs = reinterpret_cast<int8_t *>(b);
+  const size_t o1 = ((size_t)4 * M * K + 63) & ~(size_t)63;
+  q.shift = reinterpret_cast<int32_t *>(b + o1);
+  const size_t o2 = (o1 + (size_t)M * 4 + 63) & ~(size_t)63;
+  q.xsum = reinterpret_cast<long long *>(b + o2);
+  return q;
+}
+
+int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st) {
+  MS_CHECK_ARG(M >= 1 && K >= 8 && K % 8 == 0 && K <= kQuantMaxK,
+               "quant: row length must be a multiple of 8 in [8, 16384]");
+  MS_CHECK_ARG(r.x && r.ld >= K && q.limbs && q.shift && q.xsum, "quant: missing buffers");
+  if (r.gamma)
+    hipLaunchKernelGGL(k_quant_rows<true>, dim3(M), dim3(1024), 0, st, r, K, q);
+  else
+    hipLaunchKernelGGL(k_quant_rows<false>, dim3(M), dim3(1024), 0, st, r, K, q);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }
 
 // ------------------------------------------------------------------------------
-// MFMA GEMV
+// MFMA GEMV: v_mfma_i32_16x16x64_i8 with the activation limbs as A (rows
+// 4m + l) and the weight nibbles as B (16 columns of one panel).
 // ------------------------------------------------------------------------------
-__device__ inline uint32_t and_or(uint32_t d, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(d), "s"(m), "v"(c));
-  return r;
-}
 
-__device__ inline half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
-
-// 8 nibbles -> 8 exact fp16 values (nibble - 8) in MFMA element order.
-// fp16 1024 + n has n in the low mantissa bits, so the nibble is OR-ed into
-// 0x6400 (bits 0-3: n, bits 4-7: 16n) and an exact fp16 add/FMA removes the
-// offset.  fp16 has 10 mantissa bits, hence the >> 8 for the upper nibbles.
-__device__ inline half8_t q4_to_half8(uint32_t d, uint32_t magic) {
-  const uint32_t d8 = d >> 8;
-  half2_t v0 = as_h2(and_or(d, 0x000F000Fu, magic));   // 1024 + n
-  half2_t v1 = as_h2(and_or(d, 0x00F000F0u, magic));   // 1024 + 16 n
-  half2_t v2 = as_h2(and_or(d8, 0x000F000Fu, magic));
-  half2_t v3 = as_h2(and_or(d8, 0x00F000F0u, magic));
-  v0 = v0 + (half2_t)(-1032.0f16);
-  v1 = __builtin_elementwise_fma(v1, (half2_t)(0.0625f16), (half2_t)(-72.0f16));
-  v2 = v2 + (half2_t)(-1032.0f16);
-  v3 = __builtin_elementwise_fma(v3, (half2_t)(0.0625f16), (half2_t)(-72.0f16));
-  return half8_t{v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
-}
-
-__device__ inline half8_t load_h8(const _Float16 *p) {
-  return *reinterpret_cast<const half8_t *>(p);
-}
-
-// Resolve panel slot p of panel group pg.
-__device__ inline void gemv_slot(const GemvArgs &a, int pg, int p,
-                                 const uint8_t **w, float *scale, int *col) {
-  if (a.epi == EPI_SWIGLU) {
+// Resolve panel slot p of panel group pg with selects only (no loop over the
+// argument struct: every launch parameter is read in one batch at kernel
+// entry).  Segment fields arrive as separate scalars.  Slots past the last
+// segment get segment 0's first panel (a valid address, so every load stays
+// a global load) and valid = false; their results are dropped.
+template <int EPI>
+__device__ inline void gemv_slot(const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                 float s0, float s1, float s2, int n0, int n1, int n2, int c0,
+                                 int c1, int c2, int K, int P, int pg, int p,
+                                 const uint8_t **w, float *scale, int *col, bool *valid) {
+  if constexpr (EPI == EPI_SWIGLU) {
     // paired mode: slot p comes from segment p (gate, up), same panel pg
-    const GemvSeg &sg = a.seg[p];
-    *w = sg.w + (size_t)pg * a.K * 8;
-    *scale = sg.scale;
+    *w = (p == 0 ? w0 : w1) + (size_t)pg * K * 8;
+    *scale = p == 0 ? s0 : s1;
     *col = pg * 16;
-    return;
+    *valid = true;
+  } else {
+    const int panel = pg * P + p;
+    const int si = panel < n0 ? 0 : (panel < n0 + n1 ? 1 : 2);
+    const int loc = panel - (si == 0 ? 0 : (si == 1 ? n0 : n0 + n1));
+    const bool ok = panel < n0 + n1 + n2;
+    const uint8_t *base = si == 0 ? w0 : (si == 1 ? w1 : w2);
+    const float sc = si == 0 ? s0 : (si == 1 ? s1 : s2);
+    const int cc = si == 0 ? c0 : (si == 1 ? c1 : c2);
+    *w = ok ? base + (size_t)loc * K * 8 : w0;
+    *scale = ok ? sc : 0.f;
+    *col = ok ? cc + loc * 16 : 0;
+    *valid = ok;
   }
-  int panel = pg * a.P + p;
-  for (int si = 0; si < a.nseg; ++si) {
-    const GemvSeg &sg = a.seg[si];
-    const int np = sg.n_cols / 16;
-    if (panel < np) {
-      *w = sg.w + (size_t)panel * a.K * 8;
-      *scale = sg.scale;
-      *col = sg.out_col0 + panel * 16;
-      return;
-    }
-    panel -= np;
-  }
-  *w = nullptr;
-  *scale = 0.f;
-  *col = 0;
 }
 
-// D fragment index of output row i, column j (v_mfma_f32_16x16x* layout:
+// D fragment index of output row i, column j (v_mfma_*_16x16x* layout:
 // lane j + 16*(i/4), element i%4).
 __device__ inline int dfrag(int i, int j) { return (j + 16 * (i >> 2)) * 4 + (i & 3); }
 
-// LDS bytes of the GEMV for a given configuration.
-__host__ __device__ inline size_t gemv_lds_bytes(int waves, int P, int M, int ks, bool prep) {
-  size_t b = ((size_t)waves * P * 256 + (size_t)P * M * 16) * 4;
-  if (prep) b += (size_t)2 * M * (ks + 8) * 2;
-  return b;
+// Super-tiles each wave keeps in flight per batch: A fragments of a global-A
+// GEMV live in registers next to the weights, so it holds fewer.
+template <int C, int P, int AS>
+constexpr int gemv_batch() {
+  constexpr int u = (AS == AS_QUANT ? 4 / C : 8 / C) / P;
+  return u < 1 ? 1 : u;
 }
 
-// MODE 0: M <= 8, hi rows 0..M-1 and lo rows M..2M-1 share one MFMA.
-// MODE 1: M <= 16, separate hi and lo MFMAs.
-// PREP: activations built by the block in LDS (PrepArgs).
-template <int MODE, int P, bool PREP>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
-  extern __shared__ float red[];  // [waves][P][256], vals [P][M][16], A hi/lo
-  __shared__ float sh[16];
-  constexpr int U = (MODE == 0) ? 4 : 2;  // super-tiles in flight per wave
-  const int W = a.waves;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int KG = a.K / kSuperK;
-  const int s = blockIdx.x % a.S;
-  const int pg = blockIdx.x / a.S;
-  const int G0 = (int)((long)KG * s / a.S), G1 = (int)((long)KG * (s + 1) / a.S);
-  const int M = a.M;
+// LDS layout: int partial sums [W][P][C][256], output values [P][M][16],
+// per-row shift and sum, then (AS_ROWS) limb rows [4M][K + 16].
+__host__ __device__ inline size_t gemv_lds_red(int W, int P, int C) {
+  return (size_t)W * P * C * 256 * 4;
+}
+__host__ __device__ inline size_t gemv_lds_fixed(int W, int P, int C, int M) {
+  // + per row: shift (int) and W partial sums (double); + per row scale (double)
+  return gemv_lds_red(W, P, C) + (size_t)P * M * 16 * 4 + (size_t)kGemvMaxM * 4 +
+         (size_t)kGemvMaxM * 16 * 8 + (size_t)kGemvMaxM * 8;
+}
+__host__ __device__ inline int gemv_ldl(int K) { return K + 16; }
 
-  const uint8_t *wp[P];
+// 8-row groups per thread in the row prologue: K <= 8 * rows_ng(W) * 64 * W.
+__host__ __device__ constexpr int rows_ng(int W) { return (void)W, 2; }
+
+// C: 16-row MFMA groups (4 limb rows per activation row: M <= 4C).
+// P: panels per block.  AS: GemvASource.  W: waves per block.  EPI: epilogue.
+//
+// Block pg = P panels of 16 columns over the whole K.  Wave w owns super-tiles
+// w, w+W, ...; each batch issues U of them (P panels each) before any is
+// consumed, and the first batch is issued before the prologue so that the
+// weight stream overlaps the activation quantization.
+template <int C, int P, int AS, int W, int EPI>
+__global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ float sh[32];
+  constexpr int NT = 64 * W;
+  constexpr int U = gemv_batch<C, P, AS>();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Every launch parameter the kernel uses is read here, in one batch: uses
+  // further down would otherwise become dependent argument loads.
+  const int K = launder(a.K), M = launder(a.M);
+  const int nseg = launder(a.nseg);
+  const uint8_t *sw0 = launder(a.seg[0].w), *sw1 = launder(a.seg[1].w),
+                *sw2 = launder(a.seg[2].w);
+  const float ss0 = launder(a.seg[0].scale), ss1 = launder(a.seg[1].scale),
+              ss2 = launder(a.seg[2].scale);
+  const int sn0 = launder(a.seg[0].n_cols) >> 4;
+  const int sn1 = nseg > 1 ? launder(a.seg[1].n_cols) >> 4 : 0;
+  const int sn2 = nseg > 2 ? launder(a.seg[2].n_cols) >> 4 : 0;
+  const int sc0 = launder(a.seg[0].out_col0), sc1 = launder(a.seg[1].out_col0),
+            sc2 = launder(a.seg[2].out_col0);
+  const int ldo = launder(a.ldo);
+  float *out = launder(a.out);
+  const float *resid = (EPI == EPI_RESID) ? launder(a.resid) : nullptr;
+  float *out2 = (EPI == EPI_RESID) ? launder(a.out2) : nullptr;
+  float *sw_out = (EPI == EPI_SWIGLU) ? launder(a.sw_out) : nullptr;
+  const int ldo_sw = (EPI == EPI_SWIGLU) ? launder(a.ldo_sw) : 0;
+  float *arg_val = (EPI == EPI_ARGMAX) ? launder(a.arg_val) : nullptr;
+  int32_t *arg_idx = (EPI == EPI_ARGMAX) ? launder(a.arg_idx) : nullptr;
+  RowSrc rs{};
+  QuantRows qr{};
+  if (AS == AS_ROWS) {
+    rs.x = launder(a.rows.x);
+    rs.ld = launder(a.rows.ld);
+    rs.pre_scale = launder(a.rows.pre_scale);
+    rs.norm = launder(a.rows.norm);
+    rs.y_out = launder(a.rows.y_out);
+    rs.x_out = launder(a.rows.x_out);
+  } else {
+    qr.limbs = launder(a.q.limbs);
+    qr.shift = launder(a.q.shift);
+    qr.xsum = launder(a.q.xsum);
+  }
+
+  const int KG = K / kSuperK;
+  const int pg = blockIdx.x;
+  const int nb = ((KG + W - 1) / W + U - 1) / U;  // batches (block-uniform)
+
+  const uint8_t *wl[P];
   float wsc[P];
   int col[P];
+  bool wv[P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) gemv_slot(a, pg, p, &wp[p], &wsc[p], &col[p]);
+  for (int p = 0; p < P; ++p)
+    gemv_slot<EPI>(sw0, sw1, sw2, ss0, ss1, ss2, sn0, sn1, sn2, sc0, sc1, sc2, K, P, pg, p,
+                   &wl[p], &wsc[p], &col[p], &wv[p]);
 
-  const int ks = (G1 - G0) * kSuperK;
-  const int ldl = ks + 8;
-  _Float16 *lds_hi = reinterpret_cast<_Float16 *>(red + (size_t)W * P * 256 + P * M * 16);
-  _Float16 *lds_lo = lds_hi + (size_t)M * ldl;
+  int32_t *red = reinterpret_cast<int32_t *>(lds);
+  float *vals = reinterpret_cast<float *>(lds + gemv_lds_red(W, P, C));
+  int32_t *row_s = reinterpret_cast<int32_t *>(lds + gemv_lds_red(W, P, C) + (size_t)P * M * 64);
+  double *row_xs = reinterpret_cast<double *>(row_s + kGemvMaxM);  // [kGemvMaxM][16]
+  int8_t *limbs = reinterpret_cast<int8_t *>(lds + gemv_lds_fixed(W, P, C, M));
+  const int ldl = gemv_ldl(K);
 
-  if (PREP) {
-    const int k0 = G0 * kSuperK;
-    for (int m = 0; m < M; ++m)
-      prep_row(a.prep, a.K, m, blockIdx.x == 0, k0, ks, lds_hi, lds_lo, ldl, nullptr, nullptr,
-               sh);
-    __syncthreads();
-  }
-
-  // A-fragment source rows for this lane (row i of the 16-row MFMA operand)
+  // A operand of this lane: row i of MFMA group c is limb row 16c + i
   const int i = lane & 15, g = lane >> 4;
-  const _Float16 *arow = nullptr, *arow_lo = nullptr;
-  int astride = 0;  // offset of super-tile G relative to its base, in halves
-  if (PREP) {
-    if (MODE == 0) {
-      if (i < M) arow = lds_hi + (size_t)i * ldl;
-      else if (i < 2 * M) arow = lds_lo + (size_t)(i - M) * ldl;
-    } else if (i < M) {
-      arow = lds_hi + (size_t)i * ldl;
-      arow_lo = lds_lo + (size_t)i * ldl;
-    }
-    astride = -G0 * kSuperK;
-  } else {
-    if (MODE == 0) {
-      if (i < M) arow = a.a_hi + (size_t)i * a.lda;
-      else if (i < 2 * M) arow = a.a_lo + (size_t)(i - M) * a.lda;
-    } else if (i < M) {
-      arow = a.a_hi + (size_t)i * a.lda;
-      arow_lo = a.a_lo + (size_t)i * a.lda;
-    }
-  }
-  uint32_t magic;
-  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
-
-  float4_t acc[P];
+  bool a_on[C];
 #pragma unroll
-  for (int p = 0; p < P; ++p) acc[p] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < C; ++c) a_on[c] = 16 * c + i < 4 * M;
 
-  for (int G = G0 + wave; G < G1; G += U * W) {
-    uint4 q[U][P];
-    half8_t af[U][4];
-    half8_t afl[MODE == 1 ? U : 1][4];
+  uint4 q[U][P];
+  v4i af[AS == AS_QUANT ? U : 1][C][2];
+  auto issue = [&](int bt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int Gu = G + u * W;
-      if (Gu < G1) {
+      const int Gu = min(wave + (bt * U + u) * W, KG - 1);
 #pragma unroll
-        for (int p = 0; p < P; ++p)
-          q[u][p] = *reinterpret_cast<const uint4 *>(wp[p] + (size_t)Gu * 1024 + lane * 16);
-        const int kofs = Gu * kSuperK + astride + 32 * g;
+      for (int p = 0; p < P; ++p) {
+        const u32x4 v = ldg<u32x4>(wl[p] + (size_t)Gu * 1024 + lane * 16);
+        q[u][p] = uint4{v.x, v.y, v.z, v.w};
+      }
+      if constexpr (AS == AS_QUANT) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          af[u][t] = arow ? load_h8(arow + kofs + 8 * t) : half8_t{};
-          if (MODE == 1) afl[u][t] = arow_lo ? load_h8(arow_lo + kofs + 8 * t) : half8_t{};
+        for (int c = 0; c < C; ++c) {
+          af[u][c][0] = v4i{0, 0, 0, 0};
+          af[u][c][1] = v4i{0, 0, 0, 0};
+          if (a_on[c]) {
+            const int8_t *ar = qr.limbs + (size_t)(16 * c + i) * K + Gu * 128 + 32 * g;
+            af[u][c][0] = ldg<v4i>(ar);
+            af[u][c][1] = ldg<v4i>(ar + 16);
+          }
         }
       }
     }
+  };
+
+  // ---- prologue: activation limbs, overlapping the first weight batch
+  // row_xs[m][w]: wave w's part of sum X for row m (AS_QUANT: the whole sum in w = 0)
+  if constexpr (AS == AS_ROWS) {
+    RowRegs<NT, rows_ng(W), false> R;
+    row_load<NT, rows_ng(W), false>(rs, K, 0, R);
+    issue(0);
+    int s;
+    double xw;
+    row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s, &xw);
+    if (lane == 0) row_xs[wave] = xw;
+    if (threadIdx.x == 0) row_s[0] = s;
+    for (int m = 1; m < M; ++m) {
+      row_load<NT, rows_ng(W), false>(rs, K, m, R);
+      row_finish<NT, rows_ng(W), false>(rs, K, m, blockIdx.x == 0, R, limbs, ldl, sh, &s, &xw);
+      if (lane == 0) row_xs[m * 16 + wave] = xw;
+      if (threadIdx.x == 0) row_s[m] = s;
+    }
+    __syncthreads();
+  } else {
+    if ((int)threadIdx.x < M) {
+      row_s[threadIdx.x] = ldg<int32_t>(qr.shift + threadIdx.x);
+      row_xs[threadIdx.x * 16] = (double)ldg<long long>(qr.xsum + threadIdx.x);
+    }
+    issue(0);
+  }
+
+  v4i acc[P][C];
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[p][c] = v4i{0, 0, 0, 0};
+
+  for (int bt = 0; bt < nb; ++bt) {
+    if (bt > 0) issue(bt);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int Gu = G + u * W;
-      if (Gu < G1) {
+      const int Gu = wave + (bt * U + u) * W;
+      if (Gu < KG) {
+        v4i al[C][2];
+        if constexpr (AS == AS_ROWS) {
+#pragma unroll
+          for (int c = 0; c < C; ++c) {
+            al[c][0] = v4i{0, 0, 0, 0};
+            al[c][1] = v4i{0, 0, 0, 0};
+            if (a_on[c]) {
+              const int8_t *ar = limbs + (size_t)(16 * c + i) * ldl + Gu * 128 + 32 * g;
+              al[c][0] = *reinterpret_cast<const v4i *>(ar);
+              al[c][1] = *reinterpret_cast<const v4i *>(ar + 16);
+            }
+          }
+        }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
           const uint32_t dw[4] = {q[u][p].x, q[u][p].y, q[u][p].z, q[u][p].w};
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const half8_t b = q4_to_half8(dw[t], magic);
-            acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[u][t], b, acc[p], 0, 0, 0);
-            if (MODE == 1)
-              acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afl[u][t], b, acc[p], 0, 0, 0);
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t d0 = dw[2 * h], d1 = dw[2 * h + 1];
+            const v4i b = v4i{(int)(d0 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu),
+                              (int)(d1 & 0x0F0F0F0Fu), (int)((d1 >> 4) & 0x0F0F0F0Fu)};
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+              const v4i av = (AS == AS_QUANT) ? af[u][c][h] : al[c][h];
+              acc[p][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b, acc[p][c], 0, 0, 0);
+            }
           }
         }
       }
@@ -407,63 +646,82 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   }
 
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    float *r = red + ((size_t)wave * P + p) * 256 + lane * 4;
-    r[0] = acc[p][0];
-    r[1] = acc[p][1];
-    r[2] = acc[p][2];
-    r[3] = acc[p][3];
-  }
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      int32_t *r = red + (((size_t)wave * P + p) * C + c) * 256 + lane * 4;
+      *reinterpret_cast<v4i *>(r) = acc[p][c];
+    }
   __syncthreads();
 
-  // reduce over waves: value of (slot p, row m, column j) -> vals[p][m][j]
-  const int n_out = P * M * 16;
-  float *vals = red + (size_t)W * P * 256;
-  for (int o = threadIdx.x; o < n_out; o += blockDim.x) {
-    const int p = o / (M * 16), m = (o / 16) % M, j = o % 16;
-    float v = 0.f;
-    for (int w = 0; w < W; ++w) {
-      const float *r = red + ((size_t)w * P + p) * 256;
-      v += r[dfrag(m, j)];
-      if (MODE == 0) v += r[dfrag(m + M, j)];
+  // output (slot p, row m, column j): sum the waves per limb row (exact int32),
+  // combine the limbs and the -8 offset in int64, scale once.  Loops over the
+  // slot are unrolled so every per-slot value is a compile-time index.
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    for (int o = threadIdx.x; o < M * 16; o += NT) {
+      const int m = o >> 4, j = o & 15;
+      const int c = m >> 2, r0 = 4 * (m & 3);
+      long long t = 0;
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        int d = 0;
+        for (int w = 0; w < W; ++w)
+          d += red[(((size_t)w * P + p) * C + c) * 256 + dfrag(r0 + l, j)];
+        t += (long long)d << (8 * l);
+      }
+      double xs = row_xs[m * 16];
+      if (AS == AS_ROWS)
+        for (int w = 1; w < W; ++w) xs += row_xs[m * 16 + w];
+      t -= 8 * (long long)xs;
+      vals[p * M * 16 + o] = (float)((double)t * (double)ldexpf(1.0f, -row_s[m]) * (double)wsc[p]);
     }
-    vals[o] = v * (wsc[p] * a.out_mul);
-  }
   __syncthreads();
 
-  if (a.epi == EPI_STORE || a.epi == EPI_ACCUMULATE) {
-    for (int o = threadIdx.x; o < n_out; o += blockDim.x) {
-      const int p = o / (M * 16), m = (o / 16) % M, j = o % 16;
-      if (!wp[p]) continue;
-      if (a.epi == EPI_STORE)
-        a.out[(size_t)s * a.split_stride + (size_t)m * a.ldo + col[p] + j] = vals[o];
-      else
-        a.out[(size_t)m * a.ldo + col[p] + j] += vals[o];
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ACCUMULATE || EPI == EPI_RESID) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if (!wv[p]) continue;
+      for (int o = threadIdx.x; o < M * 16; o += NT) {
+        const int m = o >> 4, j = o & 15;
+        const size_t oi = (size_t)m * ldo + col[p] + j;
+        const float v = vals[p * M * 16 + o];
+        if constexpr (EPI == EPI_STORE) {
+          out[oi] = v;
+        } else if constexpr (EPI == EPI_ACCUMULATE) {
+          out[oi] += v;
+        } else {
+          // x = x + proj (gemma4_e4b.mojo:522,538)
+          const float x = resid[oi] + v;
+          out[oi] = x;
+          if (out2) out2[oi] = x;
+        }
+      }
     }
-  } else if (a.epi == EPI_SWIGLU) {
+  } else if constexpr (EPI == EPI_SWIGLU) {
     // slot 0 = gate, slot 1 = up (same columns): swiglu_inplace
     // (kernels.mojo:519-532) fused into the producer.
-    for (int o = threadIdx.x; o < M * 16; o += blockDim.x) {
-      const int m = o / 16, j = o % 16;
+    for (int o = threadIdx.x; o < M * 16; o += NT) {
+      const int m = o >> 4, j = o & 15;
       const float gt = vals[o], up = vals[M * 16 + o];
       const float y = up * gt * (1.0f / (1.0f + expf(-gt)));
-      const size_t idx = (size_t)m * a.ldo_sw + col[0] + j;
-      if (a.out) a.out[(size_t)m * a.ldo + col[0] + j] = y;
-      _Float16 h, l;
-      split_hi_lo(y * a.sw_prescale, &h, &l);
-      a.sw_hi[idx] = h;
-      a.sw_lo[idx] = l;
+      sw_out[(size_t)m * ldo_sw + col[0] + j] = y;
     }
-  } else if (a.epi == EPI_ARGMAX) {
+  } else if constexpr (EPI == EPI_ARGMAX) {
     // logits (optional) and the block's first index of the maximum per row
-    for (int o = threadIdx.x; o < n_out; o += blockDim.x) {
-      const int p = o / (M * 16), m = (o / 16) % M, j = o % 16;
-      if (a.out) a.out[(size_t)m * a.ldo + col[p] + j] = vals[o];
+    if (out) {
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        for (int o = threadIdx.x; o < M * 16; o += NT) {
+          const int m = o >> 4, j = o & 15;
+          out[(size_t)m * ldo + col[p] + j] = vals[p * M * 16 + o];
+        }
     }
     if ((int)threadIdx.x < M) {
       const int m = threadIdx.x;
       float bv = -INFINITY;
       int bi = 0x7fffffff;
+#pragma unroll
       for (int p = 0; p < P; ++p)
         for (int j = 0; j < 16; ++j) {
           const float v = vals[(p * M + m) * 16 + j];
@@ -473,8 +731,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             bi = idx;
           }
         }
-      a.arg_val[(size_t)blockIdx.x * M + m] = bv;
-      a.arg_idx[(size_t)blockIdx.x * M + m] = bi;
+      arg_val[(size_t)blockIdx.x * M + m] = bv;
+      arg_idx[(size_t)blockIdx.x * M + m] = bi;
     }
   }
 }
@@ -487,7 +745,7 @@ __global__ __launch_bounds__(1024) void k_argmax_fin(ArgmaxFin f) {
   for (int m = 0; m < f.M; ++m) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int b = threadIdx.x; b < f.n_blocks; b += blockDim.x) {
+    for (int b = threadIdx.x; b < f.n_blocks; b += 1024) {
       const float v = f.arg_val[(size_t)b * f.M + m];
       const int idx = f.arg_idx[(size_t)b * f.M + m];
       if (v > bv || (v == bv && idx < bi)) {
@@ -498,7 +756,7 @@ __global__ __launch_bounds__(1024) void k_argmax_fin(ArgmaxFin f) {
     sv[threadIdx.x] = bv;
     si[threadIdx.x] = bi;
     __syncthreads();
-    for (int o = blockDim.x / 2; o > 0; o >>= 1) {
+    for (int o = 512; o > 0; o >>= 1) {
       if ((int)threadIdx.x < o) {
         const float v = sv[threadIdx.x + o];
         const int idx = si[threadIdx.x + o];
@@ -527,66 +785,71 @@ int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st) {
   return MS_OK;
 }
 
+size_t gemv_lds_need(const GemvArgs &a) {
+  const int C = a.M <= 4 ? 1 : 4;
+  size_t b = gemv_lds_fixed(a.waves, a.P, C, a.M);
+  if (a.asrc == AS_ROWS) b += (size_t)4 * a.M * gemv_ldl(a.K);
+  return b;
+}
+
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
-  MS_CHECK_ARG(a.M >= 1 && a.M <= 16, "GEMV: 1 <= M <= 16");
-  MS_CHECK_ARG(a.K % kSuperK == 0, "GEMV: K % 128 != 0");
-  MS_CHECK_ARG(a.waves == 4, "GEMV: 4 waves per block");
-  MS_CHECK_ARG(a.S >= 1 && a.S <= a.K / kSuperK, "GEMV: bad K split");
-  MS_CHECK_ARG(a.epi != EPI_ACCUMULATE || a.S == 1, "GEMV: accumulate needs S=1");
-  MS_CHECK_ARG(a.epi != EPI_SWIGLU || (a.S == 1 && a.P == 2 && a.nseg == 2),
-               "GEMV: SwiGLU epilogue needs S=1, P=2, two segments");
-  MS_CHECK_ARG(a.epi != EPI_ARGMAX || (a.S == 1 && a.arg_val && a.arg_idx),
-               "GEMV: argmax epilogue needs S=1 and block-max buffers");
+  MS_CHECK_ARG(a.M >= 1 && a.M <= kGemvMaxM, "GEMV: 1 <= M <= 16");
+  MS_CHECK_ARG(a.K >= kSuperK && a.K % kSuperK == 0, "GEMV: K % 128 != 0");
+  MS_CHECK_ARG(a.asrc == AS_ROWS || a.asrc == AS_QUANT, "GEMV: bad activation source");
+  MS_CHECK_ARG(a.nseg >= 1 && a.nseg <= 3, "GEMV: 1 to 3 segments");
+  MS_CHECK_ARG(a.epi != EPI_RESID || (a.resid && a.out), "GEMV: residual epilogue needs rows");
+  MS_CHECK_ARG(a.epi != EPI_SWIGLU || (a.P == 2 && a.nseg == 2 && a.sw_out),
+               "GEMV: SwiGLU epilogue needs P=2, two segments and an output");
+  MS_CHECK_ARG(a.epi != EPI_ARGMAX || (a.arg_val && a.arg_idx),
+               "GEMV: argmax epilogue needs block-max buffers");
+  MS_CHECK_ARG(a.epi == EPI_ARGMAX || a.epi == EPI_SWIGLU || a.out, "GEMV: missing output");
+  if (a.asrc == AS_ROWS) {
+    MS_CHECK_ARG(a.rows.x && a.rows.ld >= a.K && !a.rows.gamma,
+                 "GEMV: row prologue needs rows (no gamma)");
+    MS_CHECK_ARG(a.K <= 8 * rows_ng(a.waves) * 64 * a.waves, "GEMV: row prologue: row too long");
+  } else {
+    MS_CHECK_ARG(a.q.limbs && a.q.shift && a.q.xsum, "GEMV: quantized rows missing");
+  }
   long n_panels = 0;
   for (int i = 0; i < a.nseg; ++i) {
-    MS_CHECK_ARG(a.seg[i].n_cols % 16 == 0, "GEMV: segment width % 16 != 0");
+    MS_CHECK_ARG(a.seg[i].w && a.seg[i].n_cols > 0 && a.seg[i].n_cols % 16 == 0,
+                 "GEMV: segment width % 16 != 0");
     n_panels += a.seg[i].n_cols / 16;
     if (a.epi != EPI_SWIGLU)
       MS_CHECK_ARG((a.seg[i].n_cols / 16) % a.P == 0,
                    "GEMV: panels per block must divide every segment");
   }
-  const long groups = (a.epi == EPI_SWIGLU) ? a.seg[0].n_cols / 16 : n_panels / a.P;
-  const long blocks = groups * a.S;
-  const int KG = a.K / kSuperK;
-  const int ks_max = ((KG + a.S - 1) / a.S) * kSuperK;
-  const bool prep = a.prep.on != 0;
-  const size_t shmem = gemv_lds_bytes(a.waves, a.P, a.M, ks_max, prep);
-  MS_CHECK_ARG(shmem <= 160 * 1024 - 256, "GEMV: LDS budget exceeded (use the prep kernel)");
-  MS_CHECK_ARG(!prep || a.K <= kPrepMaxPer * 64 * a.waves, "GEMV: prologue row too long");
-  const bool packed = a.M <= 8;
-#define MS_GEMV_CASE(MODE, PP, PR)                                                \
-  hipLaunchKernelGGL((k_gemv<MODE, PP, PR>), dim3(blocks), dim3(64 * a.waves), shmem, \
-                     st, a)
-#define MS_GEMV_P(MODE, PR)                                                       \
-  switch (a.P) {                                                                   \
-    case 1: MS_GEMV_CASE(MODE, 1, PR); break;                                      \
-    case 2: MS_GEMV_CASE(MODE, 2, PR); break;                                      \
-    case 4: MS_GEMV_CASE(MODE, 4, PR); break;                                      \
-    default: return fail(MS_E_INVALID, "GEMV: P must be 1, 2 or 4");               \
+  if (a.epi == EPI_SWIGLU)
+    MS_CHECK_ARG(a.seg[0].n_cols == a.seg[1].n_cols, "GEMV: gate/up widths differ");
+  const long blocks = (a.epi == EPI_SWIGLU) ? a.seg[0].n_cols / 16 : n_panels / a.P;
+  const size_t shmem = gemv_lds_need(a);
+  MS_CHECK_ARG(shmem <= 160 * 1024 - 1024, "GEMV: LDS budget exceeded");
+  const int C = a.M <= 4 ? 1 : 4;
+  bool ok = false;
+  // Supported (epilogue, panels per block, activation source, waves).
+#define MS_GEMV_L(CC, EP, PP, AS, WW) \
+  hipLaunchKernelGGL((k_gemv<CC, PP, AS, WW, EP>), dim3(blocks), dim3(64 * WW), shmem, st, a)
+#define MS_GEMV(EP, PP, AS, WW)                                                   \
+  if (!ok && a.epi == EP && a.P == PP && a.asrc == AS && a.waves == WW) {        \
+    if (C == 1) MS_GEMV_L(1, EP, PP, AS, WW);                                     \
+    else MS_GEMV_L(4, EP, PP, AS, WW);                                            \
+    ok = true;                                                                    \
   }
-  if (packed) {
-    if (prep) { MS_GEMV_P(0, true) } else { MS_GEMV_P(0, false) }
-  } else {
-    if (prep) { MS_GEMV_P(1, true) } else { MS_GEMV_P(1, false) }
-  }
-#undef MS_GEMV_P
-#undef MS_GEMV_CASE
-  MS_HIP_TRY(hipGetLastError());
-  return MS_OK;
-}
-
-__global__ void k_sum_parts(float *__restrict__ out, const float *__restrict__ parts,
-                            int S, size_t n) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float v = parts[i];
-  for (int s = 1; s < S; ++s) v = v + parts[(size_t)s * n + i];
-  out[i] = v;
-}
-
-int launch_sum_parts(float *out, const float *parts, int S, size_t n, hipStream_t st) {
-  hipLaunchKernelGGL(k_sum_parts, dim3(cdiv((long)n, 256)), dim3(256), 0, st, out, parts,
-                     S, n);
+  MS_GEMV(EPI_STORE, 1, AS_ROWS, 8)
+  MS_GEMV(EPI_STORE, 1, AS_QUANT, 4)
+  MS_GEMV(EPI_STORE, 4, AS_QUANT, 4)
+  MS_GEMV(EPI_ACCUMULATE, 1, AS_QUANT, 4)
+  MS_GEMV(EPI_ACCUMULATE, 4, AS_QUANT, 4)
+  MS_GEMV(EPI_RESID, 1, AS_ROWS, 4)
+  MS_GEMV(EPI_RESID, 1, AS_ROWS, 16)
+  MS_GEMV(EPI_RESID, 1, AS_QUANT, 4)
+  MS_GEMV(EPI_SWIGLU, 2, AS_ROWS, 8)
+  MS_GEMV(EPI_SWIGLU, 2, AS_ROWS, 4)
+  MS_GEMV(EPI_SWIGLU, 2, AS_QUANT, 4)
+  MS_GEMV(EPI_ARGMAX, 4, AS_QUANT, 4)
+#undef MS_GEMV
+#undef MS_GEMV_L
+  MS_CHECK_ARG(ok, "GEMV: unsupported (epilogue, P, waves, activation source) combination");
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }
@@ -598,7 +861,7 @@ int pack_device(uint8_t *dst, const uint8_t *src, int K, int N, hipStream_t st) 
   int rc = check_q4_shape(K, N);
   if (rc) return rc;
   const size_t total = (size_t)K * N / 8;
-  hipLaunchKernelGGL(k_pack, dim3(cdiv((long)total, 256)), dim3(256), 0, st,
+  hipLaunchKernelGGL(k_pack, dim3(cdiv((long)total, kBlock)), dim3(kBlock), 0, st,
                      reinterpret_cast<uint32_t *>(dst), src, K, N);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -643,7 +906,7 @@ extern "C" int ms_dequant_q4(float *d_out, const uint8_t *d_rowmajor, int K, int
   if (int rc = require_init()) return rc;
   MS_CHECK_ARG(K > 0 && N > 0 && N % 2 == 0, "dequant: bad shape");
   const size_t nbytes = (size_t)K * N / 2;
-  hipLaunchKernelGGL(k_dequant_rowmajor, dim3(cdiv((long)nbytes, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(k_dequant_rowmajor, dim3(cdiv((long)nbytes, kBlock)), dim3(kBlock), 0,
                      ctx().stream, d_out, d_rowmajor, nbytes, scale);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
@@ -654,7 +917,7 @@ extern "C" int ms_dequant_q4_packed(float *d_out, const uint8_t *d_packed, int K
   if (int rc = require_init()) return rc;
   if (int rc = check_q4_shape(K, N)) return rc;
   const size_t total = (size_t)K * N / 8;
-  hipLaunchKernelGGL(k_dequant_packed, dim3(cdiv((long)total, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(k_dequant_packed, dim3(cdiv((long)total, kBlock)), dim3(kBlock), 0,
                      ctx().stream, d_out, reinterpret_cast<const uint32_t *>(d_packed),
                      K, N, scale);
   MS_HIP_TRY(hipGetLastError());
@@ -666,53 +929,33 @@ extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packe
   if (int rc = require_init()) return rc;
   if (int rc = check_q4_shape(K, N)) return rc;
   MS_CHECK_ARG(M >= 1, "matmul: M must be >= 1");
+  MS_CHECK_ARG(K <= kQuantMaxK, "matmul: K must be <= 16384");
   hipStream_t st = ctx().stream;
-  // The kernel-level entry point does not know the caller's data range, so it
-  // scales A by 2^-8 before the fp16 split (|A| < 1.6e7 supported); the model
-  // path derives the prescale from weight-scale bounds instead.
-  const float prescale = 1.0f / 256.0f;
-  const int chunk = 16;
-  const int KG = K / kSuperK;
+  const int chunk = kGemvMaxM;
   const int P = (N / 16) % 4 == 0 && N >= 4 * 16 * 512 ? 4 : 1;
-  const long groups = N / 16 / P;
-  int S = 1;
-  while (!accumulate && groups * S < 512 && S * 2 <= KG && KG % (S * 2) == 0) S *= 2;
-  const size_t hl = (size_t)chunk * K;
-  const size_t need = hl * 2 * sizeof(_Float16) +
-                      (S > 1 ? (size_t)S * chunk * N * sizeof(float) : 0);
   void *buf = nullptr;
-  if (int rc = scratch(need, &buf)) return rc;
-  _Float16 *hi = static_cast<_Float16 *>(buf), *lo = hi + hl;
-  float *parts = reinterpret_cast<float *>(lo + hl);
+  if (int rc = scratch(quant_rows_bytes(chunk, K), &buf)) return rc;
+  const QuantRows q = quant_rows_view(buf, chunk, K);
   for (int m0 = 0; m0 < M; m0 += chunk) {
     const int mm = (M - m0 < chunk) ? M - m0 : chunk;
-    if (int rc = launch_split(d_A + (size_t)m0 * K, mm, K, K, prescale, hi, lo, K, st))
-      return rc;
+    RowSrc r{};
+    r.x = d_A + (size_t)m0 * K;
+    r.ld = K;
+    r.pre_scale = 1.f;
+    if (int rc = launch_quant_rows(r, mm, K, q, st)) return rc;
     GemvArgs a{};
     a.epi = accumulate ? EPI_ACCUMULATE : EPI_STORE;
+    a.asrc = AS_QUANT;
     a.K = K;
     a.M = mm;
-    a.a_hi = hi;
-    a.a_lo = lo;
-    a.lda = K;
-    a.out_mul = 1.0f / prescale;
+    a.q = q;
     a.seg[0] = GemvSeg{d_packed, scale, N, 0};
     a.nseg = 1;
     a.P = P;
     a.waves = 4;
-    a.S = S;
+    a.out = d_C + (size_t)m0 * N;
     a.ldo = N;
-    float *out = d_C + (size_t)m0 * N;
-    if (S > 1) {
-      a.out = parts;
-      a.split_stride = (size_t)mm * N;
-    } else {
-      a.out = out;
-      a.split_stride = 0;
-    }
     if (int rc = launch_gemv(a, st)) return rc;
-    if (S > 1)
-      if (int rc = launch_sum_parts(out, parts, S, (size_t)mm * N, st)) return rc;
   }
   return MS_OK;
 }

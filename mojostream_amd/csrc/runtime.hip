@@ -39,7 +39,7 @@ int scratch(size_t bytes, void **out) {
 }
 
 __global__ void k_fill_random(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream) {
-  const size_t w = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t w = (size_t)blockIdx.x * kBlock + threadIdx.x;
   const size_t i0 = w * 8;
   if (i0 >= n) return;
   const uint64_t r = rand_word(seed, stream, w);
@@ -157,7 +157,7 @@ extern "C" int ms_host_free(void *h_ptr) {
 extern "C" int ms_fill_random_u8(uint8_t *d_dst, size_t n, uint64_t seed, uint64_t stream) {
   if (int rc = require_init()) return rc;
   const size_t words = (n + 7) / 8;
-  hipLaunchKernelGGL(k_fill_random, dim3(cdiv((long)words, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(k_fill_random, dim3(cdiv((long)words, kBlock)), dim3(kBlock), 0,
                      g_ctx.stream, d_dst, n, seed, stream);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
