@@ -11,6 +11,11 @@ runs four independent sequences.  TTFT is prompt ids on the host -> first id
 on the host for a 512-token prompt.
 
 Prints one JSON line (rank 0, N=1).
+
+Profiling: `--eager` times the decode with eager launches instead of the
+graph (rocprofv3 traces those), `--only decode` skips the other sections, and
+`--rocpd-summary DB` prints per-kernel averages over the last decode steps of
+a rocprofv3 database (the summaries kept with the profiles).
 """
 import argparse
 import json
@@ -23,6 +28,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "E4B-shape Q4 decode tokens/s (batch 1/4), TTFT ms; achieved HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
+# GEMV kernel of the Gate|Up projection (dominant decode kernel by bytes)
+GATEUP_KERNEL = "k_gemv<1, 2, 0, 4, 2>"
 
 
 def log(msg):
@@ -31,18 +38,16 @@ def log(msg):
 
 def decode_bytes_per_token(arch, ctx_len):
     """Algorithmic HBM bytes of one batch-1 decode token: every Q4 weight byte
-    once, plus the K and V rows read by attention and the row written."""
+    once (layers and the tied LM head), plus the K and V rows read by attention
+    and the K/V row written."""
     b = arch.weight_bytes() + arch.hidden * arch.vocab // 2
     for d in arch.layers:
-        if d.cache_kind == 1:
-            keys = min(ctx_len, d.cache_len)
-        else:
-            keys = min(ctx_len, d.cache_len)
+        keys = min(ctx_len, d.cache_len)
         b += 2 * keys * d.kv_dim * 4 + 2 * d.kv_dim * 4
     return b
 
 
-def cpu_baseline(ms, arch, seed, n_tokens):
+def cpu_baseline(arch, seed, n_tokens):
     """The oracle (C restatement of the reference CPU path, B-pack blocking,
     single thread like the reference's decode, AVX2 build when the host has
     it) timed on a bounded sample: n_tokens decode tokens of the full model."""
@@ -62,6 +67,82 @@ def cpu_baseline(ms, arch, seed, n_tokens):
                       f"(positions 0..{n_tokens - 1}), oracle/{o.name}, 1 thread"}
 
 
+def rocpd_summary(db, steps, marker="k_embed", end_marker="k_argmax_fin"):
+    """Per-kernel duration statistics over the last `steps` decode steps of a
+    rocprofv3 database (a step runs from the embedding kernel to the argmax
+    finalization; launches after the last step, such as the sweep, are
+    excluded)."""
+    import re
+    import sqlite3
+    c = sqlite3.connect(db)
+    cols = [r[1] for r in c.execute("pragma table_info(kernels)")]
+    name = "name" if "name" in cols else "kernel_name"
+    rows = c.execute(f"select {name}, start, end from kernels order by start").fetchall()
+    starts = [i for i, r in enumerate(rows) if marker in r[0]]
+    if len(starts) < steps:
+        raise SystemExit(f"only {len(starts)} decode steps in {db}")
+    last = max(i for i, r in enumerate(rows) if end_marker in r[0])
+    seg = rows[starts[-steps]:last + 1]
+    agg = {}
+    for n, s, e in seg:
+        n = re.sub(r"\(.*", "", n).replace("void ", "")
+        a = agg.setdefault(n, [0, 0.0, 1e30, 0.0])
+        d = (e - s) / 1000.0
+        a[0] += 1
+        a[1] += d
+        a[2] = min(a[2], d)
+        a[3] = max(a[3], d)
+    wall = (seg[-1][2] - seg[0][1]) / 1000.0 / steps
+    busy = sum(v[1] for v in agg.values()) / steps
+    out = [f"decode steps: {steps}; wall per step {wall:.1f} us; kernel time per step {busy:.1f} us",
+           f"{'kernel':48s} {'calls/step':>10s} {'us/step':>9s} {'avg_us':>8s} {'min_us':>8s} {'max_us':>8s}"]
+    for k, v in sorted(agg.items(), key=lambda x: -x[1][1]):
+        out.append(f"{k[:48]:48s} {v[0] / steps:10.1f} {v[1] / steps:9.1f} {v[1] / v[0]:8.2f} "
+                   f"{v[2]:8.2f} {v[3]:8.2f}")
+    return "\n".join(out)
+
+
+def pmc_summary(fetch_csv, write_csv, kernel, copy_bytes):
+    """HBM traffic per dispatch of `kernel` (decode launches: one activation
+    row) from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; KiB per
+    dispatch), each scaled by what the same counter reads for the plain copy of
+    copy_bytes in the same run."""
+    import csv
+    res = {}
+    for path, counter in ((fetch_csv, "FETCH_SIZE"), (write_csv, "WRITE_SIZE")):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        # the largest copy dispatch of the run is the calibration copy
+        copy = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        if not copy:
+            raise SystemExit(f"no calibration copy in {path}")
+        # the copy reads and writes copy_bytes
+        factor = copy_bytes / 1024.0 / max(copy)
+        # decode launches (one activation row: the smallest grid of the kernel)
+        ks = [r for r in rows if kernel in r["Kernel_Name"]]
+        g = min((int(r["Grid_Size"]) for r in ks), default=0)
+        vals = [float(r["Counter_Value"]) for r in ks if int(r["Grid_Size"]) == g]
+        if not vals:
+            raise SystemExit(f"no {kernel} dispatches in {path}")
+        res[counter] = {"factor": factor, "n": len(vals), "min_kib": min(vals),
+                        "median_kib": sorted(vals)[len(vals) // 2],
+                        "bytes": sorted(vals)[len(vals) // 2] * 1024.0 * factor}
+    res["traffic_bytes"] = res["FETCH_SIZE"]["bytes"] + res["WRITE_SIZE"]["bytes"]
+    return res
+
+
+def traffic_from_profile():
+    """Traffic per launch of the dominant kernel as recorded in the committed
+    profile summary (measured with rocprofv3 --pmc), or None."""
+    path = os.path.join(ROOT, "profiles", "gateup_gemv_e4b_decode_hbm_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -71,8 +152,28 @@ def main():
     ap.add_argument("--ttft-prompt", type=int, default=512)
     ap.add_argument("--cpu-tokens", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time the decode with eager launches")
+    ap.add_argument("--only", choices=["all", "decode"], default="all")
+    ap.add_argument("--prof-tokens", type=int, default=16)
+    ap.add_argument("--rocpd-summary", metavar="DB", help="summarize a rocprofv3 database and exit")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="one device-to-device copy of this size (HBM counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="HBM traffic of the Gate|Up GEMV from two --pmc runs and exit")
     ap.add_argument("--seed", type=int, default=42)
     args = ap.parse_args()
+    if args.rocpd_summary:
+        print(rocpd_summary(args.rocpd_summary, args.steps))
+        return
+    if args.pmc_summary:
+        r = pmc_summary(args.pmc_summary[0], args.pmc_summary[1], GATEUP_KERNEL,
+                        (args.copy_mib or 256) << 20)
+        for c in ("FETCH_SIZE", "WRITE_SIZE"):
+            v = r[c]
+            print(f"{c}: dispatches {v['n']}, median {v['median_kib']:.1f} KiB, min {v['min_kib']:.1f} KiB, "
+                  f"copy calibration factor {v['factor']:.4f} -> {v['bytes']:.0f} bytes")
+        print(f"traffic_bytes_per_launch: {r['traffic_bytes']:.0f}")
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note only)"}))
@@ -84,8 +185,10 @@ def main():
     ms.init(0)
     name, ncu, hbm = ms.device_info()
     log(f"device {name} CUs={ncu}")
-    max_pos = max(args.prompt + args.warmup + args.steps + 8, args.ttft_prompt + 8)
+    max_pos = max(args.prompt + args.warmup + args.steps + args.prof_tokens + 8,
+                  args.ttft_prompt + 8)
     arch = ms.arch_e4b(max_full_seq=max_pos)
+    use_graph = not args.eager
 
     # ---- batch 1 ---------------------------------------------------------------
     m = ms.Model(arch, max_seqs=4, max_rows=4, max_pos=max_pos)
@@ -95,76 +198,47 @@ def main():
     prompt = [int(v % arch.vocab) for v in ms.host_random_u8(4 * args.prompt, 9, 1).view(np.uint32)]
     first = m.prefill(prompt, 0)
     pos = len(prompt)
-    ids_w = m.decode([first], [pos], args.warmup)  # warmup (also captures the graph)
+    ids_w = m.decode([first], [pos], args.warmup, use_graph=use_graph)  # warmup (+ graph capture)
     pos += args.warmup
     tok = int(ids_w[-1, 0])
     ms.synchronize()
-    check = ms.lib()
     t0 = time.perf_counter()
-    ids = m.decode([tok], [pos], args.steps)
+    ids = m.decode([tok], [pos], args.steps, use_graph=use_graph)
     ms.synchronize()
     dt1 = time.perf_counter() - t0
+    pos += args.steps
     tps1 = args.steps / dt1
     ms_step = dt1 * 1e3 / args.steps
-    log(f"batch 1: {tps1:.1f} tok/s ({ms_step:.3f} ms/token)")
-    ctx_mid = pos + args.steps // 2
+    log(f"batch 1: {tps1:.1f} tok/s ({ms_step:.3f} ms/token, {'graph' if use_graph else 'eager'})")
+    ctx_mid = len(prompt) + args.warmup + args.steps // 2
     bpt = decode_bytes_per_token(arch, ctx_mid)
     step_gbps = bpt / (dt1 / args.steps) / 1e9
 
-    # ---- instrumented pass: per-kernel-class HIP events (eager launches) -------
+    # ---- instrumented pass, then the dominant kernel's duration on the device --
+    # The profiled eager pass records the last launch of each projection class;
+    # ms_prof_sweep re-launches it back to back over every layer's weights
+    # between two HIP events on the launch stream (weights cold, as in a step).
     ms.prof_enable(True)
-    m.decode([int(ids[-1, 0])], [pos + args.steps], 16, use_graph=False)
+    m.decode([int(ids[-1, 0])], [pos], args.prof_tokens, use_graph=False)
+    pos += args.prof_tokens
     prof = ms.prof_get()
     ms.prof_enable(False)
-    gu = prof["gateup_gemv"]
-    gu_ms = gu["ms"] / max(gu["launches"], 1)
-    gu_bytes = gu["bytes"] / max(gu["launches"], 1)
-    roof = {"bound": "hbm", "kernel": "k_gemv<0,2> (Gate+Up Q4 GEMV, SwiGLU epilogue)",
-            "achieved": gu_bytes / (gu_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "traffic": None, "avg_launch_us": gu_ms * 1e3,
-            "bytes_per_launch": gu_bytes}
+    eager_ms = sum(v["ms"] for v in prof.values()) / args.prof_tokens
+    log(f"per-class (eager + events, {args.prof_tokens} tokens): " + ", ".join(
+        f"{k} {v['ms'] / args.prof_tokens:.3f}ms" for k, v in prof.items() if v["launches"]))
+    sweeps = {}
+    for cls in ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv"):
+        sw = ms.prof_sweep(m, cls, passes=2)
+        sw["gbps"] = sw["bytes_per_launch"] / (sw["avg_us"] * 1e-6) / 1e9
+        sweeps[cls] = {k: round(v, 3) for k, v in sw.items()}
+        log(f"sweep {cls}: {sw['avg_us']:.2f} us/launch, {sw['gbps']:.0f} GB/s "
+            f"({sw['launches']} launches)")
+    gu = sweeps["gateup_gemv"]
+    roof = {"bound": "hbm", "kernel": f"{GATEUP_KERNEL} (Gate|Up Q4 GEMV, SwiGLU epilogue)",
+            "achieved": gu["bytes_per_launch"] / (gu["avg_us"] * 1e-6) / 1e9,
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "traffic": traffic_from_profile(),
+            "avg_launch_us": gu["avg_us"], "bytes_per_launch": gu["bytes_per_launch"]}
     roof["frac"] = roof["achieved"] / roof["peak"]
-    eager_ms = sum(v["ms"] for v in prof.values()) / 16
-    log("per-class (eager, 16 tokens): " + ", ".join(
-        f"{k} {v['ms'] / 16:.3f}ms" for k, v in prof.items() if v["launches"]))
-
-    # ---- batch 4 ------------------------------------------------------------------
-    firsts, lens = [], []
-    for s in range(4):
-        p = [int(v % arch.vocab) for v in ms.host_random_u8(4 * args.prompt, 9, 20 + s).view(np.uint32)]
-        import ctypes as C
-        t = np.asarray(p, np.int32)
-        f = C.c_int32()
-        ms.check(check.ms_prefill(m.h, s, t.ctypes.data, len(t), 0, C.byref(f)))
-        firsts.append(int(f.value))
-        lens.append(len(p))
-    w4 = m.decode(firsts, lens, args.warmup)
-    ms.synchronize()
-    t0 = time.perf_counter()
-    m.decode(w4[-1].tolist(), [l + args.warmup for l in lens], args.steps)
-    ms.synchronize()
-    dt4 = time.perf_counter() - t0
-    tps4 = 4 * args.steps / dt4
-    log(f"batch 4: {tps4:.1f} tok/s")
-    m.close()
-
-    # ---- TTFT (prompt ids on host -> first id on host) --------------------------
-    ttft = {}
-    for P in sorted({args.ttft_prompt, 2048}):
-        if P > max_pos - 8:
-            continue
-        mt = ms.Model(ms.arch_e4b(max_full_seq=max_pos), max_seqs=1, max_rows=16,
-                      max_pos=max_pos)
-        mt.fill_synthetic(args.seed)
-        pr = [int(v % arch.vocab) for v in ms.host_random_u8(4 * P, 9, 3).view(np.uint32)]
-        mt.prefill(pr[:16], 0)  # warm-up of the prefill kernels
-        mt.reset()
-        ms.synchronize()
-        t0 = time.perf_counter()
-        mt.prefill(pr, 0)
-        ttft[P] = (time.perf_counter() - t0) * 1e3
-        log(f"TTFT prompt {P}: {ttft[P]:.1f} ms")
-        mt.close()
 
     out = {
         "metric": METRIC, "value": round(tps1, 2), "unit": "tokens/s", "n_gpus": 1,
@@ -174,18 +248,74 @@ def main():
         "config": {"workload": "E4B-shape Q4 greedy decode, batch 1, weights resident",
                    "hidden": 2560, "layers": 42, "ffn": 10240, "vocab": 262144,
                    "prompt_tokens": args.prompt, "decode_steps": args.steps,
+                   "launch": "hip graph per step" if use_graph else "eager",
                    "parallelism": "single GPU"},
-        "batch4_tokens_per_s": round(tps4, 2),
-        "ttft_ms": {str(k): round(v, 2) for k, v in ttft.items()},
         "step_hbm_gbps": round(step_gbps, 1),
         "step_roofline_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "bytes_per_token": bpt,
         "eager_ms_per_token": round(eager_ms, 4),
         "roofline": roof,
+        "kernel_sweep": sweeps,
         "device": name,
     }
+
+    if args.only == "all":
+        # ---- batch 4 ----------------------------------------------------------------
+        import ctypes as C
+        check = ms.lib()
+        firsts, lens = [], []
+        for s in range(4):
+            p = [int(v % arch.vocab) for v in ms.host_random_u8(4 * args.prompt, 9, 20 + s).view(np.uint32)]
+            t = np.asarray(p, np.int32)
+            f = C.c_int32()
+            ms.check(check.ms_prefill(m.h, s, t.ctypes.data, len(t), 0, C.byref(f)))
+            firsts.append(int(f.value))
+            lens.append(len(p))
+        w4 = m.decode(firsts, lens, args.warmup, use_graph=use_graph)
+        ms.synchronize()
+        t0 = time.perf_counter()
+        m.decode(w4[-1].tolist(), [l + args.warmup for l in lens], args.steps, use_graph=use_graph)
+        ms.synchronize()
+        dt4 = time.perf_counter() - t0
+        tps4 = 4 * args.steps / dt4
+        log(f"batch 4: {tps4:.1f} tok/s")
+        out["batch4_tokens_per_s"] = round(tps4, 2)
+        m.close()
+
+        # ---- TTFT (prompt ids on host -> first id on host) --------------------------
+        ttft = {}
+        for P in sorted({args.ttft_prompt, 2048}):
+            if P > max_pos - 8:
+                continue
+            mt = ms.Model(ms.arch_e4b(max_full_seq=max_pos), max_seqs=1, max_rows=16,
+                          max_pos=max_pos)
+            mt.fill_synthetic(args.seed)
+            pr = [int(v % arch.vocab) for v in ms.host_random_u8(4 * P, 9, 3).view(np.uint32)]
+            mt.prefill(pr[:16], 0)  # warm-up of the prefill kernels
+            mt.reset()
+            ms.synchronize()
+            t0 = time.perf_counter()
+            mt.prefill(pr, 0)
+            ttft[P] = (time.perf_counter() - t0) * 1e3
+            log(f"TTFT prompt {P}: {ttft[P]:.1f} ms")
+            mt.close()
+        out["ttft_ms"] = {str(k): round(v, 2) for k, v in ttft.items()}
+    else:
+        m.close()
+
+    if args.copy_mib:
+        # a plain copy of known size: what FETCH_SIZE/WRITE_SIZE read for it
+        # scales the counters of the GEMV launches
+        nb = args.copy_mib << 20
+        src, dst = ms.DeviceBuffer(nb), ms.DeviceBuffer(nb)
+        ms.check(ms.lib().ms_memcpy_d2d(dst.ptr, src.ptr, nb))
+        ms.synchronize()
+        out["copy_calibration_bytes"] = nb
+        src.free()
+        dst.free()
+
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(ms, arch, args.seed, args.cpu_tokens)
+        out["cpu_baseline"] = cpu_baseline(arch, args.seed, args.cpu_tokens)
     print(json.dumps(out))
 
 

@@ -238,6 +238,17 @@ int ms_model_stream_stats(ms_model *m, ms_stream_stats *out);
 int ms_prof_enable(int on);
 int ms_prof_get(int cls, const char **name, long *launches, double *total_ms,
                 double *bytes);
+/* Kernel duration of one projection class (0 QKV, 2 O, 3 Gate|Up, 4 Down)
+ * measured on the device: the last launch of that class recorded while
+ * profiling was enabled is re-launched back to back `passes` times over every
+ * layer with the same shapes, each launch on that layer's weights (so weights
+ * come from HBM as in a decode step), between two HIP events on the library
+ * stream.  Outputs average microseconds and bytes of Q4 weights per launch.
+ * The re-launches overwrite only per-step scratch rows (recomputed by the next
+ * decode step); KV caches and positions are untouched.  No reference
+ * counterpart: measurement support. */
+int ms_prof_sweep(ms_model *m, int cls, int passes, double *avg_us, double *bytes_per_launch,
+                  long *launches);
 
 #ifdef __cplusplus
 }

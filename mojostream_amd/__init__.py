@@ -92,6 +92,8 @@ _SIGS = {
     "ms_prefill": [_P, _I, _P, _I, _I, _P],
     "ms_model_stream_stats": [_P, C.POINTER(StreamStats)],
     "ms_prof_enable": [_I],
+    "ms_prof_sweep": [_P, _I, _I, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                      C.POINTER(C.c_long)],
     "ms_prof_get": [_I, C.POINTER(C.c_char_p), C.POINTER(C.c_long),
                     C.POINTER(C.c_double), C.POINTER(C.c_double)],
 }
@@ -437,6 +439,21 @@ class Model:
 
 def prof_enable(on: bool) -> None:
     check(_lib.ms_prof_enable(1 if on else 0))
+
+
+PROF_CLASSES = {"qkv_gemv": 0, "attention": 1, "o_gemv": 2, "gateup_gemv": 3,
+                "down_gemv": 4, "lm_head": 5, "embed_prep": 6, "other": 7}
+
+
+def prof_sweep(model: "Model", cls: str, passes: int = 1) -> dict:
+    """Device-side duration of one projection class: its last profiled launch
+    re-run back to back over every layer's weights (ms_prof_sweep)."""
+    avg = C.c_double()
+    by = C.c_double()
+    n = C.c_long()
+    check(_lib.ms_prof_sweep(model.h, PROF_CLASSES[cls], passes, C.byref(avg), C.byref(by),
+                             C.byref(n)))
+    return dict(avg_us=avg.value, bytes_per_launch=by.value, launches=n.value)
 
 
 def prof_get() -> dict:

@@ -68,6 +68,11 @@ struct Prof {
   };
   std::vector<Rec> pending;
   size_t used = 0;
+  int cur = -1;                                 // class of the open ProfScope
+  GemvArgs last[MS_PROF_CLASSES] = {};          // last GEMV launch per class
+  int last_layer[MS_PROF_CLASSES] = {};
+  bool have[MS_PROF_CLASSES] = {};
+  int layer = -1;
 };
 static Prof g_prof;
 
@@ -144,6 +149,7 @@ struct ProfScope {
   hipEvent_t b{};
   bool active;
   ProfScope(int c, double by, hipStream_t s) : cls(c), bytes(by), st(s) {
+    g_prof.cur = c;
     active = g_prof.on && !capturing(s);
     if (active) {
       hipEvent_t a = prof_event();
@@ -154,6 +160,7 @@ struct ProfScope {
   }
   ~ProfScope() {
     if (active) (void)hipEventRecord(b, st);
+    g_prof.cur = -1;
   }
 };
 static void prof_collect() {
@@ -182,18 +189,27 @@ struct RunCfg {
 // Launch a projection of rows r: quantized in the kernel's prologue with
 // `waves` waves per block when the limb rows fit in LDS, else by the quant
 // kernel into m->quant first (the GEMV then reads them from global memory).
+static int launch_gemv_rec(const GemvArgs &a, hipStream_t st) {
+  if (g_prof.on && g_prof.cur >= 0) {
+    g_prof.last[g_prof.cur] = a;
+    g_prof.last_layer[g_prof.cur] = g_prof.layer;
+    g_prof.have[g_prof.cur] = true;
+  }
+  return launch_gemv(a, st);
+}
+
 static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipStream_t st) {
   constexpr size_t kLdsLimit = 150 * 1024;
   a.asrc = AS_ROWS;
   a.rows = r;
   a.waves = waves;
-  if (a.K <= 8 * 2 * 64 * waves && gemv_lds_need(a) <= kLdsLimit) return launch_gemv(a, st);
+  if (a.K <= 8 * 2 * 64 * waves && gemv_lds_need(a) <= kLdsLimit) return launch_gemv_rec(a, st);
   a.asrc = AS_QUANT;
   a.rows = RowSrc{};
   a.q = quant_rows_view(m->quant, a.M, a.K);
   a.waves = 4;
   if (int rc = launch_quant_rows(r, a.M, a.K, a.q, st)) return rc;
-  return launch_gemv(a, st);
+  return launch_gemv_rec(a, st);
 }
 
 // Rows entering layer l: the previous layer's output or the call's input rows.
@@ -203,6 +219,7 @@ static const float *layer_input(ms_model *m, const RunCfg &rc, int l) {
 
 static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
   Layer &Ly = m->L[l];
+  g_prof.layer = l;
   const ms_layer_desc &d = Ly.d;
   const int M = rc.B * rc.T;
   const int D = m->d.hidden, F = m->d.ffn;
@@ -931,5 +948,65 @@ extern "C" int ms_prof_get(int cls, const char **name, long *launches, double *t
   if (launches) *launches = g_prof.launches[cls];
   if (total_ms) *total_ms = g_prof.ms[cls];
   if (bytes) *bytes = g_prof.bytes[cls];
+  return MS_OK;
+}
+
+extern "C" int ms_prof_sweep(ms_model *m, int cls, int passes, double *avg_us,
+                             double *bytes_per_launch, long *launches) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && avg_us && passes >= 1, "prof_sweep: bad arguments");
+  MS_CHECK_ARG(cls == PC_QKV || cls == PC_O || cls == PC_GATEUP || cls == PC_DOWN,
+               "prof_sweep: class must be a layer projection");
+  MS_CHECK_ARG(g_prof.have[cls], "prof_sweep: no launch of this class recorded while profiling");
+  MS_CHECK_ARG(m->d.resident, "prof_sweep: resident models only");
+  const GemvArgs base = g_prof.last[cls];
+  const ms_layer_desc &d0 = m->L[g_prof.last_layer[cls]].d;
+  // matrices of each class: Q|K|V (0,1,2), O (3), Gate|Up (4,5), Down (6)
+  std::vector<int> layers;
+  for (int l = 0; l < (int)m->L.size(); ++l) {
+    const ms_layer_desc &d = m->L[l].d;
+    // Gate|Up and Down shapes are the same in every layer
+    const bool same = (cls == PC_GATEUP || cls == PC_DOWN) ||
+                      (d.q_dim == d0.q_dim && d.kv_dim == d0.kv_dim);
+    if (same) layers.push_back(l);
+  }
+  hipStream_t st = ctx().stream;
+  hipEvent_t e0, e1;
+  MS_HIP_TRY(hipEventCreate(&e0));
+  MS_HIP_TRY(hipEventCreate(&e1));
+  double bytes = 0;
+  long n = 0;
+  int rc = MS_OK;
+  MS_HIP_TRY(hipEventRecord(e0, st));
+  for (int p = 0; p < passes && rc == MS_OK; ++p)
+    for (int l : layers) {
+      Layer &Ly = m->L[l];
+      GemvArgs a = base;
+      if (cls == PC_QKV) {
+        for (int i = 0; i < 3; ++i) a.seg[i].w = Ly.w[i], a.seg[i].scale = Ly.scale[i];
+      } else if (cls == PC_O) {
+        a.seg[0].w = Ly.w[3], a.seg[0].scale = Ly.scale[3];
+      } else if (cls == PC_GATEUP) {
+        a.seg[0].w = Ly.w[4], a.seg[0].scale = Ly.scale[4];
+        a.seg[1].w = Ly.w[5], a.seg[1].scale = Ly.scale[5];
+      } else {
+        a.seg[0].w = Ly.w[6], a.seg[0].scale = Ly.scale[6];
+      }
+      if ((rc = launch_gemv(a, st))) break;
+      double b = 0;
+      for (int i = 0; i < a.nseg; ++i) b += (double)a.K * a.seg[i].n_cols / 2;
+      bytes += b;
+      ++n;
+    }
+  (void)hipEventRecord(e1, st);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  *avg_us = n ? (double)ms * 1e3 / n : 0.0;
+  if (bytes_per_launch) *bytes_per_launch = n ? bytes / n : 0.0;
+  if (launches) *launches = n;
   return MS_OK;
 }
