@@ -100,8 +100,9 @@ int ms_dequant_q4_packed(float *d_out, const uint8_t *d_packed, int K, int N,
 /* C (+)= A . deq(W): matmul_q4_bpack_raw, kernels.mojo:201-267 (and
  * matmul_q4_bpack :122-193 on a Q4Matrix).  A fp32 [M][K], W panel layout,
  * C fp32 [M][N].  accumulate=1 keeps the reference's C += semantics,
- * accumulate=0 overwrites.  M <= 16 runs the decode GEMV, larger M the
- * prefill GEMM. */
+ * accumulate=0 overwrites.  Rows are processed in chunks of 16 (each row
+ * quantized to a 31-bit fixed-point value, exact integer dot products);
+ * K <= 16384. */
 int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
                  int K, int N, float scale, int accumulate);
 
@@ -180,8 +181,8 @@ int ms_model_destroy(ms_model *m);
 /* Binds one of the 7 matrices (0 Q,1 K,2 V,3 O,4 Gate,5 Up,6 Down -- the
  * .mojostream type tag minus one, mojostream.mojo:21-28) of a layer.
  * `src` is row-major reference Q4, on the device if src_on_device else host.
- * Resident models pack it into HBM; streaming models require host memory
- * from ms_host_alloc and keep a packed pinned copy.
+ * Resident models pack it into HBM; streaming models take host memory and
+ * keep a packed copy in pinned host memory.
  * Replaces load_weights_from_ms (harness.mojo:80-122) and
  * get_layer_ref (sparse_pin.mojo:295-330). */
 int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_t *src,

@@ -256,7 +256,7 @@ class Arch:
 
 
 def arch_demo(max_len: int = 512, n_layers: int = 40) -> Arch:
-    """BASELINE demo: D=1024, 8q/2kv heads, hd 128, F=4096, theta 1e4."""
+    """Demo model: D=1024, 8q/2kv heads, hd 128, F=4096, theta 1e4."""
     return Arch("demo", 1024, 4096, [demo_layer(1024, 8, 2, max_len) for _ in range(n_layers)])
 
 

@@ -93,7 +93,7 @@ static void bpack_block(float *C, const float *A, const uint8_t *wq, int m0,
   }
 }
 
-/* Optional column split over threads for the checker (not the reference's
+/* Optional column split over threads for the oracle (not the reference's
  * threading, which splits rows): every C element keeps its summation order,
  * so results are bit-identical for any thread count. */
 static int g_threads = 1;
