@@ -8,75 +8,133 @@
 // softmax, sum p*v; query head hq reads kv head hq / (n_heads/n_kv).
 //
 // Two launches:
-//  k_attn_chunks   one block per (sequence, kv head, 16-key chunk, row group):
-//                  the chunk's K and V rows and q (after RoPE) for the kv
-//                  head's G query heads staged in LDS with every load issued
-//                  up front, then (max, sum, o[hd]) per (row, head).
-//  k_attn_combine  one block per (sequence, row, query head): merges the chunks
-//                  (log-sum-exp rescaling), writes the O-projection input
-//                  rows (fp32) and appends the row's K (after RoPE)
-//                  and V to the cache.  It runs after every chunk block has
-//                  read the cache, so rows that wrap the circular window never
+//  k_attn_chunks   one block per (16-key chunk, row group, sequence x kv head):
+//                  the chunk's cached K and V rows, the rows' fresh K/V and q
+//                  (after RoPE) for the kv head's G query heads staged in LDS,
+//                  then (max, sum, o[hd]) per (row, head).
+//  k_attn_combine  one block per (query head, row, sequence): merges the
+//                  chunks (log-sum-exp rescaling), writes the O-projection
+//                  input row (fp32) and appends the row's K (after RoPE) and V
+//                  to the cache.  It runs after every chunk block has read the
+//                  cache, so rows that wrap the circular window never
 //                  overwrite a key another row still needs.
-// Keys of the current rows are read from the fresh projections, older keys
-// from the cache.
+// Keys of the current rows come from the fresh projections, older keys from
+// the cache.  Every phase issues all of its global loads before the first use
+// (one memory round trip per phase after the position load).
 #include <cmath>
 
 #include "attention.h"
 
 namespace ms {
 
-// q|k|v element (row, col) of the fused projection output.
-__device__ inline float qkv_val(const AttnArgs &a, int row, int col) {
-  return a.qkv[(size_t)row * a.ld + col];
+template <class T>
+__device__ inline T aldg(const void *p) {
+  return *(const __attribute__((address_space(1))) T *)p;
+}
+template <>
+__device__ inline float4 aldg<float4>(const void *p) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 v = *(const __attribute__((address_space(1))) f32x4 *)p;
+  return float4{v.x, v.y, v.z, v.w};
 }
 
-// Element d of a head starting at column c0 of row `row`, rotated by RoPE at
-// position pos (apply_rope_inplace, kernels.mojo:579-595; pairs (i, i+rot/2)
-// over the first rot dims).  Branch-free: the pair element and the table
-// entries are loaded for every d (clamped into range) and selected afterwards.
-__device__ inline float rope_val(const AttnArgs &a, int row, int c0, int d, int pos) {
-  const int half = a.rot >> 1;
-  const bool rot = a.apply_rope && d < a.rot;
-  const int dd = d < a.rot ? d : 0;
-  const int i = dd < half ? dd : dd - half;
-  const int pd = dd < half ? dd + half : dd - half;
-  const float x = qkv_val(a, row, c0 + d);
-  const float y = qkv_val(a, row, c0 + pd);
-  const size_t ti = a.apply_rope ? (size_t)pos * half + i : 0;
-  const float cv = a.apply_rope ? a.cos_t[ti] : 1.f;
-  const float sv = a.apply_rope ? a.sin_t[ti] : 0.f;
-  const float r = (dd < half) ? x * cv - y * sv : y * sv + x * cv;
-  return rot ? r : x;
+// Launch parameters as scalars, read once at kernel entry (an opaque register
+// move keeps the compiler from re-reading the argument struct later).
+template <class T>
+__device__ inline T keep(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
 }
 
-__device__ inline void key_range(const AttnArgs &a, int p, int *lo, int *hi) {
-  if (a.cache_kind == MS_CACHE_CIRCULAR) {
-    const int l = p - a.cache_len + 1;
+struct AttnP {
+  int T, q_dim, kv_dim, n_heads, n_kv, G, rot, half, circular, cache_len, clamp, ld, apply_rope,
+      n_chunks, write_cache;
+  float scale;
+  const float *qkv, *cos_t, *sin_t;
+  const int32_t *pos;
+  float *kc, *vc, *part, *out;
+  size_t cache_seq_stride;
+};
+
+__device__ inline AttnP load_params(const AttnArgs &a) {
+  AttnP p;
+  p.T = keep(a.T);
+  p.q_dim = keep(a.q_dim);
+  p.kv_dim = keep(a.kv_dim);
+  p.n_heads = keep(a.n_heads);
+  p.n_kv = keep(a.n_kv);
+  p.G = p.n_heads / p.n_kv;
+  p.rot = keep(a.rot);
+  p.half = p.rot >> 1;
+  p.circular = keep(a.cache_kind) == MS_CACHE_CIRCULAR;
+  p.cache_len = keep(a.cache_len);
+  p.clamp = keep(a.clamp);
+  p.ld = keep(a.ld);
+  p.apply_rope = keep(a.apply_rope);
+  p.n_chunks = keep(a.n_chunks);
+  p.write_cache = keep(a.write_cache);
+  p.scale = keep(a.scale);
+  p.qkv = keep(a.qkv);
+  p.cos_t = keep(a.cos_t);
+  p.sin_t = keep(a.sin_t);
+  p.pos = keep(a.pos);
+  p.kc = keep(a.kc);
+  p.vc = keep(a.vc);
+  p.part = keep(a.part);
+  p.out = keep(a.out);
+  p.cache_seq_stride = keep(a.cache_seq_stride);
+  return p;
+}
+
+__device__ inline void key_range(const AttnP &p, int pos, int *lo, int *hi) {
+  if (p.circular) {
+    const int l = pos - p.cache_len + 1;
     *lo = l > 0 ? l : 0;
-    *hi = p;
+    *hi = pos;
   } else {
     *lo = 0;
-    int h = p;
-    if (a.clamp && h > a.cache_len - 1) h = a.cache_len - 1;
+    int h = pos;
+    if (p.clamp && h > p.cache_len - 1) h = p.cache_len - 1;
     *hi = h;
   }
 }
 
-__device__ inline int cache_slot(const AttnArgs &a, int t) {
-  return a.cache_kind == MS_CACHE_CIRCULAR ? t % a.cache_len : t;
+__device__ inline int cache_slot(const AttnP &p, int t) {
+  return p.circular ? t % p.cache_len : t;
 }
 
-__device__ inline int row_group(const AttnArgs &a, int *RG) {
-  const int G = a.n_heads / a.n_kv;
-  const int TR = max(1, min(a.T, kAttnMaxTG / G));
-  *RG = (a.T + TR - 1) / TR;
-  return TR;
+// Element d of a head (starting at column c0 of qkv row `row`) after RoPE at
+// position pos (apply_rope_inplace, kernels.mojo:579-595: pairs (i, i+rot/2)
+// over the first rot dims).  Split into a load step and a compute step so the
+// loads of many elements are issued together.
+struct RopeIn {
+  float x, y, c, s;
+  bool rot, lo;
+};
+
+__device__ inline void rope_load(const AttnP &p, int row, int c0, int d, int pos, RopeIn &r) {
+  const bool rot = p.apply_rope && d < p.rot;
+  const bool lo = d < p.half;
+  const int i = lo ? d : d - p.half;
+  const int pd = rot ? (lo ? d + p.half : d - p.half) : d;
+  const float *base = p.qkv + (size_t)row * p.ld + c0;
+  r.x = aldg<float>(base + d);
+  r.y = aldg<float>(base + pd);
+  const size_t ti = rot ? (size_t)pos * p.half + i : 0;
+  r.c = rot ? aldg<float>(p.cos_t + ti) : 1.f;
+  r.s = rot ? aldg<float>(p.sin_t + ti) : 0.f;
+  r.rot = rot;
+  r.lo = lo;
 }
 
+__device__ inline float rope_apply(const RopeIn &r) {
+  if (!r.rot) return r.x;
+  return r.lo ? r.x * r.c - r.y * r.s : r.y * r.s + r.x * r.c;
+}
+
+// 256-thread block reduction (sum or max); every thread gets the result.
 __device__ inline float block_reduce(float v, float *sh, bool is_max) {
-  // 256-thread blocks (a blockDim read would load the dispatch packet)
-  constexpr int nw = 4;
+  constexpr int nw = 4;  // 256 threads: a blockDim read would load the dispatch packet
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -87,37 +145,39 @@ __device__ inline float block_reduce(float v, float *sh, bool is_max) {
   if (lane == 0) sh[w] = v;
   __syncthreads();
   float t = sh[0];
+#pragma unroll
   for (int i = 1; i < nw; ++i) t = is_max ? fmaxf(t, sh[i]) : t + sh[i];
   return t;
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
+constexpr int kRopeBatch = 8;  // q elements per thread per load batch
+
+// TGM: compile-time bound on the (row, query head) pairs of a block (4 for a
+// decode step with 4 query heads per kv head, kAttnMaxTG for prefill row
+// groups); rows past the real count hold zero queries, so every LDS read of
+// the score loop is unconditional.
+template <int HD, int TGM>
+__global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs args) {
   extern __shared__ float lds[];
   constexpr int CH = kAttnChunk;
   constexpr int F4 = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
   constexpr int NV = HD / 64;            // float4 per thread per key (scores)
   constexpr int DPT = (HD + 255) / 256;  // P.V dims per thread
-  const int G = a.n_heads / a.n_kv;
-  int RG;
-  const int TR = row_group(a, &RG);
-  int bid = blockIdx.x;
-  const int rg = bid % RG;
-  bid /= RG;
-  const int c = bid % a.n_chunks;
-  bid /= a.n_chunks;
-  const int h = bid % a.n_kv;
-  const int b = bid / a.n_kv;
+  const AttnP p = load_params(args);
   const int tid = threadIdx.x;
+  const int c = blockIdx.x, rg = blockIdx.y;
+  const int b = (int)blockIdx.z / p.n_kv, h = (int)blockIdx.z % p.n_kv;
+  const int G = p.G;
+  const int TR = max(1, min(p.T, kAttnMaxTG / G));
 
-  const int base = a.pos[b];
+  const int base = aldg<int32_t>(p.pos + b);
   int kmin, kmax, dummy;
-  key_range(a, base, &kmin, &dummy);
-  key_range(a, base + a.T - 1, &dummy, &kmax);
+  key_range(p, base, &kmin, &dummy);
+  key_range(p, base + p.T - 1, &dummy, &kmax);
   const int c0 = kmin + c * CH;
   if (c0 > kmax) return;  // beyond the attended span at this position
   const int r0 = rg * TR;
-  const int nr = min(TR, a.T - r0);
+  const int nr = min(TR, p.T - r0);
   const int TG = nr * G;
   const int nk = min(CH, kmax - c0 + 1);
 
@@ -127,31 +187,34 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
   float *ss = sq + kAttnLds;           // [TG][CH] scores -> probabilities
   float *sm = ss + kAttnMaxTG * CH;    // [TG]
   float *sl = sm + kAttnMaxTG;         // [TG]
-  const float *kcache = a.kc + (size_t)b * a.cache_seq_stride;
-  const float *vcache = a.vc + (size_t)b * a.cache_seq_stride;
+  const float *kcache = p.kc + (size_t)b * p.cache_seq_stride;
+  const float *vcache = p.vc + (size_t)b * p.cache_seq_stride;
 
-  // cache rows of the chunk -> LDS, all loads in flight at once
+  // ---- phase 1: every load of the cached rows and of the first q batch
   float4 kr[F4], vr[F4];
 #pragma unroll
   for (int j = 0; j < F4; ++j) {
-    const int f = tid + 256 * j;            // float4 index in [CH][HD/4]
+    const int f = tid + 256 * j;  // float4 index in [CH][HD/4]
     const int k = f / (HD / 4), d4 = f % (HD / 4);
     const int kp = c0 + k;
+    kr[j] = float4{0.f, 0.f, 0.f, 0.f};
+    vr[j] = float4{0.f, 0.f, 0.f, 0.f};
     if (k < nk && kp < base) {
-      const size_t off = (size_t)cache_slot(a, kp) * a.kv_dim + h * HD + 4 * d4;
-      kr[j] = *reinterpret_cast<const float4 *>(kcache + off);
-      vr[j] = *reinterpret_cast<const float4 *>(vcache + off);
-    } else {
-      kr[j] = float4{0.f, 0.f, 0.f, 0.f};
-      vr[j] = float4{0.f, 0.f, 0.f, 0.f};
+      const size_t off = (size_t)cache_slot(p, kp) * p.kv_dim + h * HD + 4 * d4;
+      kr[j] = aldg<float4>(kcache + off);
+      vr[j] = aldg<float4>(vcache + off);
     }
   }
-  // rotated q for rows r0..r0+nr-1, query heads h*G..h*G+G-1
-#pragma unroll 4
-  for (int e = tid; e < TG * HD; e += 256) {
-    const int tg = e / HD, d = e % HD;
-    const int t = r0 + tg / G, g = tg % G;
-    sq[e] = rope_val(a, b * a.T + t, (h * G + g) * HD, d, base + t);
+  const int nq = TG * HD;
+  RopeIn qi[kRopeBatch];
+#pragma unroll
+  for (int u = 0; u < kRopeBatch; ++u) {
+    const int e = tid + 256 * u;
+    if (e < nq) {
+      const int tg = e / HD, d = e % HD;
+      const int t = r0 + tg / G, g = tg % G;
+      rope_load(p, b * p.T + t, (h * G + g) * HD, d, base + t, qi[u]);
+    }
   }
   // slots of this call's rows are filled below; every other slot (cache rows,
   // and zeros past the chunk end so that 0 * v stays finite) is written here
@@ -164,37 +227,76 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
       reinterpret_cast<float4 *>(sv)[f] = vr[j];
     }
   }
+#pragma unroll
+  for (int u = 0; u < kRopeBatch; ++u) {
+    const int e = tid + 256 * u;
+    if (e < nq) sq[e] = rope_apply(qi[u]);
+  }
+  for (int e = nq + tid; e < TGM * HD; e += 256) sq[e] = 0.f;
+  // remaining q elements (prefill row groups), in batches
+  for (int e0 = 256 * kRopeBatch; e0 < nq; e0 += 256 * kRopeBatch) {
+#pragma unroll
+    for (int u = 0; u < kRopeBatch; ++u) {
+      const int e = e0 + tid + 256 * u;
+      if (e < nq) {
+        const int tg = e / HD, d = e % HD;
+        const int t = r0 + tg / G, g = tg % G;
+        rope_load(p, b * p.T + t, (h * G + g) * HD, d, base + t, qi[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRopeBatch; ++u) {
+      const int e = e0 + tid + 256 * u;
+      if (e < nq) sq[e] = rope_apply(qi[u]);
+    }
+  }
   // rows of this call that fall in the chunk: fresh K (after RoPE) and V
-  const int kin0 = max(c0, base), kin1 = min(c0 + nk, base + a.T);
-  for (int e = tid; e < (kin1 - kin0) * HD; e += 256) {
-    const int kp = kin0 + e / HD, d = e % HD;
-    const int row = b * a.T + (kp - base);
-    sk[(kp - c0) * HD + d] = rope_val(a, row, a.q_dim + h * HD, d, kp);
-    sv[(kp - c0) * HD + d] = qkv_val(a, row, a.q_dim + a.kv_dim + h * HD + d);
+  const int kin0 = max(c0, base), kin1 = min(c0 + nk, base + p.T);
+  const int nin = (kin1 - kin0) * HD;
+  for (int e0 = 0; e0 < nin; e0 += 256 * kRopeBatch) {
+    RopeIn ki[kRopeBatch];
+    float vv[kRopeBatch];
+#pragma unroll
+    for (int u = 0; u < kRopeBatch; ++u) {
+      const int e = e0 + tid + 256 * u;
+      if (e < nin) {
+        const int kp = kin0 + e / HD, d = e % HD;
+        const int row = b * p.T + (kp - base);
+        rope_load(p, row, p.q_dim + h * HD, d, kp, ki[u]);
+        vv[u] = aldg<float>(p.qkv + (size_t)row * p.ld + p.q_dim + p.kv_dim + h * HD + d);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRopeBatch; ++u) {
+      const int e = e0 + tid + 256 * u;
+      if (e < nin) {
+        const int kp = kin0 + e / HD, d = e % HD;
+        sk[(kp - c0) * HD + d] = rope_apply(ki[u]);
+        sv[(kp - c0) * HD + d] = vv[u];
+      }
+    }
   }
   __syncthreads();
 
-  // scores: thread (key kk, dim group dg of 16)
+  // ---- scores: thread (key kk, dim group dg of 16); keys past the chunk end
+  // hold zeros, rows past TG zero queries: no conditional LDS reads
   const int kk = tid >> 4, dg = tid & 15;
   const int kp = c0 + kk;
-  float acc[kAttnMaxTG];
+  float acc[TGM];
 #pragma unroll
-  for (int i = 0; i < kAttnMaxTG; ++i) acc[i] = 0.f;
-  if (kk < nk) {
+  for (int i = 0; i < TGM; ++i) acc[i] = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int d = dg * 4 + 64 * i;
-      const float4 kv = *reinterpret_cast<const float4 *>(sk + kk * HD + d);
+  for (int i = 0; i < NV; ++i) {
+    const int d = dg * 4 + 64 * i;
+    const float4 kv = *reinterpret_cast<const float4 *>(sk + kk * HD + d);
 #pragma unroll
-      for (int t = 0; t < kAttnMaxTG; ++t)
-        if (t < TG) {
-          const float4 qq = *reinterpret_cast<const float4 *>(sq + t * HD + d);
-          acc[t] += qq.x * kv.x + qq.y * kv.y + qq.z * kv.z + qq.w * kv.w;
-        }
+    for (int t = 0; t < TGM; ++t) {
+      const float4 qq = *reinterpret_cast<const float4 *>(sq + t * HD + d);
+      acc[t] += qq.x * kv.x + qq.y * kv.y + qq.z * kv.z + qq.w * kv.w;
     }
   }
 #pragma unroll
-  for (int t = 0; t < kAttnMaxTG; ++t) {
+  for (int t = 0; t < TGM; ++t) {
     float v = acc[t];
     v += __shfl_xor(v, 1, 64);
     v += __shfl_xor(v, 2, 64);
@@ -203,87 +305,133 @@ __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs a) {
     acc[t] = v;
   }
   if (dg == 0) {
-    for (int t = 0; t < TG; ++t) {
-      const int row_t = r0 + t / G;
-      int lo, hi;
-      key_range(a, base + row_t, &lo, &hi);
-      const bool ok = kk < nk && kp >= lo && kp <= hi;
-      ss[t * CH + kk] = ok ? acc[t] * a.scale : -INFINITY;
+#pragma unroll
+    for (int t = 0; t < TGM; ++t) {
+      if (t < TG) {
+        const int row_t = r0 + t / G;
+        int lo, hi;
+        key_range(p, base + row_t, &lo, &hi);
+        const bool ok = kk < nk && kp >= lo && kp <= hi;
+        ss[t * CH + kk] = ok ? acc[t] * p.scale : -INFINITY;
+      }
     }
   }
   __syncthreads();
 
+  if (tid >= TG && tid < TGM) {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) ss[tid * CH + k] = 0.f;
+  }
   if (tid < TG) {
     float m = -INFINITY;
+#pragma unroll
     for (int k = 0; k < CH; ++k) m = fmaxf(m, ss[tid * CH + k]);
     float l = 0.f;
+#pragma unroll
     for (int k = 0; k < CH; ++k) {
       const float sc = ss[tid * CH + k];
-      const float p = (sc == -INFINITY) ? 0.f : expf(sc - m);
-      ss[tid * CH + k] = p;
-      l += p;
+      const float pr = (sc == -INFINITY) ? 0.f : expf(sc - m);
+      ss[tid * CH + k] = pr;
+      l += pr;
     }
     sm[tid] = m;
     sl[tid] = l;
   }
   __syncthreads();
 
+  // ---- P.V: values of the chunk in registers, probabilities broadcast from LDS
+  float *pbase = p.part + (((size_t)b * p.n_kv + h) * p.n_chunks + c) * p.T * G * (HD + 2);
 #pragma unroll
   for (int j = 0; j < DPT; ++j) {
     const int d = tid + 256 * j;
     if (d >= HD) continue;
-    for (int t = 0; t < TG; ++t) {
-      float o = 0.f;
+    float vk[CH];
 #pragma unroll
-      for (int k = 0; k < CH; ++k) o += ss[t * CH + k] * sv[k * HD + d];
-      const int row_t = r0 + t / G, g = t % G;
-      float *pp = a.part + ((((size_t)b * a.n_kv + h) * a.n_chunks + c) * a.T * G +
-                            (size_t)row_t * G + g) * (HD + 2);
-      pp[d] = o;
-      if (d == 0) {
-        pp[HD] = sm[t];
-        pp[HD + 1] = sl[t];
+    for (int k = 0; k < CH; ++k) vk[k] = sv[k * HD + d];
+    float o[TGM];
+#pragma unroll
+    for (int t = 0; t < TGM; ++t) {
+      o[t] = 0.f;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) o[t] += ss[t * CH + k] * vk[k];
+    }
+#pragma unroll
+    for (int t = 0; t < TGM; ++t) {
+      if (t < TG) {
+        const int row_t = r0 + t / G, g = t % G;
+        float *pp = pbase + ((size_t)row_t * G + g) * (HD + 2);
+        pp[d] = o[t];
+        if (d == 0) {
+          pp[HD] = sm[t];
+          pp[HD + 1] = sl[t];
+        }
       }
     }
   }
 }
 
-// One block per (sequence, row, query head): chunk weights exp(m_c - M) / L,
-// then o[d] = sum_c w_c * o_c[d] with every chunk's load of a 16-chunk group
-// in flight together.
+// One block per (query head, row, sequence): chunk weights exp(m_c - M) / L,
+// then o[d] = sum_c w_c * o_c[d] with the loads of a 16-chunk group in flight
+// together.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn_combine(AttnArgs args) {
   extern __shared__ float wsh[];  // [n_active] chunk weights
   __shared__ float sh[16];
   constexpr int DPT = (HD + 255) / 256;
-  constexpr int CG = 16;  // chunk loads in flight per dim
-  const int G = a.n_heads / a.n_kv;
-  int bid = blockIdx.x;
-  const int hq = bid % a.n_heads;
-  bid /= a.n_heads;
-  const int t = bid % a.T;
-  const int b = bid / a.T;
-  const int h = hq / G, g = hq % G;
+  constexpr int CG = HD > 256 ? 16 : 32;  // chunk rows of o loaded in the first batch
+  const AttnP p = load_params(args);
   const int tid = threadIdx.x;
-  const int base = a.pos[b];
+  const int hq = blockIdx.x, t = blockIdx.y, b = blockIdx.z;
+  const int G = p.G;
+  const int h = hq / G, g = hq % G;
+  const int base = aldg<int32_t>(p.pos + b);
   int kmin, kmax, dummy;
-  key_range(a, base, &kmin, &dummy);
-  key_range(a, base + a.T - 1, &dummy, &kmax);
+  key_range(p, base, &kmin, &dummy);
+  key_range(p, base + p.T - 1, &dummy, &kmax);
   const int n_active = (kmax - kmin) / kAttnChunk + 1;
-  const size_t cstride = (size_t)a.T * G * (HD + 2);
-  const float *pg = a.part + (((size_t)b * a.n_kv + h) * a.n_chunks * a.T * G +
+  const size_t cstride = (size_t)p.T * G * (HD + 2);
+  const float *pg = p.part + (((size_t)b * p.n_kv + h) * p.n_chunks * p.T * G +
                               (size_t)t * G + g) * (HD + 2);
+  const int row = b * p.T + t;
+  const int pt = base + t;
+  const bool do_cache =
+      p.write_cache && g == 0 && !(!p.circular && pt >= p.cache_len);
+
+  // every load of this block issued before the reductions: chunk (m, l), the
+  // first 16-chunk group of o values, and the row's K/V for the cache append
   float mloc[2], lloc[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int cc = min(tid + 256 * j, n_active - 1);
-    mloc[j] = pg[cc * cstride + HD];
-    lloc[j] = pg[cc * cstride + HD + 1];
-    if (tid + 256 * j >= n_active) {
-      mloc[j] = -INFINITY;
-      lloc[j] = 0.f;
+    const int cc = tid + 256 * j;
+    mloc[j] = -INFINITY;
+    lloc[j] = 0.f;
+    if (cc < n_active) {
+      mloc[j] = aldg<float>(pg + cc * cstride + HD);
+      lloc[j] = aldg<float>(pg + cc * cstride + HD + 1);
     }
   }
+  float v0[DPT][CG];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j)
+#pragma unroll
+    for (int u = 0; u < CG; ++u) {
+      v0[j][u] = 0.f;
+      const int d = tid + 256 * j;
+      if (d < HD && u < n_active) v0[j][u] = aldg<float>(pg + (size_t)u * cstride + d);
+    }
+  RopeIn kin[DPT];
+  float vin[DPT];
+  if (do_cache) {
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) {
+      const int d = tid + 256 * j;
+      if (d < HD) {
+        rope_load(p, row, p.q_dim + h * HD, d, pt, kin[j]);
+        vin[j] = aldg<float>(p.qkv + (size_t)row * p.ld + p.q_dim + p.kv_dim + h * HD + d);
+      }
+    }
+  }
+
   const float M = block_reduce(fmaxf(mloc[0], mloc[1]), sh, true);
   float wl[2], part = 0.f;
 #pragma unroll
@@ -299,33 +447,40 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
     if (cc < n_active) wsh[cc] = wl[j] * inv;
   }
   __syncthreads();
-  const int row = b * a.T + t;
 #pragma unroll
   for (int j = 0; j < DPT; ++j) {
     const int d = tid + 256 * j;
     if (d < HD) {
       float o = 0.f;
-      for (int c0 = 0; c0 < n_active; c0 += CG) {
+#pragma unroll
+      for (int u = 0; u < CG; ++u)
+        if (u < n_active) o += v0[j][u] * wsh[u];
+      for (int c0 = CG; c0 < n_active; c0 += CG) {
         float v[CG];
 #pragma unroll
-        for (int u = 0; u < CG; ++u) v[u] = pg[(size_t)min(c0 + u, n_active - 1) * cstride + d];
+        for (int u = 0; u < CG; ++u) {
+          v[u] = 0.f;
+          if (c0 + u < n_active) v[u] = aldg<float>(pg + (size_t)(c0 + u) * cstride + d);
+        }
+        // (prefill spans past CG chunks only)
 #pragma unroll
         for (int u = 0; u < CG; ++u)
           if (c0 + u < n_active) o += v[u] * wsh[c0 + u];
       }
-      a.out[(size_t)row * a.q_dim + hq * HD + d] = o;
+      p.out[(size_t)row * p.q_dim + hq * HD + d] = o;
     }
   }
-  if (a.write_cache && g == 0) {
+  if (do_cache) {
     // write_kv_sliding / write_kv_full (gemma4_e4b.mojo:211-249)
-    const int p = base + t;
-    if (!(a.cache_kind == MS_CACHE_LINEAR && p >= a.cache_len)) {
-      float *kc = a.kc + (size_t)b * a.cache_seq_stride;
-      float *vc = a.vc + (size_t)b * a.cache_seq_stride;
-      for (int d = tid; d < HD; d += 256) {
-        const size_t ci = (size_t)cache_slot(a, p) * a.kv_dim + h * HD + d;
-        kc[ci] = rope_val(a, row, a.q_dim + h * HD, d, p);
-        vc[ci] = qkv_val(a, row, a.q_dim + a.kv_dim + h * HD + d);
+    float *kc = p.kc + (size_t)b * p.cache_seq_stride;
+    float *vc = p.vc + (size_t)b * p.cache_seq_stride;
+    const size_t cbase = (size_t)cache_slot(p, pt) * p.kv_dim + h * HD;
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) {
+      const int d = tid + 256 * j;
+      if (d < HD) {
+        kc[cbase + d] = rope_apply(kin[j]);
+        vc[cbase + d] = vin[j];
       }
     }
   }
@@ -341,8 +496,9 @@ int attn_check(const AttnArgs &a) {
                "attention: head_dim must be 128, 256 or 512");
   MS_CHECK_ARG(a.rot % 2 == 0 && a.rot <= a.hd, "attention: bad rotary width");
   MS_CHECK_ARG(a.cache_len > 0, "attention: empty cache");
-  MS_CHECK_ARG(a.n_chunks <= kAttnMaxChunks, "attention: too many key chunks");
+  MS_CHECK_ARG(a.n_chunks >= 1 && a.n_chunks <= kAttnMaxChunks, "attention: bad key chunk count");
   MS_CHECK_ARG(a.ld >= a.q_dim + 2 * a.kv_dim, "attention: q|k|v row stride too small");
+  MS_CHECK_ARG(a.B >= 1 && a.T >= 1, "attention: empty batch");
   return MS_OK;
 }
 
@@ -352,14 +508,20 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
   const int G = a.n_heads / a.n_kv;
   const int TR = std::max(1, std::min(a.T, kAttnMaxTG / G));
   const int RG = (a.T + TR - 1) / TR;
-  const long blocks = (long)a.B * a.n_kv * a.n_chunks * RG;
+  const dim3 grid(a.n_chunks, RG, a.B * a.n_kv);
+  const int TG = TR * G;
   const size_t shmem =
       (size_t)(2 * kAttnChunk * a.hd + kAttnLds + kAttnMaxTG * kAttnChunk + 2 * kAttnMaxTG) * 4;
-  const long cblocks = (long)a.B * a.T * a.n_heads;
+  const dim3 cgrid(a.n_heads, a.T, a.B);
   const size_t cshmem = (size_t)a.n_chunks * 4;
 #define MS_ATTN(HDV)                                                                      \
-  hipLaunchKernelGGL(k_attn_chunks<HDV>, dim3(blocks), dim3(256), shmem, st, a);       \
-  hipLaunchKernelGGL(k_attn_combine<HDV>, dim3(cblocks), dim3(256), cshmem, st, a)
+  if (TG <= 4)                                                                             \
+    hipLaunchKernelGGL((k_attn_chunks<HDV, 4>), grid, dim3(256), shmem, st, a);          \
+  else if (TG <= 8)                                                                        \
+    hipLaunchKernelGGL((k_attn_chunks<HDV, 8>), grid, dim3(256), shmem, st, a);          \
+  else                                                                                     \
+    hipLaunchKernelGGL((k_attn_chunks<HDV, kAttnMaxTG>), grid, dim3(256), shmem, st, a); \
+  hipLaunchKernelGGL(k_attn_combine<HDV>, cgrid, dim3(256), cshmem, st, a)
   switch (a.hd) {
     case 128: MS_ATTN(128); break;
     case 256: MS_ATTN(256); break;
