@@ -188,6 +188,12 @@ int ms_model_destroy(ms_model *m);
 int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_t *src,
                         int src_on_device, float scale);
 int ms_model_set_ple(ms_model *m, int layer, float ple);
+/* Streaming models only: pinned[l] != 0 keeps layer l's weights in HBM; the
+ * two-slot double buffer then streams only the other layers, alternating
+ * slots among them (SparsePinEngine: pinned layers via get_layer_ref, the
+ * skipping prefetcher advance/next_non_pinned, sparse_pin.mojo:88-92,268-330).
+ * Call before binding the weights of any layer whose flag changes. */
+int ms_model_set_pinned(ms_model *m, const uint8_t *pinned);
 /* Tied Q4 LM head (LMHead v1, lm_head.mojo:41-116); h_gamma NULL = ones. */
 int ms_model_set_lm_head(ms_model *m, const uint8_t *src, int src_on_device,
                          float scale, const float *h_gamma);
@@ -219,6 +225,84 @@ int ms_decode_run(ms_model *m, int n_steps, int use_graph, int32_t *h_ids_out);
  * positions h_pos0.. and returns the first greedy id (TTFT path). */
 int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_tokens,
                int pos0, int32_t *h_first_id);
+
+/* Shapes the model was created with; `layers` (n_layers entries) may be NULL.
+ * No reference counterpart (the reference reads its constants directly). */
+int ms_model_get_desc(const ms_model *m, ms_model_desc *desc, ms_layer_desc *layers);
+/* BOS embedding row (LMHead.bos_emb, lm_head.mojo:41-58).  When set, the row
+ * at position 0 of ms_prefill takes it instead of the embedding of its token
+ * (apply_bos_embedding, lm_head.mojo:133-143, used for prompt position 0 by
+ * gemma4_e4b_infer.mojo:94,116-117).  h_bos NULL clears it. */
+int ms_model_set_bos(ms_model *m, const float *h_bos);
+
+/* ---- .mojostream weight files (host side) -------------------------------- */
+/* MojoStreamMeta (mojostream.mojo:47-69) plus the fields the reference parses
+ * but does not keep, and the Engram extension of format tag 2
+ * (convert.py:383-398; zeros when absent). */
+typedef struct {
+  uint32_t version, format_tag, n_layers, hidden, kv_dim, ffn_dim, n_heads,
+      n_kv_heads;
+  uint64_t n_tensors, dir_offset, data_start;
+  uint32_t engram_version, n_kv_shared, sliding_kv_dim, full_kv_dim, ple_dim,
+      sliding_window;
+  uint64_t file_bytes;
+  double load_ms; /* time of the whole-file read */
+} ms_file_meta;
+/* TensorEntry (mojostream.mojo:73-91) with the flags word. */
+typedef struct {
+  uint32_t layer_id, mat_type, rows, cols;
+  float scale;
+  uint32_t flags;
+  uint64_t data_offset;
+} ms_file_entry;
+/* Head size and projection widths of one layer (get_layer_dims,
+ * convert.py:195-225). */
+typedef struct {
+  int is_full, head_dim, q_dim, kv_dim;
+} ms_file_layer;
+typedef struct ms_file ms_file;
+
+/* MojoStreamFile(path) (mojostream.mojo:101-113): one whole-file read, header
+ * and directory parse.  Fails on a missing file, a bad magic (first four
+ * bytes "MOJO") or a header/directory that extends past the end. */
+int ms_file_open(const char *path, ms_file **out);
+int ms_file_close(ms_file *f);
+int ms_file_get_meta(const ms_file *f, ms_file_meta *out);
+int ms_file_get_entry(const ms_file *f, int index, ms_file_entry *out);
+/* Layer-type map used by the guards and loaders: is_full[n_layers] (NULL
+ * restores the default: full attention at (layer+1) % 6 == 0 for a hybrid
+ * file, is_full_attn gemma4_e4b.mojo:60-63; none otherwise). */
+int ms_file_set_layer_types(ms_file *f, const uint8_t *is_full, int n_layers);
+int ms_file_layer_info(const ms_file *f, int layer, ms_file_layer *out);
+/* tensor_ptr (mojostream.mojo:156-175): host pointer into the file buffer,
+ * the tensor's scale and its byte count (0 for PLE entries).  An absent
+ * tensor is MS_E_IO (the reference returns the buffer start, scale 0). */
+int ms_file_tensor(const ms_file *f, int layer, int mat_type,
+                   const uint8_t **h_ptr, float *scale, size_t *bytes);
+/* ple_scale (mojostream.mojo:177-182): 1.0 when there is no entry. */
+int ms_file_ple_scale(const ms_file *f, int layer, float *out);
+/* ShapeGuard (validate_gemma4_shape mojostream.mojo:190-219,
+ * _check_shape stream_runner.mojo:280-309), layer-type-aware. */
+int ms_file_shape_guard(const ms_file *f);
+/* TensorGuard (validate_tensor_entries stream_runner.mojo:313-380): entry
+ * order, per-layer shapes, 4096 alignment, file bounds, scale > 0. */
+int ms_file_tensor_guard(const ms_file *f);
+/* Seeded synthetic .mojostream file (create_fake_model.py:188-281).  Uses
+ * n_layers, hidden, kv_dim, ffn_dim, n_heads, n_kv_heads, and the Engram
+ * fields when engram_version != 0; is_full may be NULL (default map).  The
+ * weights equal those the Python synthetic-model helpers put on the device
+ * for the same seed. */
+int ms_file_write_synthetic(const char *path, const ms_file_meta *hdr,
+                            const uint8_t *is_full, uint64_t seed);
+/* Runs both guards, checks the model's shapes against the file and binds
+ * every matrix and PLE scale (the load loops of run_harness
+ * harness.mojo:80-122 and StreamingRunner stream_runner.mojo:188-270). */
+int ms_model_load_file(ms_model *m, const ms_file *f);
+/* Tied Q4 LM head file, version 1 (load_lm_head lm_head.mojo:61-116): sets
+ * the head (gamma = ones) and the BOS row.  The FP32 version 2 is refused. */
+int ms_model_load_lm_head_file(ms_model *m, const char *path);
+int ms_lm_head_file_write_synthetic(const char *path, int hidden, int vocab,
+                                    uint64_t seed);
 
 /* ---- streaming statistics ------------------------------------------------ */
 typedef struct {

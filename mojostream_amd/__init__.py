@@ -55,6 +55,28 @@ class StreamStats(C.Structure):
                 ("wait_ms", C.c_double), ("total_ms", C.c_double)]
 
 
+class FileMeta(C.Structure):
+    """ms_file_meta: MojoStreamMeta (mojostream.mojo:47-69) + Engram fields."""
+    _fields_ = [(n, C.c_uint32) for n in ("version", "format_tag", "n_layers", "hidden",
+                                          "kv_dim", "ffn_dim", "n_heads", "n_kv_heads")] + \
+               [(n, C.c_uint64) for n in ("n_tensors", "dir_offset", "data_start")] + \
+               [(n, C.c_uint32) for n in ("engram_version", "n_kv_shared", "sliding_kv_dim",
+                                          "full_kv_dim", "ple_dim", "sliding_window")] + \
+               [("file_bytes", C.c_uint64), ("load_ms", C.c_double)]
+
+
+class FileEntry(C.Structure):
+    """ms_file_entry: TensorEntry (mojostream.mojo:73-91)."""
+    _fields_ = [("layer_id", C.c_uint32), ("mat_type", C.c_uint32), ("rows", C.c_uint32),
+                ("cols", C.c_uint32), ("scale", C.c_float), ("flags", C.c_uint32),
+                ("data_offset", C.c_uint64)]
+
+
+class FileLayer(C.Structure):
+    _fields_ = [("is_full", C.c_int), ("head_dim", C.c_int), ("q_dim", C.c_int),
+                ("kv_dim", C.c_int)]
+
+
 _P = C.c_void_p
 _I = C.c_int
 _SZ = C.c_size_t
@@ -91,6 +113,22 @@ _SIGS = {
     "ms_decode_run": [_P, _I, _I, _P],
     "ms_prefill": [_P, _I, _P, _I, _I, _P],
     "ms_model_stream_stats": [_P, C.POINTER(StreamStats)],
+    "ms_model_get_desc": [_P, C.POINTER(ModelDesc), C.POINTER(LayerDesc)],
+    "ms_model_set_bos": [_P, _P],
+    "ms_model_set_pinned": [_P, _P],
+    "ms_file_open": [C.c_char_p, C.POINTER(C.c_void_p)], "ms_file_close": [_P],
+    "ms_file_get_meta": [_P, C.POINTER(FileMeta)],
+    "ms_file_get_entry": [_P, _I, C.POINTER(FileEntry)],
+    "ms_file_set_layer_types": [_P, _P, _I],
+    "ms_file_layer_info": [_P, _I, C.POINTER(FileLayer)],
+    "ms_file_tensor": [_P, _I, _I, C.POINTER(C.c_void_p), C.POINTER(C.c_float),
+                       C.POINTER(C.c_size_t)],
+    "ms_file_ple_scale": [_P, _I, C.POINTER(C.c_float)],
+    "ms_file_shape_guard": [_P], "ms_file_tensor_guard": [_P],
+    "ms_file_write_synthetic": [C.c_char_p, C.POINTER(FileMeta), _P, _U64],
+    "ms_model_load_file": [_P, _P],
+    "ms_model_load_lm_head_file": [_P, C.c_char_p],
+    "ms_lm_head_file_write_synthetic": [C.c_char_p, _I, _I, _U64],
     "ms_prof_enable": [_I],
     "ms_prof_sweep": [_P, _I, _I, C.POINTER(C.c_double), C.POINTER(C.c_double),
                       C.POINTER(C.c_long)],
@@ -307,7 +345,8 @@ class Model:
     """Owner of an ms_model handle."""
 
     def __init__(self, arch: Arch, max_seqs: int = 1, max_rows: int = 1,
-                 max_pos: int = 4096, resident: bool = True):
+                 max_pos: int = 4096, resident: bool = True,
+                 pinned: Optional[Sequence[bool]] = None):
         self.arch = arch
         self.max_seqs, self.max_rows, self.max_pos = max_seqs, max_rows, max_pos
         desc = ModelDesc(hidden=arch.hidden, ffn=arch.ffn, n_layers=arch.n_layers,
@@ -318,6 +357,16 @@ class Model:
         check(_lib.ms_model_create(C.byref(desc), arr, C.byref(h)))
         self.h = h.value
         self._pinned: List[int] = []
+        if pinned is not None:
+            flags = np.asarray(pinned, dtype=np.uint8)
+            if flags.size != arch.n_layers:
+                self.close()
+                raise MSError(f"pinned: need {arch.n_layers} flags, got {flags.size}")
+            try:
+                check(_lib.ms_model_set_pinned(self.h, flags.ctypes.data))
+            except MSError:
+                self.close()
+                raise
 
     def close(self) -> None:
         if self.h:
@@ -388,6 +437,30 @@ class Model:
 
     def reset(self) -> None:
         check(_lib.ms_model_reset(self.h))
+
+    def set_bos(self, bos: Optional[np.ndarray]) -> None:
+        """BOS row for prompt position 0 (apply_bos_embedding, lm_head.mojo:133-143)."""
+        if bos is None:
+            check(_lib.ms_model_set_bos(self.h, None))
+            return
+        b = np.ascontiguousarray(bos, dtype=np.float32)
+        if b.size != self.arch.hidden:
+            raise MSError(f"set_bos: need {self.arch.hidden} values, got {b.size}")
+        check(_lib.ms_model_set_bos(self.h, b.ctypes.data))
+
+    def load_file(self, f) -> None:
+        """Guards + bind every matrix and PLE scale of a MojoStreamFile."""
+        check(_lib.ms_model_load_file(self.h, f.h))
+
+    def load_lm_head_file(self, path: str) -> None:
+        """Tied Q4 head, version 1 (load_lm_head, lm_head.mojo:61-116)."""
+        check(_lib.ms_model_load_lm_head_file(self.h, os.fsencode(path)))
+
+    def get_desc(self):
+        d = ModelDesc()
+        arr = (LayerDesc * self.arch.n_layers)()
+        check(_lib.ms_model_get_desc(self.h, C.byref(d), arr))
+        return d, list(arr)
 
     def layer_forward(self, layer: int, x: np.ndarray, base: Sequence[int], T: int) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -48,6 +48,7 @@ struct Layer {
   size_t cache_seq_stride = 0;
   int rope = 0;
   int n_chunks = 1;
+  int pinned = 0;  // streaming models: weights kept in HBM, never copied per call
 };
 
 // profiling classes
@@ -89,6 +90,8 @@ struct ms_model {
   float lm_scale = 0.f;
   float *gamma = nullptr;
   bool has_lm = false;
+  float *bos = nullptr;      // BOS embedding row for prompt position 0, or null
+  float *bos_buf = nullptr;  // device storage of that row
   // workspaces
   // rows between kernels: x_in (embeddings), xs (layer output), xn and x2n
   // (normalised attention / FFN inputs, the residual bases), x2 (after O)
@@ -393,10 +396,9 @@ static int enqueue_output(ms_model *m, const RunCfg &rc, hipStream_t st) {
 }
 
 // ---- streaming: two HBM slots filled on the copy stream ----------------------
-// Copies layer l's packed weights into slot l%2 once the layer that used the
-// slot before has finished; a/b bracket the copies on the copy stream.
-static int stream_prefetch(ms_model *m, int l, hipEvent_t a, hipEvent_t b) {
-  const int s = l & 1;
+// Copies layer l's packed weights into slot s once the streamed layer that
+// used the slot before has finished; a/b bracket the copies on the copy stream.
+static int stream_prefetch(ms_model *m, int l, int s, hipEvent_t a, hipEvent_t b) {
   Layer &Ly = m->L[l];
   MS_HIP_TRY(hipStreamWaitEvent(ctx().copy_stream, m->ev_free[s], 0));
   MS_HIP_TRY(hipEventRecord(a, ctx().copy_stream));
@@ -425,12 +427,20 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
     MS_HIP_TRY(hipEventRecord(m->ev_free[0], st));
     MS_HIP_TRY(hipEventRecord(m->ev_free[1], st));
     std::vector<hipEvent_t> cp0, cp1, w0, w1;
+    int n_streamed = 0;
     for (int l = l0; l < l1; ++l) {
+      if (m->L[l].pinned) {
+        // pinned layer (SparsePinEngine.get_layer_ref, sparse_pin.mojo:295-330):
+        // weights already in HBM; the copy stream moves on to the next
+        // streamed layer while this one computes
+        if (int r = enqueue_layer(m, l, rc, st)) return r;
+        continue;
+      }
+      const int s = n_streamed++ & 1;
       hipEvent_t a = mk(), b = mk();
-      if (int r = stream_prefetch(m, l, a, b)) return r;
+      if (int r = stream_prefetch(m, l, s, a, b)) return r;
       cp0.push_back(a);
       cp1.push_back(b);
-      const int s = l & 1;
       hipEvent_t c = mk(), e = mk();
       MS_HIP_TRY(hipEventRecord(c, st));
       MS_HIP_TRY(hipStreamWaitEvent(st, m->ev_ready[s], 0));
@@ -652,7 +662,7 @@ extern "C" int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_
   const int K[7] = {D, D, D, Ly.d.q_dim, D, D, F};
   const int N[7] = {Ly.d.q_dim, Ly.d.kv_dim, Ly.d.kv_dim, D, F, F, D};
   hipStream_t st = ctx().stream;
-  if (m->d.resident) {
+  if (m->d.resident || Ly.pinned) {
     if (!Ly.w[mat]) {
       int rc = dmalloc(m, (void **)&Ly.w[mat], Ly.bytes[mat]);
       if (rc) return rc;
@@ -687,6 +697,17 @@ extern "C" int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_
   return MS_OK;
 }
 
+extern "C" int ms_model_set_pinned(ms_model *m, const uint8_t *pinned) {
+  MS_CHECK_ARG(m && pinned, "set_pinned: null argument");
+  MS_CHECK_ARG(!m->d.resident, "set_pinned: resident models keep every layer in HBM");
+  for (size_t l = 0; l < m->L.size(); ++l)
+    if ((pinned[l] != 0) != (m->L[l].pinned != 0) && m->L[l].set_mask)
+      return fail(MS_E_STATE, "set_pinned: layer " + std::to_string(l) +
+                                  " already has weights; pin layers before binding them");
+  for (size_t l = 0; l < m->L.size(); ++l) m->L[l].pinned = pinned[l] != 0;
+  return MS_OK;
+}
+
 extern "C" int ms_model_set_ple(ms_model *m, int layer, float ple) {
   MS_CHECK_ARG(m && layer >= 0 && layer < (int)m->L.size(), "set_ple: bad layer");
   MS_CHECK_ARG(ple > 0.f && std::isfinite(ple), "set_ple: PLE scale must be > 0");
@@ -695,6 +716,28 @@ extern "C" int ms_model_set_ple(ms_model *m, int layer, float ple) {
     (void)hipGraphExecDestroy(m->gexec);
     m->gexec = nullptr;
   }
+  return MS_OK;
+}
+
+extern "C" int ms_model_get_desc(const ms_model *m, ms_model_desc *desc, ms_layer_desc *layers) {
+  MS_CHECK_ARG(m && desc, "get_desc: null argument");
+  *desc = m->d;
+  if (layers)
+    for (size_t l = 0; l < m->L.size(); ++l) layers[l] = m->L[l].d;
+  return MS_OK;
+}
+
+extern "C" int ms_model_set_bos(ms_model *m, const float *h_bos) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m, "set_bos: null model");
+  m->bos = nullptr;
+  if (!h_bos) return MS_OK;
+  if (!m->bos_buf)
+    if (int rc = dmalloc(m, (void **)&m->bos_buf, (size_t)m->d.hidden * 4)) return rc;
+  MS_HIP_TRY(hipMemcpyAsync(m->bos_buf, h_bos, (size_t)m->d.hidden * 4, hipMemcpyHostToDevice,
+                            ctx().stream));
+  MS_HIP_TRY(hipStreamSynchronize(ctx().stream));
+  m->bos = m->bos_buf;
   return MS_OK;
 }
 
@@ -899,6 +942,8 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
     MS_HIP_TRY(hipMemcpyAsync(m->pos + seq, &base, 4, hipMemcpyHostToDevice, st));
     if ((rcode = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, dtok + c0, t, m->x_in, st)))
       break;
+    if (m->bos && base == 0)
+      MS_HIP_TRY(hipMemcpyAsync(m->x_in, m->bos, (size_t)D * 4, hipMemcpyDeviceToDevice, st));
     RunCfg rc{};
     rc.B = 1;
     rc.T = t;
