@@ -492,8 +492,8 @@ int attn_check(const AttnArgs &a) {
   MS_CHECK_ARG(G <= kAttnMaxTG, "attention: GQA group too large");
   const int TR = std::max(1, std::min(a.T, kAttnMaxTG / G));
   MS_CHECK_ARG(TR * G * a.hd <= kAttnLds, "attention: q staging exceeds LDS budget");
-  MS_CHECK_ARG(a.hd == 128 || a.hd == 256 || a.hd == 512,
-               "attention: head_dim must be 128, 256 or 512");
+  MS_CHECK_ARG(a.hd == 64 || a.hd == 128 || a.hd == 256 || a.hd == 512,
+               "attention: head_dim must be 64, 128, 256 or 512");
   MS_CHECK_ARG(a.rot % 2 == 0 && a.rot <= a.hd, "attention: bad rotary width");
   MS_CHECK_ARG(a.cache_len > 0, "attention: empty cache");
   MS_CHECK_ARG(a.n_chunks >= 1 && a.n_chunks <= kAttnMaxChunks, "attention: bad key chunk count");
@@ -523,6 +523,7 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
     hipLaunchKernelGGL((k_attn_chunks<HDV, kAttnMaxTG>), grid, dim3(256), shmem, st, a); \
   hipLaunchKernelGGL(k_attn_combine<HDV>, cgrid, dim3(256), cshmem, st, a)
   switch (a.hd) {
+    case 64: MS_ATTN(64); break;
     case 128: MS_ATTN(128); break;
     case 256: MS_ATTN(256); break;
     default: MS_ATTN(512); break;

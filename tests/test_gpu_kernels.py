@@ -139,6 +139,8 @@ ATTN_CASES = [
     ("full-e4b", 4096, 1024, 512, 8, 2, 0, 4096, 1, 1, 383),
     ("full-clamp", 4096, 1024, 512, 8, 2, 0, 256, 1, 2, 300),
     ("demo", 1024, 256, 128, 8, 2, 0, 512, 0, 4, 400),
+    # first_light / create_fake_model dims: 16 q / 4 kv heads of 64 (main.mojo:225-227)
+    ("g4-hd64", 1024, 256, 64, 16, 4, 0, 256, 0, 4, 200),
     ("14b", 5120, 1024, 128, 40, 8, 0, 4096, 0, 1, 4000),
     ("first-token", 2048, 512, 256, 8, 2, 1, 512, 0, 1, 0),
 ]

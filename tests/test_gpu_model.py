@@ -112,7 +112,7 @@ def test_e4b_full_per_layer_hidden(gpu, fast_oracle):
 def test_e4b_full_greedy_ids(gpu, fast_oracle):
     ms = gpu
     arch = ms.arch_e4b(max_full_seq=512)
-    n_steps = int(os.environ.get("MS_GREEDY_STEPS", "12"))
+    n_steps = int(os.environ.get("MS_GREEDY_STEPS", "100"))
     say(f"E4B 42 layers + vocab 262144: prefill 6 + greedy {n_steps} steps")
     m = build(ms, arch, max_seqs=1, max_rows=16, max_pos=512)
     om = synthetic_oracle_model(fast_oracle, arch, SEED)
