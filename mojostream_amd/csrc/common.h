@@ -63,10 +63,11 @@ __host__ __device__ inline uint64_t rand_word(uint64_t seed, uint64_t stream,
 // 128G..128G+127; lane l (0..63) owns 16 bytes at offset 16*l holding the 32
 // nibbles of column 16*nb + (l%16), rows 128G + 32*(l/16) + 0..31.  Dword t
 // (0..3) of those 16 bytes covers rows +8t..+8t+7; row offset e (0..7) sits in
-// nibble q(e) = (e>>1) + 4*(e&1), so one dword yields four fp16x2 pairs
-// (rows e, e+1) with one bit-op each.  This is the B operand layout of
-// v_mfma_f32_16x16x32_f16 (B[k][j]: lane j + 16*(k/8), element k%8) with MFMA
-// k-block t of super-tile G mapped to rows 128G + 32*(l/16) + 8t + e.
+// nibble q(e) = (e>>1) + 4*(e&1).  Dwords 2h and 2h+1 are the B operand of
+// MFMA h of the super-tile for v_mfma_i32_16x16x64_i8 (B[k][j]: lane
+// j + 16*(k/16), byte k%16): their low nibbles and their high nibbles, each
+// masked to bytes, give rows {0,4,1,5} / {2,6,3,7} of each 8-row group, an
+// order the activation operand is stored in to match.
 constexpr int kPanelCols = 16;
 // Threads per block of the simple 1-D kernels.  Device code uses this
 // constant rather than blockDim, whose value is loaded from the dispatch packet.

@@ -23,9 +23,9 @@ enum GemvEpilogue {
 
 // Activation rows enter the MFMA as four signed int8 limbs of a per-row
 // fixed-point value X = rint(y * 2^s), |X| < 2^30:  y * 2^s = sum_l limb_l 2^(8l).
-// The weights enter as their raw nibbles n (0..15), so the integer dot product
-// sum_k X_k (n_k - 8) = sum_k X_k n_k - 8 sum_k X_k is exact; it is scaled by
-// 2^-s and the tensor scale once per output.
+// The weights enter as signed bytes n - 8 (n the nibble), so each limb's
+// integer dot product sum_k limb_l(k) (n_k - 8) is exact in int32; the limbs
+// are combined in int64 and scaled by 2^-s and the tensor scale once per output.
 enum GemvASource {
   AS_ROWS = 0,   // prologue: every block quantizes the fp32 rows into LDS
   AS_QUANT = 1,  // limbs prepared in global memory by launch_quant_rows
@@ -45,11 +45,10 @@ struct RowSrc {
 
 // Quantized rows in global memory: limb l of row m at
 // limbs[(4m + l) * K + limb position of k] (MFMA fragment order per 128-row
-// super-tile), shift[m] = s, xsum[m] = sum_k X_k.
+// super-tile), shift[m] = s.
 struct QuantRows {
   int8_t *limbs;
   int32_t *shift;
-  long long *xsum;
 };
 
 struct GemvArgs {
@@ -93,7 +92,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t st);
 size_t gemv_lds_need(const GemvArgs &a);
 // Quantize M rows of length K (one block per row) into q.
 int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st);
-// Device bytes of a QuantRows buffer for M rows of length K (limbs, shifts, sums).
+// Device bytes of a QuantRows buffer for M rows of length K (limbs, shifts).
 size_t quant_rows_bytes(int M, int K);
 // Carve a QuantRows view out of one buffer of quant_rows_bytes(M, K).
 QuantRows quant_rows_view(void *buf, int M, int K);

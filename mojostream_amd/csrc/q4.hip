@@ -112,20 +112,36 @@ __device__ inline T launder(T v) {
   return v;
 }
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Wave reductions: DPP moves inside each 16-lane row (quad permutes, then
+// the half-row and row mirrors leave the row total in every lane of the row),
+// then readlane of the four row totals.  The result is wave-uniform.  No LDS
+// round trips (a shuffle through ds_bpermute costs an LDS access and a wait
+// per step).
+template <int CTRL>
+__device__ inline float dpp_f(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float lane_f(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ inline float row_sum16(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
   return v;
+}
+__device__ inline float wave_sum(float v) {
+  v = row_sum16(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 __device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ inline double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Block reductions over NT threads; every thread returns the result.
@@ -156,18 +172,6 @@ __device__ inline float block_max(float v, float *sh) {
   for (int i = 1; i < nw; ++i) t = fmaxf(t, sh[i]);
   return t;
 }
-template <int NT>
-__device__ inline double block_sum_d(double v, double *sh) {
-  constexpr int nw = NT / 64;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  v = wave_sum_d(v);
-  __syncthreads();
-  if (lane == 0) sh[w] = v;
-  __syncthreads();
-  double t = 0.0;
-  for (int i = 0; i < nw; ++i) t += sh[i];
-  return t;
-}
 
 // ------------------------------------------------------------------------------
 // Row quantization.
@@ -176,7 +180,8 @@ __device__ inline double block_sum_d(double v, double *sh) {
 // super-tile, lane group g of the B operand holds rows 32g..32g+31 of its
 // column, dword t = rows 8t..8t+7 with row e in nibble (e>>1) + 4(e&1).  The
 // B fragment of MFMA h (two per super-tile) is the four dwords
-// [d & 0x0F0F0F0F, (d >> 4) & 0x0F0F0F0F] of dwords t = 2h and 2h+1, so byte b
+// [d & 0x0F0F0F0F, (d >> 4) & 0x0F0F0F0F] of dwords t = 2h and 2h+1 (each byte
+// then mapped to the signed value n - 8), so byte b
 // of the low/high word holds rows e = {0,4,1,5} / {2,6,3,7}.  The A limbs are
 // stored in that same order: an 8-row group t of lane group g lands at byte
 // 128G + 32g + 16(t>>1) + 8(t&1), low word then high word.
@@ -186,7 +191,7 @@ __device__ inline int limb_pos8(int k) {
 }
 
 // X = rint(v * mul) for eight consecutive rows; limb l of the group as its
-// low/high words.  Returns sum X.
+// low/high words.
 //
 // For |X| < 2^30 the bytes of E = (X + 0x80808080) ^ 0x80808080 are the four
 // balanced limbs of X: X + 0x80808080 = sum_l u_l 2^(8l) with bytes u_l, so
@@ -199,14 +204,12 @@ __device__ inline uint32_t byte_gather(uint32_t a, uint32_t b, uint32_t c, uint3
          (((d >> sh) & 0xFFu) << 24);
 }
 
-__device__ inline long long quant8(const float (&v)[8], float mul, uint32_t (&lo)[4],
-                                   uint32_t (&hi)[4]) {
+__device__ inline void quant8(const float (&v)[8], float mul, uint32_t (&lo)[4],
+                              uint32_t (&hi)[4]) {
   uint32_t E[8];
-  long long xs = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int x = (int)rintf(v[e] * mul);
-    xs += x;
     E[e] = ((uint32_t)x + 0x80808080u) ^ 0x80808080u;
   }
 #pragma unroll
@@ -214,7 +217,6 @@ __device__ inline long long quant8(const float (&v)[8], float mul, uint32_t (&lo
     lo[l] = byte_gather(E[0], E[4], E[1], E[5], l);
     hi[l] = byte_gather(E[2], E[6], E[3], E[7], l);
   }
-  return xs;
 }
 
 // Per-row shift s with max|y| * 2^s < 2^30.
@@ -288,12 +290,11 @@ __device__ inline void block_sum_max(float &ss, float &mx, float *sh) {
 // Transform (x * pre_scale, rmsnorm, gamma: rmsnorm_inplace kernels.mojo:474-489,
 // ple_scale_inplace :506-516, rmsnorm_weighted_inplace :598-613), optional
 // fp32 stores by `writer`, quantization and limb stores: limb l of row m goes
-// to dst + (4m + l) * ld_dst + limb position.  Returns the row shift s and the
-// calling wave's part of sum X (summed over the waves by the caller).
+// to dst + (4m + l) * ld_dst + limb position.  Returns the row shift s.
 template <int NT, int NG, bool GAM>
 __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
                                   RowRegs<NT, NG, GAM> &R, int8_t *dst, size_t ld_dst,
-                                  float *sh, int *s_out, double *xs_wave) {
+                                  float *sh, int *s_out) {
   const int nq = K >> 3;
   float y[NG][8];
   float ss = 0.f, mx = 0.f;
@@ -334,7 +335,6 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
   }
   const int s = row_shift(amax);
   const float mul = ldexpf(1.0f, s);
-  long long xs = 0;
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     const int q = (int)threadIdx.x + gi * NT;
@@ -353,38 +353,28 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
       }
     }
     uint32_t lo[4], hi[4];
-    xs += quant8(y[gi], mul, lo, hi);
+    quant8(y[gi], mul, lo, hi);
     const int pos = limb_pos8(8 * q);
 #pragma unroll
     for (int l = 0; l < 4; ++l)
       *reinterpret_cast<uint2 *>(dst + (size_t)(4 * m + l) * ld_dst + pos) = uint2{lo[l], hi[l]};
   }
   *s_out = s;
-  *xs_wave = wave_sum_d((double)xs);  // |sum| < 2^44: exact in double
 }
 
 template <bool GAM>
 __global__ __launch_bounds__(1024) void k_quant_rows(RowSrc r, int K, QuantRows q) {
   __shared__ float sh[32];
-  __shared__ double shd[16];
   RowRegs<1024, 2, GAM> R;
   const int m = blockIdx.x;
   row_load<1024, 2, GAM>(r, K, m, R);
   int s;
-  double xw;
-  row_finish<1024, 2, GAM>(r, K, m, true, R, q.limbs, K, sh, &s, &xw);
-  if ((threadIdx.x & 63) == 0) shd[threadIdx.x >> 6] = xw;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double t = 0.0;
-    for (int w = 0; w < 16; ++w) t += shd[w];
-    q.shift[m] = s;
-    q.xsum[m] = (long long)t;
-  }
+  row_finish<1024, 2, GAM>(r, K, m, true, R, q.limbs, K, sh, &s);
+  if (threadIdx.x == 0) q.shift[m] = s;
 }
 
 size_t quant_rows_bytes(int M, int K) {
-  return (size_t)4 * M * K + (size_t)M * 4 + 64 + (size_t)M * 8 + 64;
+  return (size_t)4 * M * K + 64 + (size_t)M * 4;
 }
 
 QuantRows quant_rows_view(void *buf, int M, int K) {
@@ -393,15 +383,13 @@ QuantRows quant_rows_view(void *buf, int M, int K) {
   q.limbs = reinterpret_cast<int8_t *>(b);
   const size_t o1 = ((size_t)4 * M * K + 63) & ~(size_t)63;
   q.shift = reinterpret_cast<int32_t *>(b + o1);
-  const size_t o2 = (o1 + (size_t)M * 4 + 63) & ~(size_t)63;
-  q.xsum = reinterpret_cast<long long *>(b + o2);
   return q;
 }
 
 int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st) {
   MS_CHECK_ARG(M >= 1 && K >= 8 && K % 8 == 0 && K <= kQuantMaxK,
                "quant: row length must be a multiple of 8 in [8, 16384]");
-  MS_CHECK_ARG(r.x && r.ld >= K && q.limbs && q.shift && q.xsum, "quant: missing buffers");
+  MS_CHECK_ARG(r.x && r.ld >= K && q.limbs && q.shift, "quant: missing buffers");
   if (r.gamma)
     hipLaunchKernelGGL(k_quant_rows<true>, dim3(M), dim3(1024), 0, st, r, K, q);
   else
@@ -446,27 +434,34 @@ __device__ inline void gemv_slot(const uint8_t *w0, const uint8_t *w1, const uin
   }
 }
 
+// Low nibbles of the four bytes of d as signed bytes n - 8 (the Q4 zero point
+// folded into the operand): n + 0x78 stays inside its byte for n <= 15, and
+// flipping bit 7 turns it into the two's complement of n - 8.
+__device__ inline int nib_s8(uint32_t d) {
+  return (int)(((d & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
+}
+
 // D fragment index of output row i, column j (v_mfma_*_16x16x* layout:
 // lane j + 16*(i/4), element i%4).
 __device__ inline int dfrag(int i, int j) { return (j + 16 * (i >> 2)) * 4 + (i & 3); }
 
 // Super-tiles each wave keeps in flight per batch: A fragments of a global-A
-// GEMV live in registers next to the weights, so it holds fewer.
+// GEMV live in registers next to the weights, so it holds fewer.  Ten per
+// wave lets the decode shapes (E4B gate|up: 5 per panel at W = 4) finish
+// in one batch.
 template <int C, int P, int AS>
 constexpr int gemv_batch() {
-  constexpr int u = (AS == AS_QUANT ? 4 / C : 8 / C) / P;
+  constexpr int u = (AS == AS_QUANT ? 4 / C : 10 / C) / P;
   return u < 1 ? 1 : u;
 }
 
 // LDS layout: int partial sums [W][P][C][256], output values [P][M][16],
-// per-row shift and sum, then (AS_ROWS) limb rows [4M][K + 16].
+// per-row shift, then (AS_ROWS) limb rows [4M][K + 16] (16-byte aligned).
 __host__ __device__ inline size_t gemv_lds_red(int W, int P, int C) {
   return (size_t)W * P * C * 256 * 4;
 }
 __host__ __device__ inline size_t gemv_lds_fixed(int W, int P, int C, int M) {
-  // + per row: shift (int) and W partial sums (double); + per row scale (double)
-  return gemv_lds_red(W, P, C) + (size_t)P * M * 16 * 4 + (size_t)kGemvMaxM * 4 +
-         (size_t)kGemvMaxM * 16 * 8 + (size_t)kGemvMaxM * 8;
+  return gemv_lds_red(W, P, C) + (size_t)P * M * 16 * 4 + (size_t)kGemvMaxM * 4;
 }
 __host__ __device__ inline int gemv_ldl(int K) { return K + 16; }
 
@@ -486,7 +481,10 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
   __shared__ float sh[32];
   constexpr int NT = 64 * W;
   constexpr int U = gemv_batch<C, P, AS>();
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave-uniform in a scalar register: tile predicates below are then scalar
+  // branches, and loads behind them need no merge (and no wait) at the join
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   // Every launch parameter the kernel uses is read here, in one batch: uses
   // further down would otherwise become dependent argument loads.
   const int K = launder(a.K), M = launder(a.M);
@@ -520,7 +518,6 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
   } else {
     qr.limbs = launder(a.q.limbs);
     qr.shift = launder(a.q.shift);
-    qr.xsum = launder(a.q.xsum);
   }
 
   const int KG = K / kSuperK;
@@ -539,7 +536,6 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
   int32_t *red = reinterpret_cast<int32_t *>(lds);
   float *vals = reinterpret_cast<float *>(lds + gemv_lds_red(W, P, C));
   int32_t *row_s = reinterpret_cast<int32_t *>(lds + gemv_lds_red(W, P, C) + (size_t)P * M * 64);
-  double *row_xs = reinterpret_cast<double *>(row_s + kGemvMaxM);  // [kGemvMaxM][16]
   int8_t *limbs = reinterpret_cast<int8_t *>(lds + gemv_lds_fixed(W, P, C, M));
   const int ldl = gemv_ldl(K);
 
@@ -551,14 +547,20 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
 
   uint4 q[U][P];
   v4i af[AS == AS_QUANT ? U : 1][C][2];
-  auto issue = [&](int bt) {
+  // Loads of super-tiles u0..u1-1 of batch bt; tiles past the end of K are
+  // not loaded (their slots stay zero and are never consumed).
+  auto issue_part = [&](int bt, int u0, int u1) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int Gu = min(wave + (bt * U + u) * W, KG - 1);
+      if (u < u0 || u >= u1) continue;
+      const int Gu = wave + (bt * U + u) * W;
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        const u32x4 v = ldg<u32x4>(wl[p] + (size_t)Gu * 1024 + lane * 16);
-        q[u][p] = uint4{v.x, v.y, v.z, v.w};
+        q[u][p] = uint4{0u, 0u, 0u, 0u};
+        if (Gu < KG) {
+          const u32x4 v = ldg<u32x4>(wl[p] + (size_t)Gu * 1024 + lane * 16);
+          q[u][p] = uint4{v.x, v.y, v.z, v.w};
+        }
       }
       if constexpr (AS == AS_QUANT) {
 #pragma unroll
@@ -574,30 +576,30 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
       }
     }
   };
+  auto issue = [&](int bt) { issue_part(bt, 0, U); };
 
   // ---- prologue: activation limbs, overlapping the first weight batch
-  // row_xs[m][w]: wave w's part of sum X for row m (AS_QUANT: the whole sum in w = 0)
   if constexpr (AS == AS_ROWS) {
+    // The row is tiny next to the weights, but its loads queue behind every
+    // weight load already in flight on the chip.  Only one super-tile per
+    // panel goes out before the row has arrived; the rest of the first batch
+    // follows, overlapping the norm and the quantization.
     RowRegs<NT, rows_ng(W), false> R;
     row_load<NT, rows_ng(W), false>(rs, K, 0, R);
-    issue(0);
+    issue_part(0, 0, 1);
+    asm volatile("" ::"v"(R.v[0][0]), "v"(R.v[rows_ng(W) - 1][7]) : "memory");
+    issue_part(0, 1, U);
     int s;
-    double xw;
-    row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s, &xw);
-    if (lane == 0) row_xs[wave] = xw;
+    row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s);
     if (threadIdx.x == 0) row_s[0] = s;
     for (int m = 1; m < M; ++m) {
       row_load<NT, rows_ng(W), false>(rs, K, m, R);
-      row_finish<NT, rows_ng(W), false>(rs, K, m, blockIdx.x == 0, R, limbs, ldl, sh, &s, &xw);
-      if (lane == 0) row_xs[m * 16 + wave] = xw;
+      row_finish<NT, rows_ng(W), false>(rs, K, m, blockIdx.x == 0, R, limbs, ldl, sh, &s);
       if (threadIdx.x == 0) row_s[m] = s;
     }
     __syncthreads();
   } else {
-    if ((int)threadIdx.x < M) {
-      row_s[threadIdx.x] = ldg<int32_t>(qr.shift + threadIdx.x);
-      row_xs[threadIdx.x * 16] = (double)ldg<long long>(qr.xsum + threadIdx.x);
-    }
+    if ((int)threadIdx.x < M) row_s[threadIdx.x] = ldg<int32_t>(qr.shift + threadIdx.x);
     issue(0);
   }
 
@@ -632,8 +634,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const uint32_t d0 = dw[2 * h], d1 = dw[2 * h + 1];
-            const v4i b = v4i{(int)(d0 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu),
-                              (int)(d1 & 0x0F0F0F0Fu), (int)((d1 >> 4) & 0x0F0F0F0Fu)};
+            const v4i b = v4i{nib_s8(d0), nib_s8(d0 >> 4), nib_s8(d1), nib_s8(d1 >> 4)};
 #pragma unroll
             for (int c = 0; c < C; ++c) {
               const v4i av = (AS == AS_QUANT) ? af[u][c][h] : al[c][h];
@@ -654,9 +655,10 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
     }
   __syncthreads();
 
-  // output (slot p, row m, column j): sum the waves per limb row (exact int32),
-  // combine the limbs and the -8 offset in int64, scale once.  Loops over the
-  // slot are unrolled so every per-slot value is a compile-time index.
+  // output (slot p, row m, column j): sum the waves per limb row (exact int32:
+  // |limb * (n - 8)| <= 1024 per term, K <= 16384), combine the limbs in
+  // int64, scale once.  Loops over the slot are unrolled so every per-slot
+  // value is a compile-time index.
 #pragma unroll
   for (int p = 0; p < P; ++p)
     for (int o = threadIdx.x; o < M * 16; o += NT) {
@@ -670,10 +672,6 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
           d += red[(((size_t)w * P + p) * C + c) * 256 + dfrag(r0 + l, j)];
         t += (long long)d << (8 * l);
       }
-      double xs = row_xs[m * 16];
-      if (AS == AS_ROWS)
-        for (int w = 1; w < W; ++w) xs += row_xs[m * 16 + w];
-      t -= 8 * (long long)xs;
       vals[p * M * 16 + o] = (float)((double)t * (double)ldexpf(1.0f, -row_s[m]) * (double)wsc[p]);
     }
   __syncthreads();
@@ -808,7 +806,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
                  "GEMV: row prologue needs rows (no gamma)");
     MS_CHECK_ARG(a.K <= 8 * rows_ng(a.waves) * 64 * a.waves, "GEMV: row prologue: row too long");
   } else {
-    MS_CHECK_ARG(a.q.limbs && a.q.shift && a.q.xsum, "GEMV: quantized rows missing");
+    MS_CHECK_ARG(a.q.limbs && a.q.shift, "GEMV: quantized rows missing");
   }
   long n_panels = 0;
   for (int i = 0; i < a.nseg; ++i) {
