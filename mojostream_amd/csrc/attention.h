@@ -34,4 +34,12 @@ constexpr int kAttnMaxChunks = 512;
 int launch_attention(const AttnArgs &a, hipStream_t st);
 int attn_check(const AttnArgs &a);
 
+// Prefill attention for one sequence (B = 1) and many rows: RoPE of the rows'
+// q and k into qr [T][q_dim] / kr [T][kv_dim], a flash-attention pass on fp32
+// MFMA (one block per 16 rows and kv head, one wave per query head), then the
+// cache append of the rows.  Needs 4 query heads per kv head and head_dim
+// 128, 256 or 512 (prefill_flash_ok); a.part is not used.
+bool prefill_flash_ok(const AttnArgs &a);
+int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, hipStream_t st);
+
 }  // namespace ms

@@ -533,4 +533,281 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
   return MS_OK;
 }
 
+
+// ------------------------------------------------------------------------------
+// Prefill attention: many rows of one sequence.
+//
+//  k_rope_rows      q and k of every row after RoPE (qr, kr).
+//  k_flash_prefill  one block per (16 rows, kv head), wave g = query head
+//                   h*4 + g.  Keys in tiles of 16: K (row pitch HD + 4) and V
+//                   transposed (V^T, pitch 20) staged in LDS, the next tile's
+//                   loads in registers while the current one computes.
+//                   S = Q K^T and O += P V on v_mfma_f32_16x16x4f32 (fp32
+//                   products, fp32 sums); online softmax with DPP row
+//                   reductions (the 16 keys of a score row sit in one 16-lane
+//                   row of the C fragment).  Keys older than the rows come
+//                   from the cache, the rows' own keys from kr / qkv.
+//  k_cache_append   the rows' k (after RoPE) and v into the cache, after every
+//                   block has read it (a circular window must not lose a key
+//                   an earlier row still needs).
+// The dot product runs over the head dims in the order d = 16u + 4c + r for
+// MFMA step 4u + r and k-group c, the same for q and k, so each lane loads its
+// q as float4 and reads K with one 16-byte LDS load per four steps.
+// ------------------------------------------------------------------------------
+typedef float af32x4 __attribute__((ext_vector_type(4)));
+
+template <int CTRL>
+__device__ inline float adpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// max / sum over the 16 lanes of each row of the wave (quad permutes, then the
+// half-row and row mirrors); every lane of the row gets the result
+__device__ inline float row16_max(float v) {
+  v = fmaxf(v, adpp<0xB1>(v));
+  v = fmaxf(v, adpp<0x4E>(v));
+  v = fmaxf(v, adpp<0x141>(v));
+  return fmaxf(v, adpp<0x140>(v));
+}
+__device__ inline float row16_sum(float v) {
+  v += adpp<0xB1>(v);
+  v += adpp<0x4E>(v);
+  v += adpp<0x141>(v);
+  return v + adpp<0x140>(v);
+}
+
+__global__ __launch_bounds__(256) void k_rope_rows(AttnArgs args, float *qr, float *kr, int hd) {
+  const AttnP p = load_params(args);
+  const int r = blockIdx.x;
+  const int pos = aldg<int32_t>(p.pos) + r;
+  const int nq = p.q_dim, nall = p.q_dim + p.kv_dim;
+#pragma unroll 4
+  for (int e = threadIdx.x; e < nall; e += 256) {
+    const bool isq = e < nq;
+    const int ee = isq ? e : e - nq;
+    const int head = ee / hd, d = ee - head * hd;
+    RopeIn ri;
+    rope_load(p, r, (isq ? 0 : nq) + head * hd, d, pos, ri);
+    const float v = rope_apply(ri);
+    if (isq)
+      qr[(size_t)r * nq + ee] = v;
+    else
+      kr[(size_t)r * p.kv_dim + ee] = v;
+  }
+}
+
+// DS waves per query head, each with 1/DS of the head dims (its q and o in
+// registers); their partial scores meet in LDS.
+template <int HD, int DS>
+constexpr int flash_lds_floats() {
+  return 16 * (HD + 4) + HD * 20 + 4 * DS * 16 * 20 + (DS > 1 ? 4 * DS * 256 : 0);
+}
+
+template <int HD, int DS>
+__global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const float *qr,
+                                                            const float *kr) {
+  constexpr int NT = 256 * DS;
+  constexpr int HW = HD / DS;             // head dims per wave
+  constexpr int NU = HW / 16;             // q float4 per lane; O tiles of 16 dims
+  constexpr int KP = HD + 4;              // K row pitch (floats)
+  constexpr int VP = 20;                  // V^T row pitch
+  constexpr int PP = 20;                  // P row pitch
+  constexpr int NF = 16 * HD / 4 / NT;    // float4 of K (and of V) per thread per tile
+  extern __shared__ __align__(16) float fl[];
+  float *Ks = fl;                     // [16][KP]
+  float *VT = Ks + 16 * KP;           // [HD][VP]
+  float *Ps = VT + HD * VP;           // [4 DS][16][PP]
+  float *Sx = Ps + 4 * DS * 16 * PP;  // [4 DS][256] partial scores (DS > 1)
+  const AttnP p = load_params(args);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int li = lane & 15, lk = lane >> 4;
+  const int g = wave / DS, hf = wave % DS;
+  const int h = blockIdx.y, hq = h * 4 + g;
+  const int d0 = hf * HW;  // first head dim of this wave
+  const int r0 = blockIdx.x * 16;
+  const int base = aldg<int32_t>(p.pos);
+  const int rlast = min(r0 + 15, p.T - 1);
+  int klo, khi, dummy;
+  key_range(p, base + r0, &klo, &dummy);
+  key_range(p, base + rlast, &dummy, &khi);
+  const int kbeg = klo & ~15;
+
+  // q rows of this wave (A operand, head dims in MFMA order)
+  af32x4 q[NU];
+  {
+    const int row = r0 + li;
+    const float *qp = qr + (size_t)row * p.q_dim + hq * HD + d0 + 4 * lk;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      q[u] = af32x4{0.f, 0.f, 0.f, 0.f};
+      if (row < p.T) q[u] = aldg<af32x4>(qp + 16 * u);
+    }
+  }
+  // key range of each of this lane's four score rows
+  int rlo[4], rhi[4];
+  bool rok[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = r0 + 4 * lk + e;
+    rok[e] = row < p.T;
+    key_range(p, base + row, &rlo[e], &rhi[e]);
+  }
+
+  af32x4 kreg[NF], vreg[NF];
+  auto tile_load = [&](int k0) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int idx = tid + NT * f, key = idx / (HD / 4), d4 = idx % (HD / 4);
+      const int k = k0 + key;
+      kreg[f] = af32x4{0.f, 0.f, 0.f, 0.f};
+      vreg[f] = af32x4{0.f, 0.f, 0.f, 0.f};
+      if (k <= khi) {
+        if (k < base) {
+          const size_t o = (size_t)cache_slot(p, k) * p.kv_dim + h * HD + 4 * d4;
+          kreg[f] = aldg<af32x4>(p.kc + o);
+          vreg[f] = aldg<af32x4>(p.vc + o);
+        } else {
+          const int rr = k - base;
+          kreg[f] = aldg<af32x4>(kr + (size_t)rr * p.kv_dim + h * HD + 4 * d4);
+          vreg[f] = aldg<af32x4>(p.qkv + (size_t)rr * p.ld + p.q_dim + p.kv_dim + h * HD + 4 * d4);
+        }
+      }
+    }
+  };
+  auto tile_store = [&]() {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int idx = tid + NT * f, key = idx / (HD / 4), d4 = idx % (HD / 4);
+      *reinterpret_cast<af32x4 *>(Ks + key * KP + 4 * d4) = kreg[f];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) VT[(4 * d4 + c) * VP + key] = vreg[f][c];
+    }
+  };
+
+  af32x4 o[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) o[u] = af32x4{0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    m[e] = -INFINITY;
+    l[e] = 0.f;
+  }
+  float *Pw = Ps + wave * 16 * PP;
+
+  tile_load(kbeg);
+  tile_store();
+  __syncthreads();
+  for (int k0 = kbeg; k0 <= khi; k0 += 16) {
+    const bool more = k0 + 16 <= khi;
+    if (more) tile_load(k0 + 16);
+    // scores over this wave's dims: row 4lk + e, key k0 + li
+    af32x4 sc = af32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const af32x4 kv = *reinterpret_cast<const af32x4 *>(Ks + li * KP + d0 + 16 * u + 4 * lk);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(q[u][r], kv[r], sc, 0, 0, 0);
+    }
+    if constexpr (DS > 1) {
+      // sum the partial scores of the head's DS waves, in wave order (every
+      // wave of the head gets the same bits)
+      *reinterpret_cast<af32x4 *>(Sx + wave * 256 + lane * 4) = sc;
+      __syncthreads();
+      af32x4 t = *reinterpret_cast<const af32x4 *>(Sx + (g * DS) * 256 + lane * 4);
+#pragma unroll
+      for (int w2 = 1; w2 < DS; ++w2)
+        t += *reinterpret_cast<const af32x4 *>(Sx + (g * DS + w2) * 256 + lane * 4);
+      sc = t;
+    }
+    const int key = k0 + li;
+    float pe[4], corr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool ok = rok[e] && key >= rlo[e] && key <= rhi[e];
+      const float x = ok ? sc[e] * p.scale : -INFINITY;
+      const float mn = fmaxf(m[e], row16_max(x));
+      const float msafe = mn == -INFINITY ? 0.f : mn;
+      pe[e] = ok ? expf(x - msafe) : 0.f;
+      corr[e] = m[e] == -INFINITY ? 0.f : expf(m[e] - msafe);
+      l[e] = l[e] * corr[e] + row16_sum(pe[e]);
+      m[e] = mn;
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[u][e] *= corr[e];
+    // P: C layout [row][key] -> LDS -> A layout (this wave only; LDS accesses
+    // of one wave complete in order)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Pw[(4 * lk + e) * PP + li] = pe[e];
+    __builtin_amdgcn_wave_barrier();
+    const af32x4 pa = *reinterpret_cast<const af32x4 *>(Pw + li * PP + 4 * lk);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const af32x4 vt =
+          *reinterpret_cast<const af32x4 *>(VT + (d0 + 16 * u + li) * VP + 4 * lk);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        o[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[r], vt[r], o[u], 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with this tile (and with Sx)
+    if (more) tile_store();
+    __syncthreads();
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = r0 + 4 * lk + e;
+    if (row >= p.T) continue;
+    const float inv = 1.0f / l[e];
+    float *op = p.out + (size_t)row * p.q_dim + hq * HD + d0 + li;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) op[16 * u] = o[u][e] * inv;
+  }
+}
+
+// write_kv_sliding / write_kv_full (gemma4_e4b.mojo:211-249) for the rows
+__global__ __launch_bounds__(256) void k_cache_append(AttnArgs args, const float *kr) {
+  const AttnP p = load_params(args);
+  const int r = blockIdx.x;
+  const int pt = aldg<int32_t>(p.pos) + r;
+  if (!p.circular && pt >= p.cache_len) return;  // linear cache full: dropped
+  const size_t cb = (size_t)cache_slot(p, pt) * p.kv_dim;
+  for (int c = threadIdx.x; c < p.kv_dim; c += 256) {
+    p.kc[cb + c] = aldg<float>(kr + (size_t)r * p.kv_dim + c);
+    p.vc[cb + c] = aldg<float>(p.qkv + (size_t)r * p.ld + p.q_dim + p.kv_dim + c);
+  }
+}
+
+bool prefill_flash_ok(const AttnArgs &a) {
+  return a.B == 1 && a.n_kv > 0 && a.n_heads == 4 * a.n_kv &&
+         (a.hd == 128 || a.hd == 256 || a.hd == 512);
+}
+
+int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, hipStream_t st) {
+  if (int rc = attn_check(a)) return rc;
+  MS_CHECK_ARG(prefill_flash_ok(a), "prefill attention: needs B = 1, 4 query heads per kv "
+                                    "head and head_dim 128, 256 or 512");
+  MS_CHECK_ARG(a.qkv && a.pos && a.out && a.kc && a.vc && qr && kr,
+               "prefill attention: missing buffers");
+  hipLaunchKernelGGL(k_rope_rows, dim3(a.T), dim3(256), 0, st, a, qr, kr, a.hd);
+  const dim3 grid((a.T + 15) / 16, a.n_kv);
+#define MS_FLASH(HDV, DSV)                                                                \
+  hipLaunchKernelGGL((k_flash_prefill<HDV, DSV>), grid, dim3(256 * DSV),                   \
+                     (flash_lds_floats<HDV, DSV>() * 4), st, a, (const float *)qr,         \
+                     (const float *)kr)
+  switch (a.hd) {
+    case 128: MS_FLASH(128, 1); break;
+    case 256: MS_FLASH(256, 2); break;
+    default: MS_FLASH(512, 2); break;
+  }
+#undef MS_FLASH
+  if (a.write_cache)
+    hipLaunchKernelGGL(k_cache_append, dim3(a.T), dim3(256), 0, st, a, (const float *)kr);
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
+}
+
 }  // namespace ms

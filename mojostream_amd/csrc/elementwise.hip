@@ -198,8 +198,12 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.out = d_out;
   if (int rc = attn_check(a)) return rc;
   const int G = a.n_heads / a.n_kv;
+  // many rows: the flash-attention prefill path (needs no chunk partials, but
+  // buffers for the rows' q and k)
+  const bool flash = T > kGemvMaxM && prefill_flash_ok(a);
   const size_t qkv_f = (size_t)T * ld;
-  const size_t part_f = (size_t)a.n_kv * a.n_chunks * T * G * (a.hd + 2);
+  const size_t part_f = flash ? (size_t)T * (L->q_dim + L->kv_dim)
+                              : (size_t)a.n_kv * a.n_chunks * T * G * (a.hd + 2);
   const size_t need = (qkv_f + part_f) * 4 + 64;
   void *buf = nullptr;
   if (int rc = scratch(need, &buf)) return rc;
@@ -216,7 +220,11 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.qkv = qkv;
   a.part = part;
   a.pos = dpos;
-  if (int rc = launch_attention(a, st)) return rc;
+  if (flash) {
+    if (int rc = launch_attention_prefill(a, part, part + (size_t)T * L->q_dim, st)) return rc;
+  } else if (int rc = launch_attention(a, st)) {
+    return rc;
+  }
   MS_HIP_TRY(hipStreamSynchronize(st));
   return MS_OK;
 }

@@ -1,0 +1,268 @@
+// Q4 GEMM for prefill rows (M > 16) on v_mfma_i32_16x16x64_i8.
+//
+// The operands are those of the GEMV in q4.hip: activation rows quantized by
+// launch_quant_rows into four int8 limbs per value (limb row 4m + l, MFMA
+// fragment order inside each 128-row super-tile of K) and the weights as
+// signed bytes n - 8 straight from the panel layout.  Each limb row's dot
+// product is exact in int32; the four limbs of an output combine in int64 and
+// are scaled by 2^-s and the tensor scale with the GEMV's expression, so a
+// row gets the same value from this kernel as from the GEMV.
+//
+// Tiling: a block computes kBM = 32 activation rows (128 limb rows, 8 MFMA A
+// tiles) by 8 panels (128 columns).  Wave (wa, wb) owns A tiles 4wa..4wa+3 and
+// panels 4wb..4wb+3: 16 accumulators and 32 MFMAs per 128-row step of K.  The
+// A operand of a step (128 limb rows x 128 bytes) is staged in LDS, double
+// buffered, rows padded to 144 bytes so that the 16 rows one operand read
+// touches fall in different banks.  Each wave loads its panels' 1 KiB
+// super-tiles straight into registers, one step ahead.  In the D fragment of
+// an A tile, lane j + 16r holds the four limbs of activation row r, column j,
+// so the limbs combine inside the lane and no cross-wave reduction is needed.
+//
+// EPI_SWIGLU: wave column wb = 0 computes gate panels, wb = 1 the up panels of
+// the same columns; the gate values pass through LDS and the up waves write
+// up * gate * sigmoid(gate) (swiglu_inplace, kernels.mojo:519-532).
+#include "devutil.h"
+#include "q4.h"
+
+namespace ms {
+namespace {
+
+constexpr int kBM = 32;                  // activation rows per block
+constexpr int kApitch = 144;             // LDS bytes per staged limb row
+constexpr int kAstage = 4 * kBM * kApitch;  // one K step of A
+constexpr int kGemmLds = 2 * kAstage;
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int M = launder(g.M), K = launder(g.K);
+  const int8_t *limbs = launder(g.a.limbs);
+  const int32_t *shift = launder(g.a.shift);
+  const uint8_t *sw0 = launder(g.seg[0].w), *sw1 = launder(g.seg[1].w),
+                *sw2 = launder(g.seg[2].w);
+  const float ss0 = launder(g.seg[0].scale), ss1 = launder(g.seg[1].scale),
+              ss2 = launder(g.seg[2].scale);
+  const int nseg = launder(g.nseg);
+  const int sn0 = launder(g.seg[0].n_cols) >> 4;
+  const int sn1 = nseg > 1 ? launder(g.seg[1].n_cols) >> 4 : 0;
+  const int sn2 = nseg > 2 ? launder(g.seg[2].n_cols) >> 4 : 0;
+  const int sc0 = launder(g.seg[0].out_col0), sc1 = launder(g.seg[1].out_col0),
+            sc2 = launder(g.seg[2].out_col0);
+  float *out = launder(g.out);
+  const int ldo = launder(g.ldo);
+  const float *resid = EPI == EPI_RESID ? launder(g.resid) : nullptr;
+  float *out2 = EPI == EPI_RESID ? launder(g.out2) : nullptr;
+  float *sw_out = EPI == EPI_SWIGLU ? launder(g.sw_out) : nullptr;
+  const int ldo_sw = EPI == EPI_SWIGLU ? launder(g.ldo_sw) : 0;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int wa = wave & 1, wb = wave >> 1;
+  const int r0 = blockIdx.y * kBM;
+  const int KG = K >> 7;
+
+  // this wave's four panels (scalar: block and wave uniform)
+  const uint8_t *wp[4];
+  float wsc[4];
+  int col[4];
+  bool pv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (EPI == EPI_SWIGLU) {
+      const int cp = blockIdx.x * 4 + j;
+      pv[j] = cp < sn0;
+      wp[j] = (wb == 0 ? sw0 : sw1) + (size_t)(pv[j] ? cp : 0) * K * 8;
+      wsc[j] = wb == 0 ? ss0 : ss1;
+      col[j] = cp * 16;
+    } else {
+      const int pi = blockIdx.x * 8 + 4 * wb + j;
+      const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
+      const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
+      pv[j] = pi < sn0 + sn1 + sn2;
+      const uint8_t *base = si == 0 ? sw0 : (si == 1 ? sw1 : sw2);
+      wp[j] = pv[j] ? base + (size_t)loc * K * 8 : sw0;
+      wsc[j] = si == 0 ? ss0 : (si == 1 ? ss1 : ss2);
+      col[j] = (si == 0 ? sc0 : (si == 1 ? sc1 : sc2)) + loc * 16;
+    }
+  }
+
+  // A staging: 128 limb rows x 128 bytes = 1024 pieces of 16 bytes; thread t
+  // moves pieces t, t + 256, t + 512, t + 768 (eight threads per row).
+  const int8_t *abase = limbs + (size_t)(4 * r0) * K;
+  u32x4 ar[4];
+  auto a_load = [&](int G) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, row = e >> 3, c = e & 7;
+      ar[i] = ldg<u32x4>(abase + (size_t)row * K + (size_t)G * 128 + c * 16);
+    }
+  };
+  auto a_store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, row = e >> 3, c = e & 7;
+      *reinterpret_cast<u32x4 *>(lds + buf * kAstage + row * kApitch + c * 16) = ar[i];
+    }
+  };
+  auto b_load = [&](int G, u32x4 (&br)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      br[j] = u32x4{0u, 0u, 0u, 0u};
+      if (pv[j]) br[j] = ldg<u32x4>(wp[j] + (size_t)G * 1024 + lane * 16);
+    }
+  };
+
+  v4i acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[a][j] = v4i{0, 0, 0, 0};
+
+  const int li = lane & 15, lg = lane >> 4;
+  auto compute = [&](int buf, const u32x4 (&br)[4]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i bf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t d0 = br[j][2 * h], d1 = br[j][2 * h + 1];
+        bf[j] = v4i{nib_s8(d0), nib_s8(d0 >> 4), nib_s8(d1), nib_s8(d1 >> 4)};
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const v4i af = *reinterpret_cast<const v4i *>(
+            lds + buf * kAstage + (16 * (4 * wa + a) + li) * kApitch + 32 * lg + 16 * h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[a][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[a][j], 0, 0, 0);
+      }
+    }
+  };
+
+  u32x4 bc[4], bn[4];
+  a_load(0);
+  b_load(0, bc);
+  a_store(0);
+  __syncthreads();
+  for (int G = 0; G < KG; ++G) {
+    const int buf = G & 1;
+    const bool more = G + 1 < KG;
+    if (more) {
+      a_load(G + 1);
+      b_load(G + 1, bn);
+    }
+    compute(buf, bc);
+    if (more) a_store(buf ^ 1);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bc[j] = bn[j];
+  }
+
+  // ---- epilogue: lane (column jc, row rr of each A tile)
+  const int jc = lane & 15, rr = lane >> 4;
+  float v[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int row = r0 + 4 * (4 * wa + a) + rr;
+    const float sc = row < M ? ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4i d = acc[a][j];
+      const long long t = (long long)d[0] + ((long long)d[1] << 8) + ((long long)d[2] << 16) +
+                          ((long long)d[3] << 24);
+      v[a][j] = (float)((double)t * (double)sc * (double)wsc[j]);
+    }
+  }
+  if constexpr (EPI == EPI_SWIGLU) {
+    // gate values of wave (wa, 0) -> LDS -> wave (wa, 1)
+    float *xg = reinterpret_cast<float *>(lds);
+    if (wb == 0) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xg[((wa * 4 + a) * 4 + j) * 64 + lane] = v[a][j];
+    }
+    __syncthreads();
+    if (wb == 1) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int row = r0 + 4 * (4 * wa + a) + rr;
+        if (row >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (!pv[j]) continue;
+          const float gt = xg[((wa * 4 + a) * 4 + j) * 64 + lane], up = v[a][j];
+          sw_out[(size_t)row * ldo_sw + col[j] + jc] = up * gt * (1.0f / (1.0f + expf(-gt)));
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int row = r0 + 4 * (4 * wa + a) + rr;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (!pv[j]) continue;
+        const size_t oi = (size_t)row * ldo + col[j] + jc;
+        if constexpr (EPI == EPI_STORE) {
+          out[oi] = v[a][j];
+        } else if constexpr (EPI == EPI_ACCUMULATE) {
+          out[oi] += v[a][j];
+        } else {
+          const float x = resid[oi] + v[a][j];
+          out[oi] = x;
+          if (out2) out2[oi] = x;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int gemm_row_pad(int M) { return (M + kBM - 1) / kBM * kBM; }
+
+int launch_gemm(const GemmArgs &g, hipStream_t st) {
+  MS_CHECK_ARG(g.M >= 1 && g.K >= 128 && g.K % 128 == 0 && g.K <= kQuantMaxK,
+               "GEMM: K must be a multiple of 128 in [128, 16384]");
+  MS_CHECK_ARG(g.a.limbs && g.a.shift, "GEMM: quantized rows missing");
+  MS_CHECK_ARG(g.nseg >= 1 && g.nseg <= 3, "GEMM: 1..3 weight segments");
+  for (int i = 0; i < g.nseg; ++i)
+    MS_CHECK_ARG(g.seg[i].w && g.seg[i].n_cols > 0 && g.seg[i].n_cols % 16 == 0,
+                 "GEMM: segment columns must be a positive multiple of 16");
+  const dim3 blk(256);
+  const int gy = gemm_row_pad(g.M) / kBM;
+  switch (g.epi) {
+    case EPI_STORE:
+    case EPI_ACCUMULATE:
+    case EPI_RESID: {
+      MS_CHECK_ARG(g.out && g.ldo > 0, "GEMM: output missing");
+      MS_CHECK_ARG(g.epi != EPI_RESID || g.resid, "GEMM: residual missing");
+      int np = 0;
+      for (int i = 0; i < g.nseg; ++i) np += g.seg[i].n_cols / 16;
+      const dim3 grid((np + 7) / 8, gy);
+      if (g.epi == EPI_STORE)
+        hipLaunchKernelGGL(k_gemm<EPI_STORE>, grid, blk, kGemmLds, st, g);
+      else if (g.epi == EPI_ACCUMULATE)
+        hipLaunchKernelGGL(k_gemm<EPI_ACCUMULATE>, grid, blk, kGemmLds, st, g);
+      else
+        hipLaunchKernelGGL(k_gemm<EPI_RESID>, grid, blk, kGemmLds, st, g);
+      break;
+    }
+    case EPI_SWIGLU: {
+      MS_CHECK_ARG(g.nseg == 2 && g.seg[0].n_cols == g.seg[1].n_cols && g.sw_out,
+                   "GEMM: SwiGLU needs gate and up of equal width and an output");
+      const dim3 grid((g.seg[0].n_cols / 16 + 3) / 4, gy);
+      hipLaunchKernelGGL(k_gemm<EPI_SWIGLU>, grid, blk, kGemmLds, st, g);
+      break;
+    }
+    default:
+      return fail(MS_E_INVALID, "GEMM: unsupported epilogue");
+  }
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
+}
+
+}  // namespace ms

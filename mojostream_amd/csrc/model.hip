@@ -102,6 +102,11 @@ struct ms_model {
   void *quant = nullptr;
   int quant_k = 0;
   float *qkv = nullptr, *attn_part = nullptr;
+  // prefill: rows per chunk (0: no prefill workspace), attention rows per
+  // launch inside a chunk and their base positions on the device
+  int prefill_rows = 0;
+  int32_t *ppos = nullptr;
+  float *fq = nullptr, *fk = nullptr;  // prefill rows' q and k after RoPE
   int32_t *pos = nullptr, *tok = nullptr, *ids_hist = nullptr, *step = nullptr;
   int hist_cap = 1024;
   float *arg_val = nullptr;
@@ -180,6 +185,12 @@ static void prof_collect() {
 }
 
 // ---- per-layer enqueue --------------------------------------------------------
+// Prefill processes the prompt in chunks of up to kPrefillRows rows; their
+// projections run as GEMMs.  Attention over a chunk runs kPrefillAttnRows rows
+// per launch (its partial-result buffer grows with the rows of a launch).
+constexpr int kPrefillRows = 512;
+constexpr int kPrefillAttnRows = 32;
+
 struct RunCfg {
   int B, T;                 // sequences, rows per sequence
   const float *in_rows;     // first layer input rows [B*T][D]
@@ -203,6 +214,24 @@ static int launch_gemv_rec(const GemvArgs &a, hipStream_t st) {
 
 static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipStream_t st) {
   constexpr size_t kLdsLimit = 150 * 1024;
+  if (a.M > kGemvMaxM) {
+    // prefill rows: quantize every row once, then the MFMA GEMM
+    GemmArgs g{};
+    g.epi = a.epi;
+    g.M = a.M;
+    g.K = a.K;
+    g.a = quant_rows_view(m->quant, gemm_row_pad(a.M), a.K);
+    for (int i = 0; i < 3; ++i) g.seg[i] = a.seg[i];
+    g.nseg = a.nseg;
+    g.out = a.out;
+    g.ldo = a.ldo;
+    g.resid = a.resid;
+    g.out2 = a.out2;
+    g.sw_out = a.sw_out;
+    g.ldo_sw = a.ldo_sw;
+    if (int rc = launch_quant_rows(r, a.M, a.K, g.a, st)) return rc;
+    return launch_gemm(g, st);
+  }
   a.asrc = AS_ROWS;
   a.rows = r;
   a.waves = waves;
@@ -281,7 +310,23 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.write_cache = 1;
     // KV bytes read at the current position are counted by bench.py
     ProfScope ps(PC_ATTN, 0.0, st);
-    if (int rc2 = launch_attention(a, st)) return rc2;
+    if (rc.B == 1 && rc.T > kGemvMaxM && m->fq && prefill_flash_ok(a)) {
+      // prefill rows: flash attention on fp32 MFMA
+      if (int rc2 = launch_attention_prefill(a, m->fq, m->fk, st)) return rc2;
+    } else if (rc.T <= kPrefillAttnRows || rc.B != 1) {
+      if (int rc2 = launch_attention(a, st)) return rc2;
+    } else {
+      // a prefill chunk: consecutive row groups, each attending to the cache
+      // the groups before it have written (base positions in m->ppos)
+      for (int s = 0, r0 = 0; r0 < rc.T; ++s, r0 += kPrefillAttnRows) {
+        AttnArgs b = a;
+        b.T = std::min(kPrefillAttnRows, rc.T - r0);
+        b.qkv = m->qkv + (size_t)r0 * ld;
+        b.out = m->aO + (size_t)r0 * d.q_dim;
+        b.pos = m->ppos + s;
+        if (int rc2 = launch_attention(b, st)) return rc2;
+      }
+    }
   }
   // 3. x2 = x + attn . Wo (residual epilogue)
   {
@@ -518,7 +563,11 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   m->d = d;
   m->Mmax = d.max_seqs * d.max_rows;
   m->h_pos.assign(d.max_seqs, 0);
-  const int M = m->Mmax;
+  // models with an LM head prefill prompts in chunks of up to kPrefillRows
+  if (d.vocab > 0) m->prefill_rows = std::max(m->Mmax, std::min(kPrefillRows, d.max_pos));
+  const int M = std::max(m->Mmax, m->prefill_rows);  // workspace rows
+  const int attn_rows = m->prefill_rows > kGemvMaxM
+                            ? std::max(d.max_rows, kPrefillAttnRows) : d.max_rows;
   auto cleanup = [&](int rc) {
     ms_model_destroy(m);
     return rc;
@@ -561,12 +610,12 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
     }
     Ly.rope = rid;
     const int ncols_qkv = ld.q_dim + 2 * ld.kv_dim;
-    const int span = ld.cache_kind == MS_CACHE_CIRCULAR ? ld.cache_len + d.max_rows - 1
-                                                        : ld.cache_len + d.max_rows;
+    const int span = ld.cache_kind == MS_CACHE_CIRCULAR ? ld.cache_len + attn_rows - 1
+                                                        : ld.cache_len + attn_rows;
     Ly.n_chunks = cdiv(span, kAttnChunk);
     const int G = ld.n_heads / ld.n_kv_heads;
     max_part = std::max(max_part, (size_t)d.max_seqs * ld.n_kv_heads * Ly.n_chunks *
-                                      d.max_rows * G * (ld.head_dim + 2));
+                                      attn_rows * G * (ld.head_dim + 2));
     m->qkv_max = std::max(m->qkv_max, ncols_qkv);
     m->q_max = std::max(m->q_max, ld.q_dim);
     m->quant_k = std::max(m->quant_k, std::max(std::max(d.hidden, d.ffn), ld.q_dim));
@@ -583,7 +632,12 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
       (rc = dmalloc(m, (void **)&m->x2n, (size_t)M * D * 4)) ||
       (rc = dmalloc(m, (void **)&m->aO, (size_t)M * m->q_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->aF, (size_t)M * F * 4)) ||
-      (rc = dmalloc(m, &m->quant, quant_rows_bytes(M, m->quant_k))))
+      (rc = dmalloc(m, &m->quant, quant_rows_bytes(gemm_row_pad(M), m->quant_k))) ||
+      (rc = dmalloc(m, (void **)&m->ppos, (size_t)(M / kPrefillAttnRows + 2) * 4)))
+    return cleanup(rc);
+  if (m->prefill_rows > kGemvMaxM &&
+      ((rc = dmalloc(m, (void **)&m->fq, (size_t)m->prefill_rows * m->q_max * 4)) ||
+       (rc = dmalloc(m, (void **)&m->fk, (size_t)m->prefill_rows * m->kv_max * 4))))
     return cleanup(rc);
   if ((rc = dmalloc(m, (void **)&m->qkv, (size_t)M * m->qkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
@@ -930,16 +984,23 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
     MS_CHECK_ARG(h_tokens[i] >= 0 && h_tokens[i] < m->d.vocab, "prefill: token id out of range");
   hipStream_t st = ctx().stream;
   const int D = m->d.hidden;
-  const int T = m->d.max_rows;
+  // rows per chunk: the prefill workspace (projections as GEMMs)
+  const int T = std::max(m->d.max_rows, m->prefill_rows);
   int32_t *dtok = nullptr;
   MS_HIP_TRY(hipMallocAsync((void **)&dtok, (size_t)n_tokens * 4, st));
   MS_HIP_TRY(hipMemcpyAsync(dtok, h_tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, st));
   int rcode = MS_OK;
+  std::vector<int32_t> sub;
   for (int c0 = 0; c0 < n_tokens && rcode == MS_OK; c0 += T) {
     const int t = std::min(T, n_tokens - c0);
     const int base = pos0 + c0;
     if ((rcode = check_positions(m, &base, 1, t, 0))) break;
     MS_HIP_TRY(hipMemcpyAsync(m->pos + seq, &base, 4, hipMemcpyHostToDevice, st));
+    // base position of each attention row group of the chunk
+    sub.clear();
+    for (int r0 = 0; r0 < t; r0 += kPrefillAttnRows) sub.push_back(base + r0);
+    MS_HIP_TRY(hipMemcpyAsync(m->ppos, sub.data(), sub.size() * 4, hipMemcpyHostToDevice, st));
+    MS_HIP_TRY(hipStreamSynchronize(st));  // `sub` is reused by the next chunk
     if ((rcode = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, dtok + c0, t, m->x_in, st)))
       break;
     if (m->bos && base == 0)

@@ -84,6 +84,22 @@ struct ArgmaxFin {
   int32_t *step;        // step counter (with ids_hist)
 };
 
+// Prefill GEMM (gemm.hip): the rows of `a` are quantized for
+// gemm_row_pad(M) rows (rows past M are read but never stored).
+struct GemmArgs {
+  int epi;        // EPI_STORE, EPI_ACCUMULATE, EPI_RESID or EPI_SWIGLU (gate, up)
+  int M, K;
+  QuantRows a;
+  GemvSeg seg[3];
+  int nseg;
+  float *out;     // [M][ldo]
+  int ldo;
+  const float *resid;  // EPI_RESID: [M][ldo]
+  float *out2;         // EPI_RESID: optional copy
+  float *sw_out;       // EPI_SWIGLU: [M][ldo_sw]
+  int ldo_sw;
+};
+
 constexpr int kGemvMaxM = 16;
 constexpr int kQuantMaxK = 16384;  // longest row a 1024-thread block quantizes
 
@@ -98,5 +114,8 @@ size_t quant_rows_bytes(int M, int K);
 QuantRows quant_rows_view(void *buf, int M, int K);
 int pack_device(uint8_t *dst, const uint8_t *src, int K, int N, hipStream_t st);
 int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st);
+int launch_gemm(const GemmArgs &g, hipStream_t st);
+// Rows a GEMM reads from its quantized operand (M rounded up to the row tile).
+int gemm_row_pad(int M);
 
 }  // namespace ms

@@ -2,12 +2,15 @@
 // MFMA GEMV used for decode (M <= 16 rows) with fused epilogues.
 //
 // Reference: matmul_q4_bpack_raw (kernels.mojo:201-267) computes
-// C += A . deq(W) with w = (nibble-8)*scale.  Here the weight nibbles go into
-// v_mfma_i32_16x16x64_i8 as they are (three bit operations per eight weights),
-// each activation row as four int8 limbs of a 31-bit fixed-point value with a
-// per-row power-of-two scale, so the dot product sum X*(n-8) is exact integer
-// arithmetic; it is scaled by 2^-s and the tensor scale once per output.  For
-// M <= 4 the 4M limb rows share one MFMA, so one MFMA covers 1024 weights.
+// C += A . deq(W) with w = (nibble-8)*scale.  Here the weights go into
+// v_mfma_i32_16x16x64_i8 as signed bytes n-8 (a few bit operations per eight
+// weights), each activation row as four int8 limbs of a 31-bit fixed-point
+// value with a per-row power-of-two scale, so the dot product sum X*(n-8) is
+// exact integer arithmetic; it is scaled by 2^-s and the tensor scale once per
+// output.  For M <= 4 the 4M limb rows share one MFMA, so one MFMA covers
+// 1024 weights.  Prefill rows (M > 16) go through the GEMM in gemm.hip, which
+// uses the same operands and therefore gives the same values.
+#include "devutil.h"
 #include "q4.h"
 
 #include <cmath>
@@ -86,31 +89,6 @@ __global__ void k_dequant_packed(float *__restrict__ out,
 // ------------------------------------------------------------------------------
 // helpers
 // ------------------------------------------------------------------------------
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// Global-memory loads through an explicit global pointer: generic (flat)
-// loads also count against the LDS wait counter, so an LDS wait would stall
-// on them.
-template <class T>
-__device__ inline T ldg(const void *p) {
-  return *(const __attribute__((address_space(1))) T *)p;
-}
-template <>
-__device__ inline float4 ldg<float4>(const void *p) {
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
-  const f32x4 v = *(const __attribute__((address_space(1))) f32x4 *)p;
-  return float4{v.x, v.y, v.z, v.w};
-}
-
-// A uniform value passed through an opaque register move: the compiler can no
-// longer turn selects between such values back into an indexed memory access
-// (which would put them in scratch memory or re-read the argument struct).
-template <class T>
-__device__ inline T launder(T v) {
-  asm volatile("" : "+s"(v));
-  return v;
-}
 
 // Wave reductions: DPP moves inside each 16-lane row (quad permutes, then
 // the half-row and row mirrors leave the row total in every lane of the row),
@@ -432,13 +410,6 @@ __device__ inline void gemv_slot(const uint8_t *w0, const uint8_t *w1, const uin
     *col = ok ? cc + loc * 16 : 0;
     *valid = ok;
   }
-}
-
-// Low nibbles of the four bytes of d as signed bytes n - 8 (the Q4 zero point
-// folded into the operand): n + 0x78 stays inside its byte for n <= 15, and
-// flipping bit 7 turns it into the two's complement of n - 8.
-__device__ inline int nib_s8(uint32_t d) {
-  return (int)(((d & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
 }
 
 // D fragment index of output row i, column j (v_mfma_*_16x16x* layout:
@@ -929,6 +900,27 @@ extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packe
   MS_CHECK_ARG(M >= 1, "matmul: M must be >= 1");
   MS_CHECK_ARG(K <= kQuantMaxK, "matmul: K must be <= 16384");
   hipStream_t st = ctx().stream;
+  if (M > kGemvMaxM) {
+    // many rows: quantize all of them once, then the MFMA GEMM
+    const int Mp = gemm_row_pad(M);
+    void *buf = nullptr;
+    if (int rc = scratch(quant_rows_bytes(Mp, K), &buf)) return rc;
+    GemmArgs g{};
+    g.epi = accumulate ? EPI_ACCUMULATE : EPI_STORE;
+    g.M = M;
+    g.K = K;
+    g.a = quant_rows_view(buf, Mp, K);
+    RowSrc r{};
+    r.x = d_A;
+    r.ld = K;
+    r.pre_scale = 1.f;
+    if (int rc = launch_quant_rows(r, M, K, g.a, st)) return rc;
+    g.seg[0] = GemvSeg{d_packed, scale, N, 0};
+    g.nseg = 1;
+    g.out = d_C;
+    g.ldo = N;
+    return launch_gemm(g, st);
+  }
   const int chunk = kGemvMaxM;
   const int P = (N / 16) % 4 == 0 && N >= 4 * 16 * 512 ? 4 : 1;
   void *buf = nullptr;

@@ -56,7 +56,9 @@ def test_dequant_and_pack_bit_exact(gpu, oracle, K, N):
 MATMUL_SHAPES = [(M, K, K) for M in (1, 4, 64) for K in (1024, 4096)] + [
     (1, 2560, 2048), (4, 2560, 512), (1, 2048, 2560), (4, 2560, 10240), (1, 10240, 2560),
     (4, 4096, 2560), (1, 2560, 4096), (2, 2560, 1024), (16, 2560, 512), (9, 1024, 1024),
-    (1, 5120, 1024), (1, 13824, 5120)]
+    (1, 5120, 1024), (1, 13824, 5120),
+    # M > 16: quantize once, MFMA GEMM (prefill shapes)
+    (17, 2560, 3072), (100, 2560, 1024), (333, 1024, 512), (200, 10240, 256)]
 
 
 @pytest.mark.parametrize("M,K,N", MATMUL_SHAPES)
@@ -78,6 +80,29 @@ def test_q4_matmul_vs_f64(gpu, oracle, M, K, N):
         assert rel_max(oracle.matmul(A, q4, N, 0.1), ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,K,N", [(48, 2560, 512), (70, 1024, 160), (256, 4096, 128)])
+def test_q4_gemm_rows_equal_gemv_rows(gpu, M, K, N):
+    """The GEMM (M > 16) and the GEMV (row chunks of <= 16) use the same exact
+    integer operands and the same scaling, so every row must agree bit for bit."""
+    ms = gpu
+    say(f"GEMM vs GEMV rows M={M} K={K} N={N}")
+    q4 = ms.host_random_u8(K * N // 2, 31, K + N).reshape(K, N // 2)
+    A = (RNG.standard_normal((M, K)) * RNG.uniform(0.01, 100, (M, 1))).astype(np.float32)
+    _, d_pk = packed(ms, q4, K, N)
+    dA = ms.DeviceBuffer.from_array(A)
+    dC = ms.DeviceBuffer(M * N * 4)
+    ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pk.ptr, M, K, N, 0.07, 0))
+    full = dC.download(np.float32, (M, N))
+    rows = []
+    for m0 in range(0, M, 16):
+        mm = min(16, M - m0)
+        dAc = ms.DeviceBuffer.from_array(np.ascontiguousarray(A[m0:m0 + mm]))
+        dCc = ms.DeviceBuffer(mm * N * 4)
+        ms.check(ms.lib().ms_q4_matmul(dCc.ptr, dAc.ptr, d_pk.ptr, mm, K, N, 0.07, 0))
+        rows.append(dCc.download(np.float32, (mm, N)))
+    assert np.array_equal(full, np.concatenate(rows))
+
+
 def test_q4_matmul_accumulates(gpu, oracle):
     ms = gpu
     M, K, N = 4, 1024, 256
@@ -86,6 +111,15 @@ def test_q4_matmul_accumulates(gpu, oracle):
     A = RNG.standard_normal((M, K)).astype(np.float32)
     C0 = RNG.standard_normal((M, N)).astype(np.float32)
     _, d_pk = packed(ms, q4, K, N)
+    dA = ms.DeviceBuffer.from_array(A)
+    dC = ms.DeviceBuffer.from_array(C0)
+    ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pk.ptr, M, K, N, 0.1, 1))
+    ref = C0 + oracle.matmul_f64(A, q4, N, 0.1)
+    assert rel_max(dC.download(np.float32, (M, N)), ref) < 1e-5
+    # many rows (GEMM path) accumulate the same way
+    M = 40
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    C0 = RNG.standard_normal((M, N)).astype(np.float32)
     dA = ms.DeviceBuffer.from_array(A)
     dC = ms.DeviceBuffer.from_array(C0)
     ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pk.ptr, M, K, N, 0.1, 1))
@@ -143,6 +177,13 @@ ATTN_CASES = [
     ("g4-hd64", 1024, 256, 64, 16, 4, 0, 256, 0, 4, 200),
     ("14b", 5120, 1024, 128, 40, 8, 0, 4096, 0, 1, 4000),
     ("first-token", 2048, 512, 256, 8, 2, 1, 512, 0, 1, 0),
+    # many rows of one sequence: the flash-attention prefill path
+    ("prefill-sliding", 2048, 512, 256, 8, 2, 1, 512, 0, 200, 0),
+    ("prefill-sliding-wrap", 2048, 512, 256, 8, 2, 1, 512, 0, 333, 650),
+    ("prefill-full", 4096, 1024, 512, 8, 2, 0, 4096, 1, 300, 100),
+    ("prefill-full-clamp", 4096, 1024, 512, 8, 2, 0, 256, 1, 64, 230),
+    ("prefill-demo", 1024, 256, 128, 8, 2, 0, 512, 0, 48, 17),
+    ("prefill-14b-chunks", 5120, 1024, 128, 40, 8, 0, 4096, 0, 20, 100),
 ]
 
 
