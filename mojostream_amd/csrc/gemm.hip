@@ -9,18 +9,21 @@
 // row gets the same value from this kernel as from the GEMV.
 //
 // Tiling: a block computes kBM = 32 activation rows (128 limb rows, 8 MFMA A
-// tiles) by 8 panels (128 columns).  Wave (wa, wb) owns A tiles 4wa..4wa+3 and
-// panels 4wb..4wb+3: 16 accumulators and 32 MFMAs per 128-row step of K.  The
-// A operand of a step (128 limb rows x 128 bytes) is staged in LDS, double
-// buffered, rows padded to 144 bytes so that the 16 rows one operand read
+// tiles) by 4 kWB panels (8 panels, 128 columns).  Wave (wa, wb) owns A tiles
+// 4wa..4wa+3 and panels 4wb..4wb+3: 16 accumulators and 32 MFMAs per 128-row
+// step of K.  (A 16-panel tile measured the same on the prefill shapes.)  The
+// A operand of a step (128 limb rows x 128 bytes) is staged in LDS (a ring of
+// three steps), rows padded to 144 bytes so that the 16 rows one operand read
 // touches fall in different banks.  Each wave loads its panels' 1 KiB
-// super-tiles straight into registers, one step ahead.  In the D fragment of
+// super-tiles straight into registers.  Loads run two steps ahead of the
+// MFMAs, which a step's MFMA time alone does not cover.  In the D fragment of
 // an A tile, lane j + 16r holds the four limbs of activation row r, column j,
 // so the limbs combine inside the lane and no cross-wave reduction is needed.
 //
-// EPI_SWIGLU: wave column wb = 0 computes gate panels, wb = 1 the up panels of
-// the same columns; the gate values pass through LDS and the up waves write
-// up * gate * sigmoid(gate) (swiglu_inplace, kernels.mojo:519-532).
+// EPI_SWIGLU: the first half of the wave columns computes gate panels, the
+// second half the up panels of the same columns; the gate values pass through
+// LDS and the up waves write up * gate * sigmoid(gate) (swiglu_inplace,
+// kernels.mojo:519-532).
 #include "devutil.h"
 #include "q4.h"
 
@@ -28,12 +31,15 @@ namespace ms {
 namespace {
 
 constexpr int kBM = 32;                  // activation rows per block
+constexpr int kWB = 2;                   // wave columns: 4 panels each
+constexpr int kNT = 128 * kWB;           // threads (2 wave rows x kWB wave columns)
 constexpr int kApitch = 144;             // LDS bytes per staged limb row
 constexpr int kAstage = 4 * kBM * kApitch;  // one K step of A
-constexpr int kGemmLds = 2 * kAstage;
+constexpr int kStages = 3;                  // A steps resident in LDS
+constexpr int kGemmLds = kStages * kAstage;
 
 template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int M = launder(g.M), K = launder(g.K);
   const int8_t *limbs = launder(g.a.limbs);
@@ -59,6 +65,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int wa = wave & 1, wb = wave >> 1;
+  // EPI_SWIGLU: wave columns [0, kWB/2) hold gate panels, the rest the up
+  // panels of the same columns
+  const int half = wb / (kWB / 2), sub = wb % (kWB / 2);
   const int r0 = blockIdx.y * kBM;
   const int KG = K >> 7;
 
@@ -70,13 +79,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if constexpr (EPI == EPI_SWIGLU) {
-      const int cp = blockIdx.x * 4 + j;
+      const int cp = blockIdx.x * (2 * kWB) + 4 * sub + j;
       pv[j] = cp < sn0;
-      wp[j] = (wb == 0 ? sw0 : sw1) + (size_t)(pv[j] ? cp : 0) * K * 8;
-      wsc[j] = wb == 0 ? ss0 : ss1;
+      wp[j] = (half == 0 ? sw0 : sw1) + (size_t)(pv[j] ? cp : 0) * K * 8;
+      wsc[j] = half == 0 ? ss0 : ss1;
       col[j] = cp * 16;
     } else {
-      const int pi = blockIdx.x * 8 + 4 * wb + j;
+      const int pi = blockIdx.x * (4 * kWB) + 4 * wb + j;
       const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
       const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
       pv[j] = pi < sn0 + sn1 + sn2;
@@ -88,20 +97,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
   }
 
   // A staging: 128 limb rows x 128 bytes = 1024 pieces of 16 bytes; thread t
-  // moves pieces t, t + 256, t + 512, t + 768 (eight threads per row).
+  // moves pieces t, t + kNT, ... (eight threads per row).
+  constexpr int NA = 1024 / kNT;
   const int8_t *abase = limbs + (size_t)(4 * r0) * K;
-  u32x4 ar[4];
-  auto a_load = [&](int G) {
+  auto a_load = [&](int G, u32x4 (&ar)[NA]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i, row = e >> 3, c = e & 7;
+    for (int i = 0; i < NA; ++i) {
+      const int e = tid + kNT * i, row = e >> 3, c = e & 7;
       ar[i] = ldg<u32x4>(abase + (size_t)row * K + (size_t)G * 128 + c * 16);
     }
   };
-  auto a_store = [&](int buf) {
+  auto a_store = [&](int buf, const u32x4 (&ar)[NA]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i, row = e >> 3, c = e & 7;
+    for (int i = 0; i < NA; ++i) {
+      const int e = tid + kNT * i, row = e >> 3, c = e & 7;
       *reinterpret_cast<u32x4 *>(lds + buf * kAstage + row * kApitch + c * 16) = ar[i];
     }
   };
@@ -140,23 +149,37 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
   };
 
-  u32x4 bc[4], bn[4];
-  a_load(0);
+  // Software pipeline, two steps deep: the loads of step G + 2 go out while
+  // step G computes; step G + 1's A (loaded one step earlier) enters LDS at
+  // the end of step G.
+  u32x4 a1[NA], a2[NA], bc[4], b1[4], b2[4];
+  a_load(0, a1);
   b_load(0, bc);
-  a_store(0);
+  a_store(0, a1);
+  if (KG > 1) {
+    a_load(1, a1);
+    b_load(1, b1);
+  }
   __syncthreads();
+  int buf = 0;
   for (int G = 0; G < KG; ++G) {
-    const int buf = G & 1;
-    const bool more = G + 1 < KG;
-    if (more) {
-      a_load(G + 1);
-      b_load(G + 1, bn);
+    const bool more2 = G + 2 < KG;
+    if (more2) {
+      a_load(G + 2, a2);
+      b_load(G + 2, b2);
     }
     compute(buf, bc);
-    if (more) a_store(buf ^ 1);
+    const int nbuf = buf == kStages - 1 ? 0 : buf + 1;
+    if (G + 1 < KG) a_store(nbuf, a1);
     __syncthreads();
+    buf = nbuf;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bc[j] = bn[j];
+    for (int i = 0; i < NA; ++i) a1[i] = a2[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bc[j] = b1[j];
+      b1[j] = b2[j];
+    }
   }
 
   // ---- epilogue: lane (column jc, row rr of each A tile)
@@ -175,16 +198,17 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
   }
   if constexpr (EPI == EPI_SWIGLU) {
-    // gate values of wave (wa, 0) -> LDS -> wave (wa, 1)
+    // gate values of wave (wa, sub) -> LDS -> up wave (wa, sub)
     float *xg = reinterpret_cast<float *>(lds);
-    if (wb == 0) {
+    const int xo = (wa * (kWB / 2) + sub) * 16;
+    if (half == 0) {
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xg[((wa * 4 + a) * 4 + j) * 64 + lane] = v[a][j];
+        for (int j = 0; j < 4; ++j) xg[(xo + a * 4 + j) * 64 + lane] = v[a][j];
     }
     __syncthreads();
-    if (wb == 1) {
+    if (half == 1) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const int row = r0 + 4 * (4 * wa + a) + rr;
@@ -192,7 +216,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           if (!pv[j]) continue;
-          const float gt = xg[((wa * 4 + a) * 4 + j) * 64 + lane], up = v[a][j];
+          const float gt = xg[(xo + a * 4 + j) * 64 + lane], up = v[a][j];
           sw_out[(size_t)row * ldo_sw + col[j] + jc] = up * gt * (1.0f / (1.0f + expf(-gt)));
         }
       }
@@ -232,7 +256,7 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
   for (int i = 0; i < g.nseg; ++i)
     MS_CHECK_ARG(g.seg[i].w && g.seg[i].n_cols > 0 && g.seg[i].n_cols % 16 == 0,
                  "GEMM: segment columns must be a positive multiple of 16");
-  const dim3 blk(256);
+  const dim3 blk(kNT);
   const int gy = gemm_row_pad(g.M) / kBM;
   switch (g.epi) {
     case EPI_STORE:
@@ -242,7 +266,7 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
       MS_CHECK_ARG(g.epi != EPI_RESID || g.resid, "GEMM: residual missing");
       int np = 0;
       for (int i = 0; i < g.nseg; ++i) np += g.seg[i].n_cols / 16;
-      const dim3 grid((np + 7) / 8, gy);
+      const dim3 grid((np + 4 * kWB - 1) / (4 * kWB), gy);
       if (g.epi == EPI_STORE)
         hipLaunchKernelGGL(k_gemm<EPI_STORE>, grid, blk, kGemmLds, st, g);
       else if (g.epi == EPI_ACCUMULATE)
@@ -254,7 +278,7 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
     case EPI_SWIGLU: {
       MS_CHECK_ARG(g.nseg == 2 && g.seg[0].n_cols == g.seg[1].n_cols && g.sw_out,
                    "GEMM: SwiGLU needs gate and up of equal width and an output");
-      const dim3 grid((g.seg[0].n_cols / 16 + 3) / 4, gy);
+      const dim3 grid((g.seg[0].n_cols / 16 + 2 * kWB - 1) / (2 * kWB), gy);
       hipLaunchKernelGGL(k_gemm<EPI_SWIGLU>, grid, blk, kGemmLds, st, g);
       break;
     }
