@@ -143,6 +143,26 @@ def traffic_from_profile():
     return None
 
 
+def measure_ttft(ms, prompts, seed):
+    """TTFT: prompt ids on the host -> first greedy id on the host, one fresh
+    E4B-shape model per prompt length (after a short warm-up prefill)."""
+    import numpy as np
+    ttft = {}
+    for P in prompts:
+        mt = ms.Model(ms.arch_e4b(max_full_seq=P + 8), max_seqs=1, max_rows=16, max_pos=P + 8)
+        mt.fill_synthetic(seed)
+        pr = [int(v % 262144) for v in ms.host_random_u8(4 * P, 9, 3).view(np.uint32)]
+        mt.prefill(pr[:16], 0)  # warm-up of the prefill kernels
+        mt.reset()
+        ms.synchronize()
+        t0 = time.perf_counter()
+        mt.prefill(pr, 0)
+        ttft[P] = (time.perf_counter() - t0) * 1e3
+        log(f"TTFT prompt {P}: {ttft[P]:.1f} ms")
+        mt.close()
+    return ttft
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,7 +173,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time the decode with eager launches")
-    ap.add_argument("--only", choices=["all", "decode"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "ttft"], default="all",
+                    help="decode: batch-1 decode only; ttft: prefill (TTFT) only")
     ap.add_argument("--prof-tokens", type=int, default=16)
     ap.add_argument("--rocpd-summary", metavar="DB", help="summarize a rocprofv3 database and exit")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -185,6 +206,11 @@ def main():
     ms.init(0)
     name, ncu, hbm = ms.device_info()
     log(f"device {name} CUs={ncu}")
+    if args.only == "ttft":
+        ttft = measure_ttft(ms, sorted({args.ttft_prompt, 2048}), args.seed)
+        print(json.dumps({"ttft_ms": {str(k): round(v, 2) for k, v in ttft.items()},
+                          "device": name}))
+        return
     max_pos = max(args.prompt + args.warmup + args.steps + args.prof_tokens + 8,
                   args.ttft_prompt + 8)
     arch = ms.arch_e4b(max_full_seq=max_pos)
@@ -282,23 +308,7 @@ def main():
         out["batch4_tokens_per_s"] = round(tps4, 2)
         m.close()
 
-        # ---- TTFT (prompt ids on host -> first id on host) --------------------------
-        ttft = {}
-        for P in sorted({args.ttft_prompt, 2048}):
-            if P > max_pos - 8:
-                continue
-            mt = ms.Model(ms.arch_e4b(max_full_seq=max_pos), max_seqs=1, max_rows=16,
-                          max_pos=max_pos)
-            mt.fill_synthetic(args.seed)
-            pr = [int(v % arch.vocab) for v in ms.host_random_u8(4 * P, 9, 3).view(np.uint32)]
-            mt.prefill(pr[:16], 0)  # warm-up of the prefill kernels
-            mt.reset()
-            ms.synchronize()
-            t0 = time.perf_counter()
-            mt.prefill(pr, 0)
-            ttft[P] = (time.perf_counter() - t0) * 1e3
-            log(f"TTFT prompt {P}: {ttft[P]:.1f} ms")
-            mt.close()
+        ttft = measure_ttft(ms, sorted({args.ttft_prompt, 2048}), args.seed)
         out["ttft_ms"] = {str(k): round(v, 2) for k, v in ttft.items()}
     else:
         m.close()

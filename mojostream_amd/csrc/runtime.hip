@@ -98,7 +98,15 @@ extern "C" int ms_device_info(char *name, size_t name_len, int *n_cu, size_t *hb
   hipDeviceProp_t prop;
   MS_HIP_TRY(hipGetDeviceProperties(&prop, g_ctx.device));
   if (name && name_len) {
-    std::snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+    char dev[256] = {0};
+    if (prop.name[0])
+      std::snprintf(dev, sizeof dev, "%s", prop.name);
+    else if (hipDeviceGetName(dev, sizeof dev, g_ctx.device) != hipSuccess)
+      dev[0] = 0;
+    if (dev[0])
+      std::snprintf(name, name_len, "%s (%s)", dev, prop.gcnArchName);
+    else
+      std::snprintf(name, name_len, "%s", prop.gcnArchName);
   }
   if (n_cu) *n_cu = prop.multiProcessorCount;
   if (hbm_bytes) *hbm_bytes = prop.totalGlobalMem;
