@@ -552,14 +552,13 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
   // ---- prologue: activation limbs, overlapping the first weight batch
   if constexpr (AS == AS_ROWS) {
     // The row is tiny next to the weights, but its loads queue behind every
-    // weight load already in flight on the chip.  Only one super-tile per
-    // panel goes out before the row has arrived; the rest of the first batch
-    // follows, overlapping the norm and the quantization.
+    // weight load already in flight on the chip.  The weights go out once the
+    // row has arrived and overlap the norm and the quantization (issuing one
+    // or two super-tiles first measured slower for every projection).
     RowRegs<NT, rows_ng(W), false> R;
     row_load<NT, rows_ng(W), false>(rs, K, 0, R);
-    issue_part(0, 0, 1);
     asm volatile("" ::"v"(R.v[0][0]), "v"(R.v[rows_ng(W) - 1][7]) : "memory");
-    issue_part(0, 1, U);
+    issue_part(0, 0, U);
     int s;
     row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s);
     if (threadIdx.x == 0) row_s[0] = s;
