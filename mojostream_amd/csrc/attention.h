@@ -18,10 +18,13 @@ struct AttnArgs {
   float *kc, *vc;              // caches [B][cache_len][kv_dim]
   size_t cache_seq_stride;     // floats between sequences
   int n_chunks;                // chunks of kAttnChunk keys per (sequence, kv head)
-  float *part;                 // [B][n_kv][n_chunks][T*G][hd+2]
+  float *part;                 // attn_part_floats(B, n_kv, n_chunks, T, G, hd)
   // combine
   float *out;                  // [B*T][q_dim]
   int write_cache;
+  // decode (T == 1): per (sequence, kv head) count of finished chunk blocks;
+  // zero on entry, left zero on exit
+  unsigned *ctr;
 };
 
 constexpr int kAttnChunk = 16;
@@ -29,8 +32,15 @@ constexpr int kAttnMaxTG = 20;    // T * (n_heads / n_kv) per block
 constexpr int kAttnLds = 10240;   // floats of q staging
 constexpr int kAttnMaxChunks = 512;
 
-// Scores + chunk softmax + P.V partials, then the merge of the chunks with the
-// cache append of the rows (two launches).
+// Floats of AttnArgs::part for B sequences of T rows in n_chunks key chunks.
+inline size_t attn_part_floats(int B, int n_kv, int n_chunks, int T, int G, int hd) {
+  return (size_t)B * n_kv * ((size_t)n_chunks * T * G * (hd + 2) + 4);
+}
+
+// T == 1 (decode): one launch; the chunk blocks append the row to the cache and
+// the last block of each (sequence, kv head) merges the chunks (needs a.ctr).
+// T > 1: scores + chunk softmax + P.V partials, then the merge of the chunks
+// with the cache append of the rows (two launches).
 int launch_attention(const AttnArgs &a, hipStream_t st);
 int attn_check(const AttnArgs &a);
 

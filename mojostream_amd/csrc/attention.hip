@@ -53,6 +53,7 @@ struct AttnP {
   const float *qkv, *cos_t, *sin_t;
   const int32_t *pos;
   float *kc, *vc, *part, *out;
+  unsigned *ctr;
   size_t cache_seq_stride;
 };
 
@@ -82,6 +83,7 @@ __device__ inline AttnP load_params(const AttnArgs &a) {
   p.vc = keep(a.vc);
   p.part = keep(a.part);
   p.out = keep(a.out);
+  p.ctr = keep(a.ctr);
   p.cache_seq_stride = keep(a.cache_seq_stride);
   return p;
 }
@@ -158,7 +160,7 @@ constexpr int kRopeBatch = 8;  // q elements per thread per load batch
 // the score loop is unconditional.
 template <int HD, int TGM>
 __global__ __launch_bounds__(256) void k_attn_chunks(AttnArgs args) {
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   constexpr int CH = kAttnChunk;
   constexpr int F4 = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
   constexpr int NV = HD / 64;            // float4 per thread per key (scores)
@@ -502,9 +504,12 @@ int attn_check(const AttnArgs &a) {
   return MS_OK;
 }
 
+static int launch_attention_decode(const AttnArgs &a, hipStream_t st);
+
 int launch_attention(const AttnArgs &a, hipStream_t st) {
   if (int rc = attn_check(a)) return rc;
   MS_CHECK_ARG(a.qkv && a.part && a.pos && a.out, "attention: missing buffers");
+  if (a.T == 1) return launch_attention_decode(a, st);
   const int G = a.n_heads / a.n_kv;
   const int TR = std::max(1, std::min(a.T, kAttnMaxTG / G));
   const int RG = (a.T + TR - 1) / TR;
@@ -806,6 +811,403 @@ int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, hipStream_
 #undef MS_FLASH
   if (a.write_cache)
     hipLaunchKernelGGL(k_cache_append, dim3(a.T), dim3(256), 0, st, a, (const float *)kr);
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
+}
+
+// ------------------------------------------------------------------------------
+// Decode attention: one row per sequence (T == 1), one launch.
+//
+//  k_attn_decode  one block per (16-slot chunk of the cache, sequence x kv
+//                 head).  Chunk c covers cache slots 16c..16c+15 at every
+//                 position: slot j of a circular cache holds position
+//                 base - ((base - j) mod W), slot j of a linear cache position
+//                 j.  Softmax does not depend on the order of the keys, so the
+//                 slot order serves, and a circular cache's rows are loaded
+//                 before the position arrives.  The slot of the current
+//                 position takes the row's fresh k (after RoPE) and v; the
+//                 block holding it also appends them to the cache, which is
+//                 safe because no other block reads that slot and the row it
+//                 replaces has left the window.  Each block writes (max, sum,
+//                 o[hd]) per query head with agent-coherent stores and counts
+//                 itself done; the last block of a (sequence, kv head) merges
+//                 the chunks and resets the counter for the next launch.
+// ------------------------------------------------------------------------------
+__device__ inline void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_agent(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float lane_of(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ inline float wave64_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
+}
+__device__ inline float wave64_sum(float v) {
+  v = row16_sum(v);
+  return (lane_of(v, 0) + lane_of(v, 16)) + (lane_of(v, 32) + lane_of(v, 48));
+}
+
+// Partner dim of d under RoPE and the rotation of x (partner y) at position
+// pos; the same arithmetic as rope_apply.
+__device__ inline int rope_partner(const AttnP &p, int d) {
+  const bool rot = p.apply_rope && d < p.rot;
+  return rot ? (d < p.half ? d + p.half : d - p.half) : d;
+}
+__device__ inline void rope_cs(const AttnP &p, int d, int pos, float &c, float &s) {
+  const bool rot = p.apply_rope && d < p.rot;
+  const int i = d < p.half ? d : d - p.half;
+  const size_t ti = rot ? (size_t)pos * p.half + i : 0;
+  c = rot ? aldg<float>(p.cos_t + ti) : 1.f;
+  s = rot ? aldg<float>(p.sin_t + ti) : 0.f;
+}
+__device__ inline float rope_mix(const AttnP &p, int d, float x, float y, float c, float s) {
+  if (!(p.apply_rope && d < p.rot)) return x;
+  return d < p.half ? x * c - y * s : y * s + x * c;
+}
+
+constexpr int kDecMergeChunks = 16;  // chunk partials per merge load batch
+constexpr int kSc1 = 16;             // buffer cache policy: sc1 (agent-coherent)
+
+template <int HD, int TGM>
+__global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
+  // 16-byte aligned: the float4 LDS accesses below (a static variable placed
+  // first would otherwise shift the dynamic region by its size)
+  extern __shared__ __align__(16) float lds[];
+  __shared__ int s_last;
+  constexpr int CH = kAttnChunk;
+  constexpr int F4 = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
+  constexpr int NV = HD / 64;            // float4 per thread per key (scores)
+  constexpr int DPT = (HD + 255) / 256;  // head dims per thread
+  const AttnP p = load_params(args);
+  const int tid = threadIdx.x;
+  const int c = blockIdx.x;
+  const int b = (int)blockIdx.y / p.n_kv, h = (int)blockIdx.y % p.n_kv;
+  const int G = p.G;
+  const int L = p.cache_len;
+  const int nq = G * HD;
+
+  float *sk = lds;              // [CH][HD] keys of the chunk
+  float *sv = sk + CH * HD;     // [CH][HD] values
+  float *sq = sv + CH * HD;     // [TGM][HD] rotated queries
+  float *ss = sq + TGM * HD;    // [TGM][CH] scores -> probabilities
+  float *sm = ss + TGM * CH;    // [TGM]
+  float *sl = sm + TGM;         // [TGM]
+  float *wsh = sl + TGM;        // [n_chunks][G] merge weights (last block)
+  const size_t cbase = (size_t)b * p.cache_seq_stride;
+  const float *qrow = p.qkv + (size_t)b * p.ld;
+
+  // ---- loads that do not depend on the position: the position itself, a
+  // circular cache's rows, the raw q of the first batch, the fresh k and v
+  const int base = aldg<int32_t>(p.pos + b);
+  float4 kr[F4], vr[F4];
+#pragma unroll
+  for (int j = 0; j < F4; ++j) {
+    kr[j] = float4{0.f, 0.f, 0.f, 0.f};
+    vr[j] = float4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (p.circular) {
+#pragma unroll
+    for (int j = 0; j < F4; ++j) {
+      const int f = tid + 256 * j;
+      const int slot = c * CH + f / (HD / 4), d4 = f % (HD / 4);
+      if (slot < L) {
+        const size_t off = cbase + (size_t)slot * p.kv_dim + h * HD + 4 * d4;
+        kr[j] = aldg<float4>(p.kc + off);
+        vr[j] = aldg<float4>(p.vc + off);
+      }
+    }
+  }
+  float qx[kRopeBatch], qy[kRopeBatch];
+#pragma unroll
+  for (int u = 0; u < kRopeBatch; ++u) {
+    const int e = tid + 256 * u;
+    qx[u] = qy[u] = 0.f;
+    if (e < nq) {
+      const int g = e / HD, d = e % HD;
+      const float *qh = qrow + (h * G + g) * HD;
+      qx[u] = aldg<float>(qh + d);
+      qy[u] = aldg<float>(qh + rope_partner(p, d));
+    }
+  }
+  float kx[DPT], ky[DPT], vx[DPT];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = tid + 256 * j;
+    kx[j] = ky[j] = vx[j] = 0.f;
+    if (d < HD) {
+      const float *kh = qrow + p.q_dim + h * HD;
+      kx[j] = aldg<float>(kh + d);
+      ky[j] = aldg<float>(kh + rope_partner(p, d));
+      vx[j] = aldg<float>(qrow + p.q_dim + p.kv_dim + h * HD + d);
+    }
+  }
+
+  // ---- the position: attended slots [0, nslots), the slot of this row
+  int lo, hi;
+  key_range(p, base, &lo, &hi);
+  const int nslots = p.circular ? min(L, base + 1) : min(hi + 1, L);
+  const int n_active = (nslots + CH - 1) / CH;
+  if (c >= n_active) return;
+  const int fslot = p.circular ? base % L : base;
+  const bool fresh_here = fslot < nslots && fslot / CH == c;
+  if (!p.circular) {
+#pragma unroll
+    for (int j = 0; j < F4; ++j) {
+      const int f = tid + 256 * j;
+      const int slot = c * CH + f / (HD / 4), d4 = f % (HD / 4);
+      if (slot < nslots) {
+        const size_t off = cbase + (size_t)slot * p.kv_dim + h * HD + 4 * d4;
+        kr[j] = aldg<float4>(p.kc + off);
+        vr[j] = aldg<float4>(p.vc + off);
+      }
+    }
+  }
+  float qc[kRopeBatch], qs[kRopeBatch];
+#pragma unroll
+  for (int u = 0; u < kRopeBatch; ++u) {
+    const int e = tid + 256 * u;
+    qc[u] = 1.f;
+    qs[u] = 0.f;
+    if (e < nq) rope_cs(p, e % HD, base, qc[u], qs[u]);
+  }
+  float kc_[DPT], ks_[DPT];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = tid + 256 * j;
+    kc_[j] = 1.f;
+    ks_[j] = 0.f;
+    if (fresh_here && d < HD) rope_cs(p, d, base, kc_[j], ks_[j]);
+  }
+
+  // cached rows (zeros for slots past the attended ones, so 0 * v stays
+  // finite); the fresh slot is filled below
+#pragma unroll
+  for (int j = 0; j < F4; ++j) {
+    const int f = tid + 256 * j;
+    const int slot = c * CH + f / (HD / 4);
+    if (slot >= nslots) {
+      kr[j] = float4{0.f, 0.f, 0.f, 0.f};
+      vr[j] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (!(fresh_here && slot == fslot)) {
+      reinterpret_cast<float4 *>(sk)[f] = kr[j];
+      reinterpret_cast<float4 *>(sv)[f] = vr[j];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kRopeBatch; ++u) {
+    const int e = tid + 256 * u;
+    if (e < nq) sq[e] = rope_mix(p, e % HD, qx[u], qy[u], qc[u], qs[u]);
+  }
+  // q elements past the first batch (more than 2048 per kv head)
+  for (int e = 256 * kRopeBatch + tid; e < nq; e += 256) {
+    const int g = e / HD, d = e % HD;
+    const float *qh = qrow + (h * G + g) * HD;
+    float cc, sn;
+    rope_cs(p, d, base, cc, sn);
+    sq[e] = rope_mix(p, d, aldg<float>(qh + d), aldg<float>(qh + rope_partner(p, d)), cc, sn);
+  }
+  for (int e = nq + tid; e < TGM * HD; e += 256) sq[e] = 0.f;
+  if (fresh_here) {
+    // write_kv_sliding / write_kv_full (gemma4_e4b.mojo:211-249)
+    const int kf = fslot - c * CH;
+    const size_t off = cbase + (size_t)fslot * p.kv_dim + h * HD;
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) {
+      const int d = tid + 256 * j;
+      if (d < HD) {
+        const float kv = rope_mix(p, d, kx[j], ky[j], kc_[j], ks_[j]);
+        sk[kf * HD + d] = kv;
+        sv[kf * HD + d] = vx[j];
+        if (p.write_cache) {
+          p.kc[off + d] = kv;
+          p.vc[off + d] = vx[j];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- scores: thread (key kk, dim group dg of 16 lanes), row sums by DPP
+  const int kk = tid >> 4, dg = tid & 15;
+  float acc[TGM];
+#pragma unroll
+  for (int i = 0; i < TGM; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int d = dg * 4 + 64 * i;
+    const float4 kv = *reinterpret_cast<const float4 *>(sk + kk * HD + d);
+#pragma unroll
+    for (int t = 0; t < TGM; ++t) {
+      const float4 qq = *reinterpret_cast<const float4 *>(sq + t * HD + d);
+      acc[t] += qq.x * kv.x + qq.y * kv.y + qq.z * kv.z + qq.w * kv.w;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TGM; ++t) acc[t] = row16_sum(acc[t]);
+  if (dg == 0) {
+    const bool ok = c * CH + kk < nslots;
+#pragma unroll
+    for (int t = 0; t < TGM; ++t)
+      if (t < G) ss[t * CH + kk] = ok ? acc[t] * p.scale : -INFINITY;
+  }
+  __syncthreads();
+  // softmax of the chunk: query head t on a 16-lane row, lane = key
+  for (int t = tid >> 4; t < G; t += 16) {
+    const int k = tid & 15;
+    const float sc = ss[t * CH + k];
+    const float m = row16_max(sc);
+    const float pr = (sc == -INFINITY) ? 0.f : expf(sc - m);
+    const float l = row16_sum(pr);
+    ss[t * CH + k] = pr;
+    if (k == 0) {
+      sm[t] = m;
+      sl[t] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- P.V of the chunk on float4 units (head t, dims 4u..4u+3).  Partials:
+  // o [n_chunks][G][HD] then (max, sum) [n_chunks][G][2] per (sequence, kv
+  // head), written with agent-coherent (sc1) stores
+  constexpr int H4 = HD / 4;
+  const int nu = G * H4;
+  const size_t bh_stride = ((size_t)p.n_chunks * G * (HD + 2) + 3) & ~(size_t)3;
+  float *po = p.part + (size_t)(b * p.n_kv + h) * bh_stride;
+  float *pml = po + (size_t)p.n_chunks * G * HD;
+  const __amdgpu_buffer_rsrc_t rs_o =
+      __builtin_amdgcn_make_buffer_rsrc(po, 0, p.n_chunks * G * HD * 4, 0x00020000);
+  float *orow = p.out + (size_t)b * p.q_dim + h * G * HD;
+  const float4 *sv4 = reinterpret_cast<const float4 *>(sv);
+  for (int u = tid; u < nu; u += 256) {
+    const int t = u / H4, d4 = u % H4;
+    af32x4 o = af32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const float pk = ss[t * CH + k];
+      const float4 v = sv4[k * H4 + d4];
+      o.x += pk * v.x;
+      o.y += pk * v.y;
+      o.z += pk * v.z;
+      o.w += pk * v.w;
+    }
+    if (n_active == 1) {
+      // the only chunk: weight 1 / sum, as in the merge
+      const float w = 1.0f / sl[t];
+      *reinterpret_cast<float4 *>(orow + 4 * u) = float4{o.x * w, o.y * w, o.z * w, o.w * w};
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b128(o, rs_o, ((c * G + t) * HD + 4 * d4) * 4, 0,
+                                             kSc1);
+    }
+  }
+  if (n_active == 1) return;
+  if (tid < G) {
+    st_agent(pml + (c * G + tid) * 2, sm[tid]);
+    st_agent(pml + (c * G + tid) * 2 + 1, sl[tid]);
+  }
+
+  // ---- count this block done; the last one merges
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();
+  if (tid == 0) {
+    unsigned *ctr = p.ctr + b * p.n_kv + h;
+    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = old + 1 == (unsigned)n_active;
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // chunk weights exp(m_c - M) / L per query head: wave w takes heads w, w+4..
+  const int wave = tid >> 6, lane = tid & 63;
+  constexpr int MPL = kAttnMaxChunks / 64;  // chunks per lane
+  for (int g = wave; g < G; g += 4) {
+    float mc[MPL], lc[MPL];
+#pragma unroll
+    for (int i = 0; i < MPL; ++i) {
+      const int cc = lane + 64 * i;
+      mc[i] = -INFINITY;
+      lc[i] = 0.f;
+      if (cc < n_active) {
+        mc[i] = ld_agent(pml + (cc * G + g) * 2);
+        lc[i] = ld_agent(pml + (cc * G + g) * 2 + 1);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MPL; ++i) mx = fmaxf(mx, mc[i]);
+    const float M = wave64_max(mx);
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < MPL; ++i) {
+      mc[i] = (mc[i] == -INFINITY) ? 0.f : expf(mc[i] - M);
+      part += lc[i] * mc[i];
+    }
+    const float inv = 1.0f / wave64_sum(part);
+#pragma unroll
+    for (int i = 0; i < MPL; ++i) {
+      const int cc = lane + 64 * i;
+      if (cc < n_active) wsh[cc * G + g] = mc[i] * inv;
+    }
+  }
+  __syncthreads();
+  // o = sum_c w_c o_c, 16-byte agent-coherent loads in batches of CB chunks
+  constexpr int CB = kDecMergeChunks;
+  for (int u = tid; u < nu; u += 256) {
+    const int t = u / H4, d4 = u % H4;
+    float4 o = float4{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < n_active; c0 += CB) {
+      af32x4 v[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const int cc = min(c0 + j, n_active - 1);
+        v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs_o, ((cc * G + t) * HD + 4 * d4) * 4, 0,
+                                                     kSc1);
+      }
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const float w = c0 + j < n_active ? wsh[(c0 + j) * G + t] : 0.f;
+        o.x += v[j].x * w;
+        o.y += v[j].y * w;
+        o.z += v[j].z * w;
+        o.w += v[j].w * w;
+      }
+    }
+    *reinterpret_cast<float4 *>(orow + 4 * u) = o;
+  }
+}
+
+static size_t attn_decode_lds(const AttnArgs &a, int tgm) {
+  const int G = a.n_heads / a.n_kv;
+  return (size_t)(2 * kAttnChunk * a.hd + tgm * a.hd + tgm * kAttnChunk + 2 * tgm +
+                  a.n_chunks * G) * 4;
+}
+
+static int launch_attention_decode(const AttnArgs &a, hipStream_t st) {
+  MS_CHECK_ARG(a.ctr, "attention: decode needs the chunk counters");
+  const int G = a.n_heads / a.n_kv;
+  const int tgm = G <= 4 ? 4 : (G <= 8 ? 8 : kAttnMaxTG);
+  const dim3 grid(a.n_chunks, a.B * a.n_kv);
+  const size_t shmem = attn_decode_lds(a, tgm);
+#define MS_DEC(HDV)                                                                        \
+  if (tgm == 4)                                                                            \
+    hipLaunchKernelGGL((k_attn_decode<HDV, 4>), grid, dim3(256), shmem, st, a);           \
+  else if (tgm == 8)                                                                       \
+    hipLaunchKernelGGL((k_attn_decode<HDV, 8>), grid, dim3(256), shmem, st, a);           \
+  else                                                                                     \
+    hipLaunchKernelGGL((k_attn_decode<HDV, kAttnMaxTG>), grid, dim3(256), shmem, st, a)
+  switch (a.hd) {
+    case 64: MS_DEC(64); break;
+    case 128: MS_DEC(128); break;
+    case 256: MS_DEC(256); break;
+    default: MS_DEC(512); break;
+  }
+#undef MS_DEC
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }

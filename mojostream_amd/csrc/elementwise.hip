@@ -203,13 +203,15 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   const bool flash = T > kGemvMaxM && prefill_flash_ok(a);
   const size_t qkv_f = (size_t)T * ld;
   const size_t part_f = flash ? (size_t)T * (L->q_dim + L->kv_dim)
-                              : (size_t)a.n_kv * a.n_chunks * T * G * (a.hd + 2);
-  const size_t need = (qkv_f + part_f) * 4 + 64;
+                              : attn_part_floats(1, a.n_kv, a.n_chunks, T, G, a.hd);
+  const size_t need = (qkv_f + part_f) * 4 + 64 + (size_t)a.n_kv * 4;
   void *buf = nullptr;
   if (int rc = scratch(need, &buf)) return rc;
   float *qkv = static_cast<float *>(buf);
   float *part = qkv + qkv_f;
   int32_t *dpos = reinterpret_cast<int32_t *>(part + part_f);
+  unsigned *ctr = reinterpret_cast<unsigned *>(dpos + 16);
+  MS_HIP_TRY(hipMemsetAsync(ctr, 0, (size_t)a.n_kv * 4, st));
   MS_HIP_TRY(hipMemcpy2DAsync(qkv, ld * 4, d_q, L->q_dim * 4, L->q_dim * 4, T,
                               hipMemcpyDeviceToDevice, st));
   MS_HIP_TRY(hipMemcpy2DAsync(qkv + L->q_dim, ld * 4, d_knew, L->kv_dim * 4,
@@ -220,6 +222,7 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.qkv = qkv;
   a.part = part;
   a.pos = dpos;
+  a.ctr = ctr;
   if (flash) {
     if (int rc = launch_attention_prefill(a, part, part + (size_t)T * L->q_dim, st)) return rc;
   } else if (int rc = launch_attention(a, st)) {

@@ -83,7 +83,7 @@ struct ms_model {
   ms_model_desc d{};
   std::vector<ms::Layer> L;
   std::vector<ms::RopeTab> ropes;
-  int qkv_max = 0, q_max = 0, kv_max = 0, hd_max = 0;
+  int qkv_max = 0, q_max = 0, kv_max = 0, hd_max = 0, nkv_max = 0;
   int Mmax = 0;
   // LM head
   uint8_t *lm_w = nullptr;
@@ -102,6 +102,7 @@ struct ms_model {
   void *quant = nullptr;
   int quant_k = 0;
   float *qkv = nullptr, *attn_part = nullptr;
+  unsigned *attn_ctr = nullptr;  // decode chunk counters [seq][kv head], kept zero
   // prefill: rows per chunk (0: no prefill workspace), attention rows per
   // launch inside a chunk and their base positions on the device
   int prefill_rows = 0;
@@ -306,6 +307,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.cache_seq_stride = Ly.cache_seq_stride;
     a.n_chunks = Ly.n_chunks;
     a.part = m->attn_part;
+    a.ctr = m->attn_ctr;
     a.out = m->aO;
     a.write_cache = 1;
     // KV bytes read at the current position are counted by bench.py
@@ -614,13 +616,14 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
                                                         : ld.cache_len + attn_rows;
     Ly.n_chunks = cdiv(span, kAttnChunk);
     const int G = ld.n_heads / ld.n_kv_heads;
-    max_part = std::max(max_part, (size_t)d.max_seqs * ld.n_kv_heads * Ly.n_chunks *
-                                      attn_rows * G * (ld.head_dim + 2));
+    max_part = std::max(max_part, attn_part_floats(d.max_seqs, ld.n_kv_heads, Ly.n_chunks,
+                                                   attn_rows, G, ld.head_dim));
     m->qkv_max = std::max(m->qkv_max, ncols_qkv);
     m->q_max = std::max(m->q_max, ld.q_dim);
     m->quant_k = std::max(m->quant_k, std::max(std::max(d.hidden, d.ffn), ld.q_dim));
     m->kv_max = std::max(m->kv_max, ld.kv_dim);
     m->hd_max = std::max(m->hd_max, ld.head_dim);
+    m->nkv_max = std::max(m->nkv_max, ld.n_kv_heads);
     m->L.push_back(Ly);
   }
   int rc;
@@ -641,13 +644,15 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
     return cleanup(rc);
   if ((rc = dmalloc(m, (void **)&m->qkv, (size_t)M * m->qkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
+      (rc = dmalloc(m, (void **)&m->attn_ctr, (size_t)d.max_seqs * m->nkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->pos, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->tok, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->step, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->ids_hist, (size_t)m->hist_cap * d.max_seqs * 4)))
     return cleanup(rc);
   if (hipMemset(m->pos, 0, 64 * 4) != hipSuccess || hipMemset(m->step, 0, 64 * 4) != hipSuccess ||
-      hipMemset(m->tok, 0, 64 * 4) != hipSuccess)
+      hipMemset(m->tok, 0, 64 * 4) != hipSuccess ||
+      hipMemset(m->attn_ctr, 0, (size_t)d.max_seqs * m->nkv_max * 4) != hipSuccess)
     return cleanup(fail(MS_E_HIP, "model: memset failed"));
   // KV caches (zero-initialised like the reference's resized Lists)
   for (auto &Ly : m->L) {

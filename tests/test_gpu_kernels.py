@@ -177,6 +177,15 @@ ATTN_CASES = [
     ("g4-hd64", 1024, 256, 64, 16, 4, 0, 256, 0, 4, 200),
     ("14b", 5120, 1024, 128, 40, 8, 0, 4096, 0, 1, 4000),
     ("first-token", 2048, 512, 256, 8, 2, 1, 512, 0, 1, 0),
+    # one row: the fused decode kernel (fresh slot at chunk edges, clamp past
+    # the cache, one kv head for 20 query heads, head_dim 64 and 128)
+    ("decode-wrap-slot16", 2048, 512, 256, 8, 2, 1, 512, 0, 1, 528),
+    ("decode-wrap-last-slot", 2048, 512, 256, 8, 2, 1, 512, 0, 1, 1023),
+    ("decode-slot15", 2048, 512, 256, 8, 2, 1, 512, 0, 1, 15),
+    ("decode-full-clamp", 4096, 1024, 512, 8, 2, 0, 256, 1, 1, 300),
+    ("decode-demo-last", 1024, 256, 128, 8, 2, 0, 512, 0, 1, 511),
+    ("decode-g4-hd64", 1024, 256, 64, 16, 4, 0, 256, 0, 1, 200),
+    ("decode-g20", 2560, 128, 128, 20, 1, 1, 512, 0, 1, 900),
     # many rows of one sequence: the flash-attention prefill path
     ("prefill-sliding", 2048, 512, 256, 8, 2, 1, 512, 0, 200, 0),
     ("prefill-sliding-wrap", 2048, 512, 256, 8, 2, 1, 512, 0, 333, 650),
