@@ -552,13 +552,16 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
   // ---- prologue: activation limbs, overlapping the first weight batch
   if constexpr (AS == AS_ROWS) {
     // The row is tiny next to the weights, but its loads queue behind every
-    // weight load already in flight on the chip.  The weights go out once the
-    // row has arrived and overlap the norm and the quantization (issuing one
-    // or two super-tiles first measured slower for every projection).
+    // weight load already in flight on the chip, so the weights go out once
+    // the row has arrived and overlap the norm and the quantization.  A wave
+    // stalls at issue once the memory pipeline is full, which would hold up
+    // its share of the quantization: at most four loads per wave go out
+    // before it, the rest after the prologue.
+    constexpr int kEarly = (4 / P) < 1 ? 1 : ((4 / P) < U ? (4 / P) : U);
     RowRegs<NT, rows_ng(W), false> R;
     row_load<NT, rows_ng(W), false>(rs, K, 0, R);
     asm volatile("" ::"v"(R.v[0][0]), "v"(R.v[rows_ng(W) - 1][7]) : "memory");
-    issue_part(0, 0, U);
+    issue_part(0, 0, kEarly);
     int s;
     row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s);
     if (threadIdx.x == 0) row_s[0] = s;
@@ -568,6 +571,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
       if (threadIdx.x == 0) row_s[m] = s;
     }
     __syncthreads();
+    if constexpr (kEarly < U) issue_part(0, kEarly, U);
   } else {
     if ((int)threadIdx.x < M) row_s[threadIdx.x] = ldg<int32_t>(qr.shift + threadIdx.x);
     issue(0);
