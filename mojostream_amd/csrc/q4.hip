@@ -168,6 +168,21 @@ __device__ inline int limb_pos8(int k) {
   return (k >> 7) * 128 + ((k >> 5) & 3) * 32 + ((k >> 4) & 1) * 16 + ((k >> 3) & 1) * 8;
 }
 
+// Rows of the 4x4 byte matrix with rows a, b, c, d: word l holds byte l of
+// a, b, c, d (in that byte order).  v_perm_b32 picks bytes of {s0, s1} (s1 the
+// low word): two rounds of four permutes.
+__device__ inline void byte_transpose4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                       uint32_t (&r)[4]) {
+  const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+  const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);
+  const uint32_t cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);
+  r[0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);  // a0 b0 c0 d0
+  r[1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);
+  r[2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+  r[3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
+}
+
 // X = rint(v * mul) for eight consecutive rows; limb l of the group as its
 // low/high words.
 //
@@ -176,12 +191,6 @@ __device__ inline int limb_pos8(int k) {
 // X = sum_l (u_l - 128) 2^(8l), and u_l - 128 as a signed byte is u_l ^ 0x80.
 // The low word of limb l takes byte l of rows {0,4,1,5}, the high word rows
 // {2,6,3,7}.
-__device__ inline uint32_t byte_gather(uint32_t a, uint32_t b, uint32_t c, uint32_t d, int l) {
-  const int sh = 8 * l;
-  return ((a >> sh) & 0xFFu) | (((b >> sh) & 0xFFu) << 8) | (((c >> sh) & 0xFFu) << 16) |
-         (((d >> sh) & 0xFFu) << 24);
-}
-
 __device__ inline void quant8(const float (&v)[8], float mul, uint32_t (&lo)[4],
                               uint32_t (&hi)[4]) {
   uint32_t E[8];
@@ -190,11 +199,8 @@ __device__ inline void quant8(const float (&v)[8], float mul, uint32_t (&lo)[4],
     const int x = (int)rintf(v[e] * mul);
     E[e] = ((uint32_t)x + 0x80808080u) ^ 0x80808080u;
   }
-#pragma unroll
-  for (int l = 0; l < 4; ++l) {
-    lo[l] = byte_gather(E[0], E[4], E[1], E[5], l);
-    hi[l] = byte_gather(E[2], E[6], E[3], E[7], l);
-  }
+  byte_transpose4(E[0], E[4], E[1], E[5], lo);
+  byte_transpose4(E[2], E[6], E[3], E[7], hi);
 }
 
 // Per-row shift s with max|y| * 2^s < 2^30.
