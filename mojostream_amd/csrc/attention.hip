@@ -777,6 +777,9 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
 __global__ __launch_bounds__(256) void k_cache_append(AttnArgs args, const float *kr) {
   const AttnP p = load_params(args);
   const int r = blockIdx.x;
+  // a circular cache keeps the last cache_len rows; older rows of the call
+  // would share their slots with later ones
+  if (p.circular && r < p.T - p.cache_len) return;
   const int pt = aldg<int32_t>(p.pos) + r;
   if (!p.circular && pt >= p.cache_len) return;  // linear cache full: dropped
   const size_t cb = (size_t)cache_slot(p, pt) * p.kv_dim;

@@ -187,9 +187,12 @@ static void prof_collect() {
 
 // ---- per-layer enqueue --------------------------------------------------------
 // Prefill processes the prompt in chunks of up to kPrefillRows rows; their
-// projections run as GEMMs.  Attention over a chunk runs kPrefillAttnRows rows
-// per launch (its partial-result buffer grows with the rows of a launch).
-constexpr int kPrefillRows = 512;
+// projections run as GEMMs.  Flash attention takes a whole chunk per launch
+// (one block per 16 rows and kv head: long chunks fill the chip); the chunked
+// attention path runs kPrefillAttnRows rows per launch (its partial-result
+// buffer grows with the rows of a launch).  Workspace grows with the chunk:
+// about 170 KB per row at E4B shapes.
+constexpr int kPrefillRows = 2048;
 constexpr int kPrefillAttnRows = 32;
 
 struct RunCfg {

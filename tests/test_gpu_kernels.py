@@ -189,6 +189,8 @@ ATTN_CASES = [
     # many rows of one sequence: the flash-attention prefill path
     ("prefill-sliding", 2048, 512, 256, 8, 2, 1, 512, 0, 200, 0),
     ("prefill-sliding-wrap", 2048, 512, 256, 8, 2, 1, 512, 0, 333, 650),
+    # more rows than the window: only the last 512 reach the cache
+    ("prefill-sliding-long", 2048, 512, 256, 8, 2, 1, 512, 0, 700, 300),
     ("prefill-full", 4096, 1024, 512, 8, 2, 0, 4096, 1, 300, 100),
     ("prefill-full-clamp", 4096, 1024, 512, 8, 2, 0, 256, 1, 64, 230),
     ("prefill-demo", 1024, 256, 128, 8, 2, 0, 512, 0, 48, 17),

@@ -126,15 +126,17 @@ def test_e4b_full_greedy_ids(gpu, fast_oracle):
     m.close()
 
 
-@pytest.mark.parametrize("n_prompt", [100, 600])
+@pytest.mark.parametrize("n_prompt", [100, 600, 2100])
 def test_e4b_prefill_gemm_vs_oracle(gpu, fast_oracle, n_prompt):
     """Prompts longer than 16 rows run their projections as MFMA GEMMs and their
-    attention in row groups; 600 rows also cross the 512-row chunk and wrap the
-    sliding window.  Prefill + 7 decode steps must give the oracle's greedy ids."""
+    attention as flash attention over the chunk; 600 rows wrap the 512-slot
+    sliding window inside one chunk, 2100 rows also cross the 2048-row chunk.
+    Prefill + 7 decode steps must give the oracle's greedy ids."""
     ms = gpu
-    arch = ms.arch_e4b(max_full_seq=1024, n_layers=6, vocab=4096)
+    max_pos = 2400 if n_prompt > 1000 else 1024
+    arch = ms.arch_e4b(max_full_seq=max_pos, n_layers=6, vocab=4096)
     say(f"E4B shapes, 6 layers, vocab 4096: GEMM prefill of {n_prompt} tokens + 7 steps")
-    m = build(ms, arch, max_seqs=1, max_rows=4, max_pos=1024)
+    m = build(ms, arch, max_seqs=1, max_rows=4, max_pos=max_pos)
     om = synthetic_oracle_model(fast_oracle, arch, SEED)
     prompt = prompt_ids(n_prompt, arch.vocab, 3)
     first = m.prefill(prompt, 0)
