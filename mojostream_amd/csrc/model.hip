@@ -350,7 +350,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.ldo = D;
     a.resid = m->xn;
     ProfScope ps(PC_O, (double)d.q_dim * D / 2, st);
-    if (int rc2 = launch_proj(m, a, r, 4, st)) return rc2;
+    if (int rc2 = launch_proj(m, a, r, 8, st)) return rc2;
   }
   // 4. x2n = rmsnorm(x2) in the prologue, Gate|Up, SwiGLU epilogue
   {

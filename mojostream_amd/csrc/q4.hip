@@ -819,6 +819,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_GEMV(EPI_ACCUMULATE, 1, AS_QUANT, 4)
   MS_GEMV(EPI_ACCUMULATE, 4, AS_QUANT, 4)
   MS_GEMV(EPI_RESID, 1, AS_ROWS, 4)
+  MS_GEMV(EPI_RESID, 1, AS_ROWS, 8)
   MS_GEMV(EPI_RESID, 1, AS_ROWS, 16)
   MS_GEMV(EPI_RESID, 1, AS_QUANT, 4)
   MS_GEMV(EPI_SWIGLU, 2, AS_ROWS, 8)
