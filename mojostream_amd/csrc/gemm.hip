@@ -1,12 +1,16 @@
 // Q4 GEMM for prefill rows (M > 16) on v_mfma_i32_16x16x64_i8.
 //
-// The operands are those of the GEMV in q4.hip: activation rows quantized by
+// The A operand is that of the GEMV in q4.hip: activation rows quantized by
 // launch_quant_rows into four int8 limbs per value (limb row 4m + l, MFMA
-// fragment order inside each 128-row super-tile of K) and the weights as
-// signed bytes n - 8 straight from the panel layout.  Each limb row's dot
-// product is exact in int32; the four limbs of an output combine in int64 and
-// are scaled by 2^-s and the tensor scale with the GEMV's expression, so a
-// row gets the same value from this kernel as from the GEMV.
+// fragment order inside each 128-row super-tile of K).  The weights enter as
+// the unsigned nibbles n straight from the panel layout (a mask per dword,
+// where the GEMV's signed n - 8 takes three operations: the conversion is
+// most of this kernel's VALU work), and the zero point comes back per row:
+// sum_k X_k (n_k - 8) = sum_k X_k n_k - 8 * xsum, with xsum = sum_k X_k from
+// the quantization.  Each limb row's dot product is exact in int32; the four
+// limbs of an output combine in int64, minus 8 * xsum, and are scaled by 2^-s
+// and the tensor scale with the GEMV's expression, so a row gets the same
+// value from this kernel as from the GEMV.
 //
 // Tiling: a block computes kBM = 32 activation rows (128 limb rows, 8 MFMA A
 // tiles) by 4 kWB panels (8 panels, 128 columns).  Wave (wa, wb) owns A tiles
@@ -44,6 +48,7 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   const int M = launder(g.M), K = launder(g.K);
   const int8_t *limbs = launder(g.a.limbs);
   const int32_t *shift = launder(g.a.shift);
+  const int64_t *xsum = launder(g.a.xsum);
   const uint8_t *sw0 = launder(g.seg[0].w), *sw1 = launder(g.seg[1].w),
                 *sw2 = launder(g.seg[2].w);
   const float ss0 = launder(g.seg[0].scale), ss1 = launder(g.seg[1].scale),
@@ -136,7 +141,8 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t d0 = br[j][2 * h], d1 = br[j][2 * h + 1];
-        bf[j] = v4i{nib_s8(d0), nib_s8(d0 >> 4), nib_s8(d1), nib_s8(d1 >> 4)};
+        bf[j] = v4i{(int)(d0 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu),
+                    (int)(d1 & 0x0F0F0F0Fu), (int)((d1 >> 4) & 0x0F0F0F0Fu)};
       }
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
@@ -189,11 +195,12 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   for (int a = 0; a < 4; ++a) {
     const int row = r0 + 4 * (4 * wa + a) + rr;
     const float sc = row < M ? ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.f;
+    const long long z = row < M ? 8 * ldg<long long>(xsum + row) : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const v4i d = acc[a][j];
       const long long t = (long long)d[0] + ((long long)d[1] << 8) + ((long long)d[2] << 16) +
-                          ((long long)d[3] << 24);
+                          ((long long)d[3] << 24) - z;
       v[a][j] = (float)((double)t * (double)sc * (double)wsc[j]);
     }
   }
@@ -251,7 +258,7 @@ int gemm_row_pad(int M) { return (M + kBM - 1) / kBM * kBM; }
 int launch_gemm(const GemmArgs &g, hipStream_t st) {
   MS_CHECK_ARG(g.M >= 1 && g.K >= 128 && g.K % 128 == 0 && g.K <= kQuantMaxK,
                "GEMM: K must be a multiple of 128 in [128, 16384]");
-  MS_CHECK_ARG(g.a.limbs && g.a.shift, "GEMM: quantized rows missing");
+  MS_CHECK_ARG(g.a.limbs && g.a.shift && g.a.xsum, "GEMM: quantized rows missing");
   MS_CHECK_ARG(g.nseg >= 1 && g.nseg <= 3, "GEMM: 1..3 weight segments");
   for (int i = 0; i < g.nseg; ++i)
     MS_CHECK_ARG(g.seg[i].w && g.seg[i].n_cols > 0 && g.seg[i].n_cols % 16 == 0,

@@ -49,6 +49,8 @@ struct RowSrc {
 struct QuantRows {
   int8_t *limbs;
   int32_t *shift;
+  int64_t *xsum;  // sum over the row of X (launch_quant_rows); the GEMM feeds
+                  // unsigned nibbles n and subtracts 8 * xsum
 };
 
 struct GemvArgs {
@@ -108,7 +110,8 @@ int launch_gemv(const GemvArgs &a, hipStream_t st);
 size_t gemv_lds_need(const GemvArgs &a);
 // Quantize M rows of length K (one block per row) into q.
 int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st);
-// Device bytes of a QuantRows buffer for M rows of length K (limbs, shifts).
+// Device bytes of a QuantRows buffer for M rows of length K (limbs, shifts,
+// row sums).
 size_t quant_rows_bytes(int M, int K);
 // Carve a QuantRows view out of one buffer of quant_rows_bytes(M, K).
 QuantRows quant_rows_view(void *buf, int M, int K);

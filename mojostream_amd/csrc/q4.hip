@@ -191,14 +191,19 @@ __device__ inline void byte_transpose4(uint32_t a, uint32_t b, uint32_t c, uint3
 // X = sum_l (u_l - 128) 2^(8l), and u_l - 128 as a signed byte is u_l ^ 0x80.
 // The low word of limb l takes byte l of rows {0,4,1,5}, the high word rows
 // {2,6,3,7}.
+// *xs (XS): the sum of the eight X values.
+template <bool XS = false>
 __device__ inline void quant8(const float (&v)[8], float mul, uint32_t (&lo)[4],
-                              uint32_t (&hi)[4]) {
+                              uint32_t (&hi)[4], long long *xs = nullptr) {
   uint32_t E[8];
+  long long sum = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int x = (int)rintf(v[e] * mul);
+    if (XS) sum += x;
     E[e] = ((uint32_t)x + 0x80808080u) ^ 0x80808080u;
   }
+  if (XS) *xs += sum;
   byte_transpose4(E[0], E[4], E[1], E[5], lo);
   byte_transpose4(E[2], E[6], E[3], E[7], hi);
 }
@@ -275,10 +280,12 @@ __device__ inline void block_sum_max(float &ss, float &mx, float *sh) {
 // ple_scale_inplace :506-516, rmsnorm_weighted_inplace :598-613), optional
 // fp32 stores by `writer`, quantization and limb stores: limb l of row m goes
 // to dst + (4m + l) * ld_dst + limb position.  Returns the row shift s.
-template <int NT, int NG, bool GAM>
+// XS: also the row's sum of X, exact (integer partial sums below 2^53 add
+// exactly in double), into *xsum_out for every thread.
+template <int NT, int NG, bool GAM, bool XS = false>
 __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
                                   RowRegs<NT, NG, GAM> &R, int8_t *dst, size_t ld_dst,
-                                  float *sh, int *s_out) {
+                                  float *sh, int *s_out, double *xsum_out = nullptr) {
   const int nq = K >> 3;
   float y[NG][8];
   float ss = 0.f, mx = 0.f;
@@ -319,6 +326,7 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
   }
   const int s = row_shift(amax);
   const float mul = ldexpf(1.0f, s);
+  long long xs = 0;
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     const int q = (int)threadIdx.x + gi * NT;
@@ -337,28 +345,45 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
       }
     }
     uint32_t lo[4], hi[4];
-    quant8(y[gi], mul, lo, hi);
+    quant8<XS>(y[gi], mul, lo, hi, &xs);
     const int pos = limb_pos8(8 * q);
 #pragma unroll
     for (int l = 0; l < 4; ++l)
       *reinterpret_cast<uint2 *>(dst + (size_t)(4 * m + l) * ld_dst + pos) = uint2{lo[l], hi[l]};
   }
   *s_out = s;
+  if constexpr (XS) {
+    double v = (double)xs;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();
+    double *shd = reinterpret_cast<double *>(sh);
+    if ((threadIdx.x & 63) == 0) shd[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) t += shd[i];
+    *xsum_out = t;
+  }
 }
 
 template <bool GAM>
 __global__ __launch_bounds__(1024) void k_quant_rows(RowSrc r, int K, QuantRows q) {
-  __shared__ float sh[32];
+  __shared__ __align__(8) float sh[32];  // also 16 doubles (row sum)
   RowRegs<1024, 2, GAM> R;
   const int m = blockIdx.x;
   row_load<1024, 2, GAM>(r, K, m, R);
   int s;
-  row_finish<1024, 2, GAM>(r, K, m, true, R, q.limbs, K, sh, &s);
-  if (threadIdx.x == 0) q.shift[m] = s;
+  double xs;
+  row_finish<1024, 2, GAM, true>(r, K, m, true, R, q.limbs, K, sh, &s, &xs);
+  if (threadIdx.x == 0) {
+    q.shift[m] = s;
+    q.xsum[m] = (int64_t)xs;
+  }
 }
 
 size_t quant_rows_bytes(int M, int K) {
-  return (size_t)4 * M * K + 64 + (size_t)M * 4;
+  return (size_t)4 * M * K + 64 + (size_t)M * 4 + 64 + (size_t)M * 8;
 }
 
 QuantRows quant_rows_view(void *buf, int M, int K) {
@@ -367,13 +392,15 @@ QuantRows quant_rows_view(void *buf, int M, int K) {
   q.limbs = reinterpret_cast<int8_t *>(b);
   const size_t o1 = ((size_t)4 * M * K + 63) & ~(size_t)63;
   q.shift = reinterpret_cast<int32_t *>(b + o1);
+  const size_t o2 = (o1 + (size_t)M * 4 + 63) & ~(size_t)63;
+  q.xsum = reinterpret_cast<int64_t *>(b + o2);
   return q;
 }
 
 int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st) {
   MS_CHECK_ARG(M >= 1 && K >= 8 && K % 8 == 0 && K <= kQuantMaxK,
                "quant: row length must be a multiple of 8 in [8, 16384]");
-  MS_CHECK_ARG(r.x && r.ld >= K && q.limbs && q.shift, "quant: missing buffers");
+  MS_CHECK_ARG(r.x && r.ld >= K && q.limbs && q.shift && q.xsum, "quant: missing buffers");
   if (r.gamma)
     hipLaunchKernelGGL(k_quant_rows<true>, dim3(M), dim3(1024), 0, st, r, K, q);
   else
