@@ -846,7 +846,11 @@ extern "C" int ms_model_reset(ms_model *m) {
   MS_CHECK_ARG(m, "reset: null model");
   std::fill(m->h_pos.begin(), m->h_pos.end(), 0);
   // positions restart at 0; stale cache contents are never read (every read
-  // position < the current position has been rewritten since the reset)
+  // position < the current position has been rewritten since the reset).
+  // The decode attention's chunk counters are left zero by every completed
+  // launch; clearing them here also recovers from an interrupted one.
+  if (int rc = require_init()) return rc;
+  MS_HIP_TRY(hipMemset(m->attn_ctr, 0, (size_t)m->d.max_seqs * m->nkv_max * 4));
   return MS_OK;
 }
 
