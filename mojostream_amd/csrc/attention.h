@@ -25,6 +25,9 @@ struct AttnArgs {
   // decode (T == 1): per (sequence, kv head) count of finished chunk blocks;
   // zero on entry, left zero on exit
   unsigned *ctr;
+  // prefill: first position of the rows as the host expects it; it sizes the
+  // key split and nothing else (the kernels read pos)
+  int plan_pos;
 };
 
 constexpr int kAttnChunk = 16;
@@ -50,6 +53,21 @@ int attn_check(const AttnArgs &a);
 // cache append of the rows.  Needs 4 query heads per kv head and head_dim
 // 128, 256 or 512 (prefill_flash_ok); a.part is not used.
 bool prefill_flash_ok(const AttnArgs &a);
-int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, hipStream_t st);
+// Row tiles attending to many keys split their key tiles over several blocks
+// (so that the launch fills the CUs), merged by a second launch.  The split
+// plan follows T, cache_len, n_kv and a.plan_pos; the splits' partials need
+// flash_part_floats(a) floats of fpart (0: no split), never more than
+// flash_part_floats_max(hd).  With a smaller or null fpart the launch does not
+// split.
+struct FlashSplit {
+  int st_tiles;  // key tiles per split
+  int maxs;      // blocks per row tile (1: no split)
+  int n_rt;      // row tiles
+  float *part;   // per block: o [16 rows][4 heads][hd], then (max, sum) [16][4][2]
+};
+size_t flash_part_floats(const AttnArgs &a);
+size_t flash_part_floats_max(int hd);
+int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, float *fpart,
+                             size_t fpart_floats, hipStream_t st);
 
 }  // namespace ms

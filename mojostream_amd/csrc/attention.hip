@@ -610,7 +610,7 @@ constexpr int flash_lds_floats() {
 
 template <int HD, int DS>
 __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const float *qr,
-                                                            const float *kr) {
+                                                            const float *kr, FlashSplit fs) {
   constexpr int NT = 256 * DS;
   constexpr int HW = HD / DS;             // head dims per wave
   constexpr int NU = HW / 16;             // q float4 per lane; O tiles of 16 dims
@@ -628,15 +628,27 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 15, lk = lane >> 4;
   const int g = wave / DS, hf = wave % DS;
-  const int h = blockIdx.y, hq = h * 4 + g;
+  // block j = (sp * n_rt + n_rt - 1 - rt) * n_kv + h: key split sp of row
+  // tile rt and kv head h.  Splits in order, the row tiles with the most keys
+  // first, the heads interleaved: the heavy blocks start first and the
+  // round-robin of blocks over the XCDs spreads every kind of block.
+  const int maxs = keep(fs.maxs), stt = keep(fs.st_tiles), n_rt = keep(fs.n_rt);
+  const int j = blockIdx.x;
+  const int h = j % p.n_kv, rt = n_rt - 1 - (j / p.n_kv) % n_rt, sp = j / (p.n_kv * n_rt);
+  const int hq = h * 4 + g;
   const int d0 = hf * HW;  // first head dim of this wave
-  const int r0 = blockIdx.x * 16;
+  const int r0 = rt * 16;
   const int base = aldg<int32_t>(p.pos);
   const int rlast = min(r0 + 15, p.T - 1);
   int klo, khi, dummy;
   key_range(p, base + r0, &klo, &dummy);
   key_range(p, base + rlast, &dummy, &khi);
   const int kbeg = klo & ~15;
+  // the last split takes every remaining tile
+  const int nsplit = maxs == 1 ? 1 : min(maxs, ((khi - kbeg) / 16 + stt) / stt);
+  if (sp >= nsplit) return;
+  const int kfirst = kbeg + sp * stt * 16;
+  const int klast = sp == nsplit - 1 ? khi : kbeg + (sp + 1) * stt * 16 - 1;
 
   // q rows of this wave (A operand, head dims in MFMA order)
   af32x4 q[NU];
@@ -701,11 +713,11 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
   }
   float *Pw = Ps + wave * 16 * PP;
 
-  tile_load(kbeg);
+  tile_load(kfirst);
   tile_store();
   __syncthreads();
-  for (int k0 = kbeg; k0 <= khi; k0 += 16) {
-    const bool more = k0 + 16 <= khi;
+  for (int k0 = kfirst; k0 <= klast; k0 += 16) {
+    const bool more = k0 + 16 <= klast;
     if (more) tile_load(k0 + 16);
     // scores over this wave's dims: row 4lk + e, key k0 + li
     af32x4 sc = af32x4{0.f, 0.f, 0.f, 0.f};
@@ -762,16 +774,138 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
     if (more) tile_store();
     __syncthreads();
   }
+  if (nsplit == 1) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int row = r0 + 4 * lk + e;
-    if (row >= p.T) continue;
-    const float inv = 1.0f / l[e];
-    float *op = p.out + (size_t)row * p.q_dim + hq * HD + d0 + li;
+    for (int e = 0; e < 4; ++e) {
+      const int row = r0 + 4 * lk + e;
+      if (row >= p.T) continue;
+      const float inv = 1.0f / l[e];
+      float *op = p.out + (size_t)row * p.q_dim + hq * HD + d0 + li;
 #pragma unroll
-    for (int u = 0; u < NU; ++u) op[16 * u] = o[u][e] * inv;
+      for (int u = 0; u < NU; ++u) op[16 * u] = o[u][e] * inv;
+    }
+  } else {
+    // partial of this split: o (unnormalized), max and sum per (row, head)
+    float *pb = keep(fs.part) + (size_t)j * 64 * (HD + 2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rl = 4 * lk + e;
+      float *po = pb + (rl * 4 + g) * HD + d0 + li;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) po[16 * u] = o[u][e];
+      if (li == 0 && hf == 0) {
+        float *pm = pb + 64 * HD + (rl * 4 + g) * 2;
+        pm[0] = m[e];
+        pm[1] = l[e];
+      }
+    }
   }
 }
+
+// Row tiles whose key tiles were split over several blocks: log-sum-exp merge
+// of the splits' partials.  One block per (row tile, kv head, query head of
+// the group); the splits' weights exp(m_s - M) / L of the 16 rows go through
+// LDS, then every thread sums float4 of o over the splits.
+constexpr int kFlashMaxSplits = 32;
+constexpr int kFlashMaxBlocks = 512;  // blocks of a split launch (two per CU)
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_flash_merge(AttnArgs args, FlashSplit fs) {
+  __shared__ float wsh[kFlashMaxSplits][16];
+  const AttnP p = load_params(args);
+  const int maxs = keep(fs.maxs), stt = keep(fs.st_tiles), n_rt = keep(fs.n_rt);
+  const int rt = blockIdx.x, h = blockIdx.y >> 2, g = blockIdx.y & 3;
+  const int r0 = rt * 16;
+  const int base = aldg<int32_t>(p.pos);
+  const int rlast = min(r0 + 15, p.T - 1);
+  int klo, khi, dummy;
+  key_range(p, base + r0, &klo, &dummy);
+  key_range(p, base + rlast, &dummy, &khi);
+  const int kbeg = klo & ~15;
+  const int nsplit = min(maxs, ((khi - kbeg) / 16 + stt) / stt);
+  if (nsplit <= 1) return;
+  // record of split s: block (s * n_rt + n_rt - 1 - rt) * n_kv + h
+  const float *pb = keep(fs.part) + ((size_t)(n_rt - 1 - rt) * p.n_kv + h) * 64 * (HD + 2);
+  const size_t sstride = (size_t)n_rt * p.n_kv * 64 * (HD + 2);
+  const int tid = threadIdx.x;
+  if (tid < 16) {
+    const float *pm = pb + 64 * HD + (tid * 4 + g) * 2;
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < nsplit; ++s2) M = fmaxf(M, pm[s2 * sstride]);
+    float L = 0.f;
+    for (int s2 = 0; s2 < nsplit; ++s2) {
+      const float ms2 = pm[s2 * sstride];
+      const float w = ms2 == -INFINITY ? 0.f : expf(ms2 - M);
+      wsh[s2][tid] = w;
+      L += pm[s2 * sstride + 1] * w;
+    }
+    // rows past T have no keys (L = 0); they are not stored
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    for (int s2 = 0; s2 < nsplit; ++s2) wsh[s2][tid] *= inv;
+  }
+  __syncthreads();
+  constexpr int N4 = 16 * HD / 4;
+#pragma unroll 4
+  for (int e = tid; e < N4; e += 256) {
+    const int rl = e / (HD / 4), d = 4 * (e % (HD / 4));
+    const int row = r0 + rl;
+    const float *po = pb + (rl * 4 + g) * HD + d;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s2 = 0; s2 < nsplit; ++s2) {
+      const float w = wsh[s2][rl];
+      const float4 v = *reinterpret_cast<const float4 *>(po + s2 * sstride);
+      acc.x += w * v.x;
+      acc.y += w * v.y;
+      acc.z += w * v.z;
+      acc.w += w * v.w;
+    }
+    if (row < p.T) {
+      float *op = p.out + (size_t)row * p.q_dim + (h * 4 + g) * HD + d;
+      op[0] = acc.x;
+      op[1] = acc.y;
+      op[2] = acc.z;
+      op[3] = acc.w;
+    }
+  }
+}
+
+// Split plan of a prefill launch.  Row tile rt (rows at positions
+// plan_pos + 16 rt ...) attends to about min(plan_pos / 16 + rt + 2, bound)
+// key tiles, bound = cache_len / 16 + 2.  Splits of st tiles, st = the launch's
+// tiles / 256 CUs (at least 8), so that the blocks make about one round of
+// the chip; no split unless the longest row tile is a third longer than st.
+// At most kFlashMaxBlocks blocks and kFlashMaxSplits splits per row tile (the
+// last split of a row tile takes every tile left).
+static FlashSplit flash_split_plan(const AttnArgs &a) {
+  FlashSplit fs{};
+  fs.n_rt = (a.T + 15) / 16;
+  fs.maxs = 1;
+  fs.st_tiles = 1 << 30;
+  const long bound = (a.cache_len + 15) / 16 + 1;
+  const long p0 = std::max(0, a.plan_pos);
+  auto tiles = [&](long rt) { return std::min((p0 + rt * 16 + 15) / 16 + 1, bound); };
+  long tot = 0;
+  for (long rt = 0; rt < fs.n_rt; ++rt) tot += tiles(rt);
+  tot *= a.n_kv;
+  const long maxw = tiles(fs.n_rt - 1);
+  long st = std::max(8L, (tot + 255) / 256);
+  if (st * 4 > maxw * 3) return fs;
+  long maxs = std::min<long>((maxw + st - 1) / st, kFlashMaxSplits);
+  maxs = std::min<long>(maxs, kFlashMaxBlocks / ((long)fs.n_rt * a.n_kv));
+  if (maxs <= 1) return fs;
+  st = std::max(st, (maxw + maxs - 1) / maxs);
+  fs.maxs = (int)maxs;
+  fs.st_tiles = (int)st;
+  return fs;
+}
+
+size_t flash_part_floats(const AttnArgs &a) {
+  const FlashSplit fs = flash_split_plan(a);
+  if (fs.maxs <= 1) return 0;
+  return (size_t)a.n_kv * fs.n_rt * fs.maxs * 64 * (a.hd + 2);
+}
+
+size_t flash_part_floats_max(int hd) { return (size_t)kFlashMaxBlocks * 64 * (hd + 2); }
 
 // write_kv_sliding / write_kv_full (gemma4_e4b.mojo:211-249) for the rows
 __global__ __launch_bounds__(256) void k_cache_append(AttnArgs args, const float *kr) {
@@ -794,18 +928,25 @@ bool prefill_flash_ok(const AttnArgs &a) {
          (a.hd == 128 || a.hd == 256 || a.hd == 512);
 }
 
-int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, hipStream_t st) {
+int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, float *fpart,
+                             size_t fpart_floats, hipStream_t st) {
   if (int rc = attn_check(a)) return rc;
   MS_CHECK_ARG(prefill_flash_ok(a), "prefill attention: needs B = 1, 4 query heads per kv "
                                     "head and head_dim 128, 256 or 512");
   MS_CHECK_ARG(a.qkv && a.pos && a.out && a.kc && a.vc && qr && kr,
                "prefill attention: missing buffers");
+  FlashSplit fs = flash_split_plan(a);
+  const size_t need = flash_part_floats(a);
+  if (need == 0 || !fpart || fpart_floats < need) fs.maxs = 1;  // no split
+  fs.part = fpart;
   hipLaunchKernelGGL(k_rope_rows, dim3(a.T), dim3(256), 0, st, a, qr, kr, a.hd);
-  const dim3 grid((a.T + 15) / 16, a.n_kv);
+  const dim3 grid(fs.maxs * fs.n_rt * a.n_kv);
 #define MS_FLASH(HDV, DSV)                                                                \
   hipLaunchKernelGGL((k_flash_prefill<HDV, DSV>), grid, dim3(256 * DSV),                   \
                      (flash_lds_floats<HDV, DSV>() * 4), st, a, (const float *)qr,         \
-                     (const float *)kr)
+                     (const float *)kr, fs);                                               \
+  if (fs.maxs > 1)                                                                         \
+  hipLaunchKernelGGL(k_flash_merge<HDV>, dim3(fs.n_rt, a.n_kv * 4), dim3(256), 0, st, a, fs)
   switch (a.hd) {
     case 128: MS_FLASH(128, 1); break;
     case 256: MS_FLASH(256, 2); break;

@@ -196,13 +196,15 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.vc = d_vcache;
   a.cache_seq_stride = 0;
   a.out = d_out;
+  a.plan_pos = base;
   if (int rc = attn_check(a)) return rc;
   const int G = a.n_heads / a.n_kv;
   // many rows: the flash-attention prefill path (needs no chunk partials, but
   // buffers for the rows' q and k)
   const bool flash = T > kGemvMaxM && prefill_flash_ok(a);
   const size_t qkv_f = (size_t)T * ld;
-  const size_t part_f = flash ? (size_t)T * (L->q_dim + L->kv_dim)
+  const size_t fsplit_f = flash ? flash_part_floats(a) : 0;
+  const size_t part_f = flash ? (size_t)T * (L->q_dim + L->kv_dim) + fsplit_f
                               : attn_part_floats(1, a.n_kv, a.n_chunks, T, G, a.hd);
   const size_t need = (qkv_f + part_f) * 4 + 64 + (size_t)a.n_kv * 4;
   void *buf = nullptr;
@@ -224,7 +226,10 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.pos = dpos;
   a.ctr = ctr;
   if (flash) {
-    if (int rc = launch_attention_prefill(a, part, part + (size_t)T * L->q_dim, st)) return rc;
+    float *fsplit = part + (size_t)T * (L->q_dim + L->kv_dim);
+    if (int rc = launch_attention_prefill(a, part, part + (size_t)T * L->q_dim,
+                                          fsplit_f ? fsplit : nullptr, fsplit_f, st))
+      return rc;
   } else if (int rc = launch_attention(a, st)) {
     return rc;
   }

@@ -108,6 +108,8 @@ struct ms_model {
   int prefill_rows = 0;
   int32_t *ppos = nullptr;
   float *fq = nullptr, *fk = nullptr;  // prefill rows' q and k after RoPE
+  float *fpart = nullptr;              // flash attention's key-split partials
+  size_t fpart_floats = 0;
   int32_t *pos = nullptr, *tok = nullptr, *ids_hist = nullptr, *step = nullptr;
   int hist_cap = 1024;
   float *arg_val = nullptr;
@@ -202,6 +204,8 @@ struct RunCfg {
   float *hidden;            // optional [n_layers][B*T][D]
   int first_layer, n_layers;
   int seq0;                 // first sequence (caches / positions offset)
+  int plan_pos;             // first row's position as the host knows it (B = 1);
+                            // sizes the prefill attention's key split only
 };
 
 // Launch a projection of rows r: quantized in the kernel's prologue with
@@ -313,11 +317,13 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.ctr = m->attn_ctr;
     a.out = m->aO;
     a.write_cache = 1;
+    a.plan_pos = rc.plan_pos;
     // KV bytes read at the current position are counted by bench.py
     ProfScope ps(PC_ATTN, 0.0, st);
     if (rc.B == 1 && rc.T > kGemvMaxM && m->fq && prefill_flash_ok(a)) {
       // prefill rows: flash attention on fp32 MFMA
-      if (int rc2 = launch_attention_prefill(a, m->fq, m->fk, st)) return rc2;
+      if (int rc2 = launch_attention_prefill(a, m->fq, m->fk, m->fpart, m->fpart_floats, st))
+        return rc2;
     } else if (rc.T <= kPrefillAttnRows || rc.B != 1) {
       if (int rc2 = launch_attention(a, st)) return rc2;
     } else {
@@ -645,6 +651,13 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
       ((rc = dmalloc(m, (void **)&m->fq, (size_t)m->prefill_rows * m->q_max * 4)) ||
        (rc = dmalloc(m, (void **)&m->fk, (size_t)m->prefill_rows * m->kv_max * 4))))
     return cleanup(rc);
+  if (m->prefill_rows > kGemvMaxM) {
+    // key-split partials of any flash launch
+    for (auto &Ly : m->L)
+      m->fpart_floats = std::max(m->fpart_floats, flash_part_floats_max(Ly.d.head_dim));
+    if (m->fpart_floats && (rc = dmalloc(m, (void **)&m->fpart, m->fpart_floats * 4)))
+      return cleanup(rc);
+  }
   if ((rc = dmalloc(m, (void **)&m->qkv, (size_t)M * m->qkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_ctr, (size_t)d.max_seqs * m->nkv_max * 4)) ||
@@ -880,6 +893,7 @@ static int forward_impl(ms_model *m, int first, int count, float *d_x, int B, in
   rc.hidden = d_hidden;
   rc.first_layer = first;
   rc.n_layers = count;
+  rc.plan_pos = h_base[0];
   if (int r = run_layers(m, rc, st)) return r;
   if (int r = enqueue_output(m, rc, st)) return r;
   MS_HIP_TRY(hipStreamSynchronize(st));
@@ -1024,6 +1038,7 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
     rc.seq0 = seq;
     rc.first_layer = 0;
     rc.n_layers = (int)m->L.size();
+    rc.plan_pos = base;
     if ((rcode = run_layers(m, rc, st))) break;
     if (c0 + t >= n_tokens) {
       // LM head on the last prompt row only
