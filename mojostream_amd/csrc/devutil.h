@@ -21,6 +21,13 @@ __device__ inline float4 ldg<float4>(const void *p) {
   return float4{v.x, v.y, v.z, v.w};
 }
 
+// Streaming load (non-temporal hint): data read once, which should not
+// displace reused data from the caches.
+template <class T>
+__device__ inline T ldg_nt(const void *p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) T *)p);
+}
+
 // A uniform value passed through an opaque register move: the compiler can no
 // longer turn selects between such values back into an indexed memory access
 // (which would put them in scratch memory or re-read the argument struct).

@@ -562,7 +562,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
       for (int p = 0; p < P; ++p) {
         q[u][p] = uint4{0u, 0u, 0u, 0u};
         if (Gu < KG) {
-          const u32x4 v = ldg<u32x4>(wl[p] + (size_t)Gu * 1024 + lane * 16);
+          const u32x4 v = ldg_nt<u32x4>(wl[p] + (size_t)Gu * 1024 + lane * 16);
           q[u][p] = uint4{v.x, v.y, v.z, v.w};
         }
       }
