@@ -251,9 +251,244 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   }
 }
 
+// ------------------------------------------------------------------------------
+// Big-tile variant for GEMMs with many blocks.  A block computes kGBM = 64
+// activation rows (256 limb rows) by kGPan = 16 panels (SwiGLU: 8 gate and
+// the 8 up panels of the same 128 columns).  Eight waves; wave (wr, wc) owns
+// limb rows 64wr..64wr+63 (4 A tiles) and panel slots 8wc..8wc+7: 32
+// accumulators.  Both operands of a K step (A 32 KiB, B 16 KiB) go from
+// global memory straight into LDS (global_load_lds_dwordx4: each wave
+// instruction fills 1 KiB, lane l the 16 bytes at l * 16), in a ring of three
+// steps, so the weights cross the L2 once per block rather than once per wave
+// row, and a K step does 64 MFMAs per wave against 16 KiB of LDS reads.  A limb rows
+// are stored without padding, the 16-byte chunk c of row r at chunk position
+// c ^ ((r >> 1) & 7): the 16 rows one A fragment read touches then fall in
+// 16 different bank groups.
+// ------------------------------------------------------------------------------
+constexpr int kGBM = 64;                     // activation rows per block
+constexpr int kGPan = 16;                    // panel slots per block
+constexpr int kGStageA = 4 * kGBM * 128;     // limb rows x 128 bytes
+constexpr int kGStageB = kGPan * 1024;       // one super-tile per panel
+constexpr int kGStage = kGStageA + kGStageB;
+constexpr int kGStages = 3;
+constexpr int kGLds = kGStages * kGStage;    // 144 KiB
+constexpr int kGNT = 512;                    // threads per block
+constexpr int kGLoads = 6;                   // direct loads per thread per K step
+constexpr int kGemmBigMinBlocks = 512;
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
+
+template <int EPI>
+__global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int M = launder(g.M), K = launder(g.K);
+  const int8_t *limbs = launder(g.a.limbs);
+  const int32_t *shift = launder(g.a.shift);
+  const int64_t *xsum = launder(g.a.xsum);
+  const uint8_t *sw0 = launder(g.seg[0].w), *sw1 = launder(g.seg[1].w),
+                *sw2 = launder(g.seg[2].w);
+  const float ss0 = launder(g.seg[0].scale), ss1 = launder(g.seg[1].scale),
+              ss2 = launder(g.seg[2].scale);
+  const int nseg = launder(g.nseg);
+  const int sn0 = launder(g.seg[0].n_cols) >> 4;
+  const int sn1 = nseg > 1 ? launder(g.seg[1].n_cols) >> 4 : 0;
+  const int sn2 = nseg > 2 ? launder(g.seg[2].n_cols) >> 4 : 0;
+  const int sc0 = launder(g.seg[0].out_col0), sc1 = launder(g.seg[1].out_col0),
+            sc2 = launder(g.seg[2].out_col0);
+  float *out = launder(g.out);
+  const int ldo = launder(g.ldo);
+  const float *resid = EPI == EPI_RESID ? launder(g.resid) : nullptr;
+  float *out2 = EPI == EPI_RESID ? launder(g.out2) : nullptr;
+  float *sw_out = EPI == EPI_SWIGLU ? launder(g.sw_out) : nullptr;
+  const int ldo_sw = EPI == EPI_SWIGLU ? launder(g.ldo_sw) : 0;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int wr = wave & 3, wc = wave >> 2;
+  const int r0 = blockIdx.y * kGBM;
+  const int KG = K >> 7;
+
+  // panel slot -> weights, scale, first column, valid (block-uniform selects)
+  auto slot = [&](int sl, const uint8_t **w, float *sc, int *col, bool *ok) {
+    if constexpr (EPI == EPI_SWIGLU) {
+      const int half = sl >> 3, cp = blockIdx.x * 8 + (sl & 7);
+      *ok = cp < sn0;
+      *w = (half == 0 ? sw0 : sw1) + (size_t)(*ok ? cp : 0) * K * 8;
+      *sc = half == 0 ? ss0 : ss1;
+      *col = cp * 16;
+    } else {
+      const int pi = blockIdx.x * kGPan + sl;
+      const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
+      const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
+      *ok = pi < sn0 + sn1 + sn2;
+      const uint8_t *base = si == 0 ? sw0 : (si == 1 ? sw1 : sw2);
+      *w = *ok ? base + (size_t)loc * K * 8 : sw0;
+      *sc = si == 0 ? ss0 : (si == 1 ? ss1 : ss2);
+      *col = (si == 0 ? sc0 : (si == 1 ? sc1 : sc2)) + loc * 16;
+    }
+  };
+  // this wave loads panel slots 2 wave, 2 wave + 1 (an invalid slot loads a
+  // valid panel: every wave issues the same number of loads per step)
+  const uint8_t *lw[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float sc;
+    int col;
+    bool ok;
+    slot(2 * wave + j, &lw[j], &sc, &col, &ok);
+  }
+  // A: this wave fills LDS blocks 4 wave + i (limb rows 8q .. 8q + 7); lane l
+  // writes row 8q + l / 8 at chunk position l % 8, which holds chunk
+  // (l % 8) ^ ((row >> 1) & 7) of the row
+  const int8_t *abase = limbs + (size_t)(4 * r0) * K;
+  const int8_t *asrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * (4 * wave + i) + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    asrc[i] = abase + (size_t)row * K + c * 16;
+  }
+  auto issue = [&](int G, int stg) {
+    uint8_t *sa = lds + stg * kGStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((gbl_void *)(asrc[i] + (size_t)G * 128),
+                                       (lds_void *)(sa + (4 * wave + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_void *)(lw[j] + (size_t)G * 1024 + lane * 16),
+                                       (lds_void *)(sa + kGStageA + (2 * wave + j) * 1024), 16,
+                                       0, 0);
+  };
+
+  v4i acc[4][8];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[a][j] = v4i{0, 0, 0, 0};
+
+  const int li = lane & 15, lg = lane >> 4;
+  const int swz = (li >> 1) & 7;  // (row >> 1) & 7 for every row this lane reads
+  auto compute = [&](int stg) {
+    const uint8_t *sa = lds + stg * kGStage;
+    const uint8_t *sb = sa + kGStageA + (8 * wc) * 1024 + lane * 16;
+    u32x4 braw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) braw[j] = *reinterpret_cast<const u32x4 *>(sb + j * 1024);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i bf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t d0 = braw[j][2 * h], d1 = braw[j][2 * h + 1];
+        bf[j] = v4i{(int)(d0 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu),
+                    (int)(d1 & 0x0F0F0F0Fu), (int)((d1 >> 4) & 0x0F0F0F0Fu)};
+      }
+      const int pos = (2 * lg + h) ^ swz;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const v4i af = *reinterpret_cast<const v4i *>(sa + (64 * wr + 16 * a + li) * 128 +
+                                                      pos * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[a][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[a][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // Ring of kGStages K steps: step G + 2 is issued into the stage step G - 1
+  // used, once every wave has passed the barrier after computing it.
+  issue(0, 0);
+  if (KG > 1) issue(1, 1);
+  for (int G = 0; G < KG; ++G) {
+    // this wave's loads of step G are in LDS (step G + 1's may be in flight)
+    if (G + 1 < KG)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | kGLoads);  // vmcnt(6)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);            // vmcnt(0)
+    __syncthreads();
+    if (G + 2 < KG) issue(G + 2, (G + 2) % kGStages);
+    compute(G % kGStages);
+  }
+
+  // ---- epilogue: lane (column jc, row rr of each A tile), one tile at a time
+  const int jc = lane & 15, rr = lane >> 4;
+  float wsc[8];
+  int col[8];
+  bool pv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint8_t *w;
+    slot(8 * wc + j, &w, &wsc[j], &col[j], &pv[j]);
+  }
+  double rsc[4];
+  long long rz[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int row = r0 + 16 * wr + 4 * a + rr;
+    rsc[a] = row < M ? (double)ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.0;
+    rz[a] = row < M ? 8 * ldg<long long>(xsum + row) : 0;
+  }
+  auto value = [&](int a, int j) {
+    const v4i d = acc[a][j];
+    const long long t = (long long)d[0] + ((long long)d[1] << 8) + ((long long)d[2] << 16) +
+                        ((long long)d[3] << 24) - rz[a];
+    return (float)((double)t * rsc[a] * (double)wsc[j]);
+  };
+  if constexpr (EPI == EPI_SWIGLU) {
+    // gate values of wave (wr, 0) -> LDS -> up wave (wr, 1)
+    __syncthreads();  // every wave is done reading the operand stages
+    float *xg = reinterpret_cast<float *>(lds) + wr * 32 * 64;
+    if (wc == 0) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xg[(a * 8 + j) * 64 + lane] = value(a, j);
+    }
+    __syncthreads();
+    if (wc == 1) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int row = r0 + 16 * wr + 4 * a + rr;
+        if (row >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (!pv[j]) continue;
+          const float gt = xg[(a * 8 + j) * 64 + lane], up = value(a, j);
+          sw_out[(size_t)row * ldo_sw + col[j] + jc] = up * gt * (1.0f / (1.0f + expf(-gt)));
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int row = r0 + 16 * wr + 4 * a + rr;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (!pv[j]) continue;
+        const size_t oi = (size_t)row * ldo + col[j] + jc;
+        const float x = value(a, j);
+        if constexpr (EPI == EPI_STORE) {
+          out[oi] = x;
+        } else if constexpr (EPI == EPI_ACCUMULATE) {
+          out[oi] += x;
+        } else {
+          const float y = resid[oi] + x;
+          out[oi] = y;
+          if (out2) out2[oi] = y;
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
-int gemm_row_pad(int M) { return (M + kBM - 1) / kBM * kBM; }
+// Rows of the quantized operand a GEMM reads: the big tile's row block.
+int gemm_row_pad(int M) { return (M + kGBM - 1) / kGBM * kGBM; }
 
 int launch_gemm(const GemmArgs &g, hipStream_t st) {
   MS_CHECK_ARG(g.M >= 1 && g.K >= 128 && g.K % 128 == 0 && g.K <= kQuantMaxK,
@@ -263,34 +498,44 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
   for (int i = 0; i < g.nseg; ++i)
     MS_CHECK_ARG(g.seg[i].w && g.seg[i].n_cols > 0 && g.seg[i].n_cols % 16 == 0,
                  "GEMM: segment columns must be a positive multiple of 16");
-  const dim3 blk(kNT);
-  const int gy = gemm_row_pad(g.M) / kBM;
-  switch (g.epi) {
-    case EPI_STORE:
-    case EPI_ACCUMULATE:
-    case EPI_RESID: {
-      MS_CHECK_ARG(g.out && g.ldo > 0, "GEMM: output missing");
-      MS_CHECK_ARG(g.epi != EPI_RESID || g.resid, "GEMM: residual missing");
-      int np = 0;
-      for (int i = 0; i < g.nseg; ++i) np += g.seg[i].n_cols / 16;
-      const dim3 grid((np + 4 * kWB - 1) / (4 * kWB), gy);
-      if (g.epi == EPI_STORE)
-        hipLaunchKernelGGL(k_gemm<EPI_STORE>, grid, blk, kGemmLds, st, g);
-      else if (g.epi == EPI_ACCUMULATE)
-        hipLaunchKernelGGL(k_gemm<EPI_ACCUMULATE>, grid, blk, kGemmLds, st, g);
-      else
-        hipLaunchKernelGGL(k_gemm<EPI_RESID>, grid, blk, kGemmLds, st, g);
-      break;
+  if (g.epi == EPI_STORE || g.epi == EPI_ACCUMULATE || g.epi == EPI_RESID) {
+    MS_CHECK_ARG(g.out && g.ldo > 0, "GEMM: output missing");
+    MS_CHECK_ARG(g.epi != EPI_RESID || g.resid, "GEMM: residual missing");
+  } else if (g.epi == EPI_SWIGLU) {
+    MS_CHECK_ARG(g.nseg == 2 && g.seg[0].n_cols == g.seg[1].n_cols && g.sw_out,
+                 "GEMM: SwiGLU needs gate and up of equal width and an output");
+  } else {
+    return fail(MS_E_INVALID, "GEMM: unsupported epilogue");
+  }
+  int np = 0;
+  for (int i = 0; i < g.nseg; ++i) np += g.seg[i].n_cols / 16;
+  const bool swiglu = g.epi == EPI_SWIGLU;
+  // the big tile when it makes at least two rounds of the CUs
+  const int gxb = swiglu ? (np / 2 + 7) / 8 : (np + kGPan - 1) / kGPan;
+  const int gyb = gemm_row_pad(g.M) / kGBM;
+  if ((long)gxb * gyb >= kGemmBigMinBlocks) {
+    const dim3 grid(gxb, gyb);
+#define MS_GB(E) hipLaunchKernelGGL(k_gemm_big<E>, grid, dim3(kGNT), kGLds, st, g)
+    switch (g.epi) {
+      case EPI_STORE: MS_GB(EPI_STORE); break;
+      case EPI_ACCUMULATE: MS_GB(EPI_ACCUMULATE); break;
+      case EPI_RESID: MS_GB(EPI_RESID); break;
+      default: MS_GB(EPI_SWIGLU); break;
     }
-    case EPI_SWIGLU: {
-      MS_CHECK_ARG(g.nseg == 2 && g.seg[0].n_cols == g.seg[1].n_cols && g.sw_out,
-                   "GEMM: SwiGLU needs gate and up of equal width and an output");
-      const dim3 grid((g.seg[0].n_cols / 16 + 2 * kWB - 1) / (2 * kWB), gy);
-      hipLaunchKernelGGL(k_gemm<EPI_SWIGLU>, grid, blk, kGemmLds, st, g);
-      break;
+#undef MS_GB
+  } else {
+    const dim3 blk(kNT);
+    const int gy = (g.M + kBM - 1) / kBM;
+    const dim3 grid(swiglu ? (np / 2 + 2 * kWB - 1) / (2 * kWB) : (np + 4 * kWB - 1) / (4 * kWB),
+                    gy);
+#define MS_GS(E) hipLaunchKernelGGL(k_gemm<E>, grid, blk, kGemmLds, st, g)
+    switch (g.epi) {
+      case EPI_STORE: MS_GS(EPI_STORE); break;
+      case EPI_ACCUMULATE: MS_GS(EPI_ACCUMULATE); break;
+      case EPI_RESID: MS_GS(EPI_RESID); break;
+      default: MS_GS(EPI_SWIGLU); break;
     }
-    default:
-      return fail(MS_E_INVALID, "GEMM: unsupported epilogue");
+#undef MS_GS
   }
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;

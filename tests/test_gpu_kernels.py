@@ -58,7 +58,9 @@ MATMUL_SHAPES = [(M, K, K) for M in (1, 4, 64) for K in (1024, 4096)] + [
     (4, 4096, 2560), (1, 2560, 4096), (2, 2560, 1024), (16, 2560, 512), (9, 1024, 1024),
     (1, 5120, 1024), (1, 13824, 5120),
     # M > 16: quantize once, MFMA GEMM (prefill shapes)
-    (17, 2560, 3072), (100, 2560, 1024), (333, 1024, 512), (200, 10240, 256)]
+    (17, 2560, 3072), (100, 2560, 1024), (333, 1024, 512), (200, 10240, 256),
+    # enough blocks for the big-tile GEMM; M and N ragged against its tile
+    (600, 1024, 16432)]
 
 
 @pytest.mark.parametrize("M,K,N", MATMUL_SHAPES)
@@ -80,7 +82,8 @@ def test_q4_matmul_vs_f64(gpu, oracle, M, K, N):
         assert rel_max(oracle.matmul(A, q4, N, 0.1), ref) < 1e-5
 
 
-@pytest.mark.parametrize("M,K,N", [(48, 2560, 512), (70, 1024, 160), (256, 4096, 128)])
+@pytest.mark.parametrize("M,K,N", [(48, 2560, 512), (70, 1024, 160), (256, 4096, 128),
+                                   (600, 1024, 16432)])
 def test_q4_gemm_rows_equal_gemv_rows(gpu, M, K, N):
     """The GEMM (M > 16) and the GEMV (row chunks of <= 16) use the same exact
     integer operands and the same scaling, so every row must agree bit for bit."""
@@ -118,6 +121,17 @@ def test_q4_matmul_accumulates(gpu, oracle):
     assert rel_max(dC.download(np.float32, (M, N)), ref) < 1e-5
     # many rows (GEMM path) accumulate the same way
     M = 40
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    C0 = RNG.standard_normal((M, N)).astype(np.float32)
+    dA = ms.DeviceBuffer.from_array(A)
+    dC = ms.DeviceBuffer.from_array(C0)
+    ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pk.ptr, M, K, N, 0.1, 1))
+    ref = C0 + oracle.matmul_f64(A, q4, N, 0.1)
+    assert rel_max(dC.download(np.float32, (M, N)), ref) < 1e-5
+    # and the big-tile GEMM (enough blocks, ragged M and N)
+    M, N = 600, 16432
+    q4 = ms.host_random_u8(K * N // 2, 5, 5).reshape(K, N // 2)
+    _, d_pk = packed(ms, q4, K, N)
     A = RNG.standard_normal((M, K)).astype(np.float32)
     C0 = RNG.standard_normal((M, N)).astype(np.float32)
     dA = ms.DeviceBuffer.from_array(A)
