@@ -367,15 +367,16 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
   }
 }
 
-template <bool GAM>
-__global__ __launch_bounds__(1024) void k_quant_rows(RowSrc r, int K, QuantRows q) {
+// One row per block of NT threads (K <= 16 NT).
+template <bool GAM, int NT>
+__global__ __launch_bounds__(NT) void k_quant_rows(RowSrc r, int K, QuantRows q) {
   __shared__ __align__(8) float sh[32];  // also 16 doubles (row sum)
-  RowRegs<1024, 2, GAM> R;
+  RowRegs<NT, 2, GAM> R;
   const int m = blockIdx.x;
-  row_load<1024, 2, GAM>(r, K, m, R);
+  row_load<NT, 2, GAM>(r, K, m, R);
   int s;
   double xs;
-  row_finish<1024, 2, GAM, true>(r, K, m, true, R, q.limbs, K, sh, &s, &xs);
+  row_finish<NT, 2, GAM, true>(r, K, m, true, R, q.limbs, K, sh, &s, &xs);
   if (threadIdx.x == 0) {
     q.shift[m] = s;
     q.xsum[m] = (int64_t)xs;
@@ -401,10 +402,18 @@ int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStre
   MS_CHECK_ARG(M >= 1 && K >= 8 && K % 8 == 0 && K <= kQuantMaxK,
                "quant: row length must be a multiple of 8 in [8, 16384]");
   MS_CHECK_ARG(r.x && r.ld >= K && q.limbs && q.shift && q.xsum, "quant: missing buffers");
-  if (r.gamma)
-    hipLaunchKernelGGL(k_quant_rows<true>, dim3(M), dim3(1024), 0, st, r, K, q);
-  else
-    hipLaunchKernelGGL(k_quant_rows<false>, dim3(M), dim3(1024), 0, st, r, K, q);
+  // many rows of up to 4096 values on 256 threads: more rows per CU, shorter
+  // reductions (a few decode rows keep the 1024 threads per row)
+  if (K <= 16 * 256 && M >= 64) {
+    if (r.gamma)
+      hipLaunchKernelGGL((k_quant_rows<true, 256>), dim3(M), dim3(256), 0, st, r, K, q);
+    else
+      hipLaunchKernelGGL((k_quant_rows<false, 256>), dim3(M), dim3(256), 0, st, r, K, q);
+  } else if (r.gamma) {
+    hipLaunchKernelGGL((k_quant_rows<true, 1024>), dim3(M), dim3(1024), 0, st, r, K, q);
+  } else {
+    hipLaunchKernelGGL((k_quant_rows<false, 1024>), dim3(M), dim3(1024), 0, st, r, K, q);
+  }
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }
