@@ -151,6 +151,15 @@ int ms_attention(const ms_layer_desc *desc, const float *d_q,
  * index of the strict maximum).  d_logits may be NULL. */
 int ms_lm_head_argmax(const float *d_x, int M, int D, const uint8_t *d_packed,
                       int vocab, float scale, float *d_logits, int32_t *d_ids);
+/* temperature_sampling (lm_head.mojo:198-254) on a logits row in device
+ * memory, with `seed` where the reference reads the clock (:246): the
+ * repetition penalty over the n_generated ids of d_generated (prompt and
+ * generated tokens, as gemma4_e4b_infer.mojo:157-182 passes them; at most
+ * 8192), greedy below temperature 0.01, else softmax at `temperature` and one
+ * LCG draw.  Like the reference it leaves the penalized logits (greedy) or the
+ * probabilities in d_logits.  The id goes to *h_id. */
+int ms_sample(float *d_logits, int vocab, float temperature, const int32_t *d_generated,
+              int n_generated, float penalty, uint64_t seed, int32_t *h_id);
 /* get_token_embedding Q4 branch (lm_head.mojo:186-195): column `token` of the
  * tied head, dequantized, for each of n tokens -> d_out [n][D]. */
 int ms_embed_q4(const uint8_t *d_packed, int D, int vocab, float scale,

@@ -100,6 +100,7 @@ _SIGS = {
     "ms_rope": [_P, _I, _I, _I, _I, _I, _F, _I],
     "ms_attention": [C.POINTER(LayerDesc), _P, _P, _P, _P, _P, _I, _I, _P],
     "ms_lm_head_argmax": [_P, _I, _I, _P, _I, _F, _P, _P],
+    "ms_sample": [_P, _I, _F, _P, _I, _F, _U64, _P],
     "ms_embed_q4": [_P, _I, _I, _F, _P, _I, _P],
     "ms_model_create": [C.POINTER(ModelDesc), C.POINTER(LayerDesc), C.POINTER(C.c_void_p)],
     "ms_model_destroy": [_P],
@@ -184,6 +185,17 @@ def device_info():
 
 
 # ---- host-side seeded data (identical to the device generator) -------------
+def sample(d_logits: "DeviceBuffer", vocab: int, temperature: float, d_generated,
+           n_generated: int, penalty: float, seed: int) -> int:
+    """temperature_sampling (lm_head.mojo:198-254) on a device logits row, with
+    an explicit seed; the row is modified in place like the reference's."""
+    out = C.c_int32()
+    gp = d_generated.ptr if d_generated is not None else None
+    check(_lib.ms_sample(d_logits.ptr, vocab, float(temperature), gp, n_generated,
+                         float(penalty), int(seed) & 0xFFFFFFFFFFFFFFFF, C.byref(out)))
+    return int(out.value)
+
+
 def host_random_u8(n: int, seed: int, stream: int) -> np.ndarray:
     out = np.empty(n, dtype=np.uint8)
     _lib.ms_host_fill_random_u8(out.ctypes.data, n, seed, stream)

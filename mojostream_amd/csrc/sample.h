@@ -1,0 +1,27 @@
+// Device token sampling (temperature_sampling, lm_head.mojo:198-254).
+#pragma once
+#include "common.h"
+
+namespace ms {
+
+constexpr int kSampleMaxHistory = 8192;  // ids of a row's history the penalty sees
+
+struct SampleArgs {
+  float *logits;          // [rows][ld]; penalized logits or probabilities on return
+  int n, ld;              // vocabulary, row stride
+  float temperature;      // <= 0.01: greedy
+  float penalty;          // > 1: repetition penalty over the history
+  int32_t *hist;          // [rows][hist_ld] token history (prompt + generated)
+  int hist_ld;
+  int32_t *hist_n;        // [rows] history length (device)
+  int hist_cap;           // hist_append: capacity of a row's history
+  int hist_append;        // append the sampled id to the history
+  uint64_t seed;          // draw seed = seed + *step + row
+  const int32_t *step;    // device step counter or null
+  int32_t *ids_out;       // [rows] or null
+  int32_t *tok_state;     // [rows] or null: next input token
+};
+
+int launch_sample(const SampleArgs &a, int rows, hipStream_t st);
+
+}  // namespace ms

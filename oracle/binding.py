@@ -58,6 +58,8 @@ _SIGS = {
     "or_layer_forward": ([C.POINTER(OrLayer), _I, _I, _P, _I, _I, _I], None),
     "or_lm_head": ([_P, _I, _I, _P, _I, _F, _P], None),
     "or_argmax": ([_P, _I], C.c_int),
+    "or_sample": ([_P, _I, _F, _P, _I, _F, C.c_uint64], C.c_int),
+    "or_sample_target": ([C.c_uint64], C.c_float),
     "or_embed": ([_P, _I, _I, _F, _I, _P], None),
     "or_decode_token": ([C.POINTER(OrLayer), _I, _I, _I, _P, _I, _F, _P, _I, _I, _P],
                         C.c_int),
@@ -138,6 +140,20 @@ class Oracle:
     def argmax(self, v: np.ndarray) -> int:
         v = np.ascontiguousarray(v, np.float32)
         return int(self.lib.or_argmax(v.ctypes.data, v.size))
+
+    def sample(self, logits: np.ndarray, temperature: float, generated, penalty: float,
+               seed: int):
+        """temperature_sampling (lm_head.mojo:198-254) with an explicit seed.
+        Returns (id, logits after the call: penalized, or probabilities)."""
+        v = np.ascontiguousarray(logits, np.float32).copy()
+        g = np.ascontiguousarray(np.asarray(generated, np.int32).reshape(-1))
+        gp = g.ctypes.data if g.size else None
+        tid = self.lib.or_sample(v.ctypes.data, v.size, temperature, gp, g.size, penalty,
+                                 int(seed) & 0xFFFFFFFFFFFFFFFF)
+        return int(tid), v
+
+    def sample_target(self, seed: int) -> float:
+        return float(self.lib.or_sample_target(int(seed) & 0xFFFFFFFFFFFFFFFF))
 
     def embed(self, wlm: np.ndarray, D: int, vocab: int, scale: float, token: int) -> np.ndarray:
         w = np.ascontiguousarray(wlm, np.uint8)

@@ -375,6 +375,48 @@ int or_argmax(const float *v, int n) {
   return best;
 }
 
+/* lm_head.mojo:247-248: lcg = (seed * 6364136223846793005 +
+ * 1442695040888963407) & 0x7FFFFFFF in wrapping 64-bit arithmetic (the low 31
+ * bits do not depend on signedness), target = Float32(lcg) / Float32(2^31 - 1). */
+float or_sample_target(uint64_t seed) {
+  const uint64_t lcg = (seed * 6364136223846793005ull + 1442695040888963407ull) & 0x7FFFFFFFull;
+  return (float)lcg / (float)0x7FFFFFFF;
+}
+
+/* temperature_sampling, lm_head.mojo:198-254 */
+int or_sample(float *logits, int n, float temperature, const int32_t *generated,
+              int n_generated, float penalty, uint64_t seed) {
+  if (penalty > 1.0f) {                       /* :211-220 */
+    for (int i = 0; i < n_generated; ++i) {
+      const int tid = generated[i];
+      if (tid >= 0 && tid < n) {
+        const float v = logits[tid];
+        logits[tid] = v > 0.0f ? v / penalty : v * penalty;
+      }
+    }
+  }
+  if (temperature <= 0.01f) return or_argmax(logits, n);  /* :222-228 */
+  const float inv_t = 1.0f / temperature;     /* :230-233 */
+  float max_v = logits[0];
+  for (int j = 1; j < n; ++j)
+    if (logits[j] > max_v) max_v = logits[j];
+  float sum_e = 0.0f;                         /* :235-239 */
+  for (int j = 0; j < n; ++j) {
+    const float e = expf((logits[j] - max_v) * inv_t);
+    logits[j] = e;
+    sum_e += e;
+  }
+  const float inv_s = 1.0f / sum_e;           /* :240-242 */
+  for (int j = 0; j < n; ++j) logits[j] = logits[j] * inv_s;
+  const float target = or_sample_target(seed);  /* :246-248 */
+  float cdf = 0.0f;                           /* :250-254 */
+  for (int j = 0; j < n; ++j) {
+    cdf += logits[j];
+    if (cdf >= target) return j;
+  }
+  return n - 1;
+}
+
 void or_embed(const uint8_t *wlm, int D, int vocab, float scale, int token,
               float *out) {
   const int pc = vocab / 2, bc = token / 2, hi = token & 1;

@@ -33,6 +33,12 @@
  *                          and 5:1, T=1..4 rows.
  *   or_lm_head / argmax    ties resolve to the lowest index; logits against
  *                          or_matmul_q4_f64.
+ *   or_sample              penalty cases with closed forms (positive divided,
+ *                          negative multiplied, repeats applied per
+ *                          occurrence, out-of-range ids ignored); greedy
+ *                          branch equals or_argmax; sampled frequencies over
+ *                          many seeds against the f64 softmax (chi-square);
+ *                          LCG targets uniform on [0, 1].
  */
 #ifndef MS_ORACLE_H
 #define MS_ORACLE_H
@@ -132,6 +138,19 @@ void or_lm_head(const float *x, int M, int D, const uint8_t *wlm, int vocab,
                 float scale, float *logits);
 /* greedy branch of temperature_sampling, lm_head.mojo:224-230. */
 int or_argmax(const float *v, int n);
+/* temperature_sampling (lm_head.mojo:198-254) with the seed as an argument
+ * where the reference reads the clock (:246).  In list order, each
+ * occurrence of an id of `generated` below n divides a positive logit by
+ * `penalty` or multiplies a non-positive one (:211-220, when penalty > 1).
+ * Temperature <= 0.01: first index of the maximum (:222-228).  Otherwise the
+ * logits become exp((v - max) / T) / sum in place (:230-243), one LCG step
+ * of the seed gives the target (:246-248), and the first index whose running
+ * fp32 sum reaches it is returned, else n - 1 (:250-254).  Modifies logits in
+ * place like the reference. */
+int or_sample(float *logits, int n, float temperature, const int32_t *generated,
+              int n_generated, float penalty, uint64_t seed);
+/* The LCG target of one seed (lm_head.mojo:247-248). */
+float or_sample_target(uint64_t seed);
 /* get_token_embedding Q4 branch, lm_head.mojo:186-195. */
 void or_embed(const uint8_t *wlm, int D, int vocab, float scale, int token,
               float *out);

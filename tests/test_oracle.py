@@ -279,3 +279,50 @@ def test_lm_head_vs_f64(oracle):
     lg = oracle.lm_head(xn, w, V, 0.09)
     ref = lm_logits(x, w, 0.09, g.astype(np.float64))
     assert rel_rmse(lg, ref) < 1e-5
+
+
+# ---- sampler (temperature_sampling, lm_head.mojo:198-254) -----------------------------
+
+def test_sample_penalty_closed_forms(oracle):
+    """Penalty per occurrence: positive divided, non-positive multiplied, ids
+    at or beyond the vocabulary ignored; greedy leaves the penalized logits."""
+    v = np.array([2.0, -1.0, 0.0, 4.0, 3.0], np.float32)
+    tid, out = oracle.sample(v, 0.0, [3, 3, 1, 2, 9, -1], 2.0, 0)
+    np.testing.assert_array_equal(out, np.array([2.0, -2.0, 0.0, 1.0, 3.0], np.float32))
+    assert tid == 4
+    # penalty 1 (or below) leaves the logits alone
+    tid, out = oracle.sample(v, 0.0, [3, 3], 1.0, 0)
+    np.testing.assert_array_equal(out, v)
+    assert tid == 3
+
+
+def test_sample_greedy_is_argmax(oracle):
+    rng = np.random.default_rng(3)
+    for _ in range(20):
+        v = rng.standard_normal(257).astype(np.float32)
+        v[rng.integers(0, 257)] = v.max()  # a tie: the first index wins
+        tid, _ = oracle.sample(v, 0.01, [], 1.0, 11)
+        assert tid == oracle.argmax(v) == int(np.argmax(v))
+
+
+def test_sample_targets_uniform(oracle):
+    t = np.array([oracle.sample_target(s) for s in range(20000)])
+    assert t.min() >= 0.0 and t.max() <= 1.0
+    hist, _ = np.histogram(t, bins=10, range=(0.0, 1.0))
+    assert np.all(np.abs(hist - 2000) < 5 * np.sqrt(2000))
+
+
+def test_sample_frequencies_match_softmax(oracle):
+    """Draw counts over many seeds against the f64 softmax at temperature T
+    (chi-square, 3 degrees of freedom)."""
+    v = np.array([0.5, 1.5, -0.3, 1.0], np.float32)
+    T = 0.7
+    p = np.exp((v.astype(np.float64) - v.max()) / T)
+    p /= p.sum()
+    n = 20000
+    counts = np.bincount([oracle.sample(v, T, [], 1.0, s)[0] for s in range(n)], minlength=4)
+    chi2 = float(np.sum((counts - n * p) ** 2 / (n * p)))
+    assert chi2 < 16.3  # p = 0.001 for 3 degrees of freedom
+    # the probabilities are left in the logits, summing to one
+    _, out = oracle.sample(v, T, [], 1.0, 0)
+    np.testing.assert_allclose(out, p, rtol=1e-6)
