@@ -238,6 +238,15 @@ int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_tokens,
 /* Shapes the model was created with; `layers` (n_layers entries) may be NULL.
  * No reference counterpart (the reference reads its constants directly). */
 int ms_model_get_desc(const ms_model *m, ms_model_desc *desc, ms_layer_desc *layers);
+/* Sampling for ms_prefill and ms_decode_run: temperature_sampling
+ * (lm_head.mojo:198-254) as gemma4_e4b_infer.mojo:134-182 calls it, in place
+ * of the greedy argmax, when temperature > 0.01 or penalty > 1 (else greedy
+ * again).  Each sequence's penalty history holds its prompt ids (from
+ * ms_prefill) and then every sampled id; ms_model_reset empties it.  The
+ * k-th LM head call that draws (counted from this call or ms_model_reset:
+ * the prefill's first token, then every decode step) draws for sequence b
+ * with seed + b + k, where the reference reads the clock.  Needs an LM head. */
+int ms_model_set_sampling(ms_model *m, float temperature, float penalty, uint64_t seed);
 /* BOS embedding row (LMHead.bos_emb, lm_head.mojo:41-58).  When set, the row
  * at position 0 of ms_prefill takes it instead of the embedding of its token
  * (apply_bos_embedding, lm_head.mojo:133-143, used for prompt position 0 by

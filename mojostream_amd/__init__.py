@@ -116,6 +116,7 @@ _SIGS = {
     "ms_model_stream_stats": [_P, C.POINTER(StreamStats)],
     "ms_model_get_desc": [_P, C.POINTER(ModelDesc), C.POINTER(LayerDesc)],
     "ms_model_set_bos": [_P, _P],
+    "ms_model_set_sampling": [_P, _F, _F, _U64],
     "ms_model_set_pinned": [_P, _P],
     "ms_file_open": [C.c_char_p, C.POINTER(C.c_void_p)], "ms_file_close": [_P],
     "ms_file_get_meta": [_P, C.POINTER(FileMeta)],
@@ -449,6 +450,14 @@ class Model:
 
     def reset(self) -> None:
         check(_lib.ms_model_reset(self.h))
+
+    def set_sampling(self, temperature: float, penalty: float = 1.0, seed: int = 0) -> None:
+        """temperature_sampling (lm_head.mojo:198-254) in prefill and decode
+        instead of the greedy argmax when temperature > 0.01 or penalty > 1;
+        the k-th drawing LM head call (prefill's first token, then each decode
+        step) draws for sequence b with seed + b + k."""
+        check(_lib.ms_model_set_sampling(self.h, float(temperature), float(penalty),
+                                         int(seed) & 0xFFFFFFFFFFFFFFFF))
 
     def set_bos(self, bos: Optional[np.ndarray]) -> None:
         """BOS row for prompt position 0 (apply_bos_embedding, lm_head.mojo:133-143)."""

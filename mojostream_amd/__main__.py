@@ -30,6 +30,11 @@ def main(argv=None) -> int:
     e.add_argument("lm_head", nargs="?")
     e.add_argument("--tokens", type=int, default=32)
     e.add_argument("--stream", action="store_true", help="stream weights from pinned host")
+    e.add_argument("--temperature", type=float, default=0.0,
+                   help="sampling temperature (<= 0.01: greedy; the reference runs 0.7)")
+    e.add_argument("--penalty", type=float, default=1.0,
+                   help="repetition penalty (the reference runs 1.2)")
+    e.add_argument("--sample-seed", type=int, default=0, help="seed of the draws")
     g = sub.add_parser("fake-model", help="write a seeded synthetic .mojostream file")
     g.add_argument("out")
     g.add_argument("--e4b", action="store_true", help="E4B shapes (default: demo shapes)")
@@ -52,7 +57,9 @@ def main(argv=None) -> int:
     elif a.cmd == "bench_q4":
         drivers.run_q4_benchmark()
     elif a.cmd == "e4b-infer":
-        drivers.run_e4b_infer(a.file, a.lm_head, n_stream=a.tokens, resident=not a.stream)
+        drivers.run_e4b_infer(a.file, a.lm_head, n_stream=a.tokens, resident=not a.stream,
+                              temperature=a.temperature, penalty=a.penalty,
+                              sample_seed=a.sample_seed)
     elif a.cmd == "fake-model":
         if a.e4b:
             streaming.write_synthetic_e4b(a.out, a.layers or 42, a.seed)

@@ -26,6 +26,7 @@
 #include "attention.h"
 #include "q4.h"
 #include "rope.h"
+#include "sample.h"
 
 namespace ms {
 
@@ -121,6 +122,16 @@ struct ms_model {
   // graph
   hipGraphExec_t gexec = nullptr;
   int g_nseq = 0;
+  // sampling (ms_model_set_sampling): temperature_sampling in place of the
+  // greedy argmax, over a per-sequence history of prompt and generated ids
+  bool sampling = false;
+  float samp_temp = 0.f, samp_pen = 1.f;
+  uint64_t samp_seed = 0;
+  float *logits = nullptr;      // [max_seqs][vocab]
+  int32_t *shist = nullptr;     // [max_seqs][kSampleMaxHistory]
+  int32_t *shist_n = nullptr;   // [max_seqs]
+  int32_t *samp_ids = nullptr;  // [max_seqs]
+  int32_t *samp_ctr = nullptr;  // LM head calls that drew since set_sampling / reset
   // streaming
   uint8_t *slot[2] = {nullptr, nullptr};
   size_t slot_bytes = 0;
@@ -426,7 +437,8 @@ static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const Argm
   a.nseg = 1;
   a.P = 4;
   a.waves = 4;
-  a.out = nullptr;
+  a.out = m->sampling ? m->logits + (size_t)rc.seq0 * m->d.vocab : nullptr;
+  a.ldo = m->d.vocab;
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
   {
@@ -440,6 +452,27 @@ static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const Argm
   f.n_blocks = m->lm_blocks;
   f.M = M;
   ProfScope ps(PC_OTHER, 0.0, st);
+  if (m->sampling) {
+    // temperature_sampling (lm_head.mojo:198-254) on the logits rows of
+    // sequences seq0 ..; the draws appended to their histories
+    SampleArgs s{};
+    s.logits = m->logits + (size_t)rc.seq0 * m->d.vocab;
+    s.n = m->d.vocab;
+    s.ld = m->d.vocab;
+    s.temperature = m->samp_temp;
+    s.penalty = m->samp_pen;
+    s.hist = m->shist + (size_t)rc.seq0 * kSampleMaxHistory;
+    s.hist_ld = kSampleMaxHistory;
+    s.hist_n = m->shist_n + rc.seq0;
+    s.hist_cap = kSampleMaxHistory;
+    s.hist_append = 1;
+    s.seed = m->samp_seed + (uint64_t)rc.seq0;
+    s.step = m->samp_ctr;
+    s.ids_out = m->samp_ids;
+    if (int r2 = launch_sample(s, M, st)) return r2;
+    f.ids_in = m->samp_ids;
+    f.draws = m->samp_ctr;
+  }
   return launch_argmax_fin(f, st);
 }
 
@@ -864,6 +897,37 @@ extern "C" int ms_model_reset(ms_model *m) {
   // launch; clearing them here also recovers from an interrupted one.
   if (int rc = require_init()) return rc;
   MS_HIP_TRY(hipMemset(m->attn_ctr, 0, (size_t)m->d.max_seqs * m->nkv_max * 4));
+  if (m->shist_n) MS_HIP_TRY(hipMemset(m->shist_n, 0, (size_t)m->d.max_seqs * 4));
+  if (m->samp_ctr) MS_HIP_TRY(hipMemset(m->samp_ctr, 0, 4));
+  return MS_OK;
+}
+
+extern "C" int ms_model_set_sampling(ms_model *m, float temperature, float penalty,
+                                     uint64_t seed) {
+  MS_CHECK_ARG(m, "set_sampling: null model");
+  MS_CHECK_ARG(temperature == temperature && penalty == penalty,
+               "set_sampling: temperature and penalty must be numbers");
+  MS_CHECK_ARG(m->lm_w, "set_sampling: the model has no LM head");
+  if (int rc = require_init()) return rc;
+  const bool on = temperature > 0.01f || penalty > 1.0f;
+  if (on && !m->logits) {
+    const size_t S = (size_t)m->d.max_seqs;
+    if (int rc = dmalloc(m, (void **)&m->logits, S * m->d.vocab * 4)) return rc;
+    if (int rc = dmalloc(m, (void **)&m->shist, S * kSampleMaxHistory * 4)) return rc;
+    if (int rc = dmalloc(m, (void **)&m->shist_n, S * 4)) return rc;
+    if (int rc = dmalloc(m, (void **)&m->samp_ids, S * 4)) return rc;
+    if (int rc = dmalloc(m, (void **)&m->samp_ctr, 4)) return rc;
+    MS_HIP_TRY(hipMemset(m->shist_n, 0, S * 4));
+  }
+  if (m->samp_ctr) MS_HIP_TRY(hipMemset(m->samp_ctr, 0, 4));
+  m->sampling = on;
+  m->samp_temp = temperature;
+  m->samp_pen = penalty;
+  m->samp_seed = seed;
+  if (m->gexec) {  // the captured step holds the former choice
+    (void)hipGraphExecDestroy(m->gexec);
+    m->gexec = nullptr;
+  }
   return MS_OK;
 }
 
@@ -1015,6 +1079,15 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
   int32_t *dtok = nullptr;
   MS_HIP_TRY(hipMallocAsync((void **)&dtok, (size_t)n_tokens * 4, st));
   MS_HIP_TRY(hipMemcpyAsync(dtok, h_tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, st));
+  if (m->sampling) {
+    // the prompt ids open the sequence's penalty history
+    // (gemma4_e4b_infer.mojo:134-139,157-161)
+    const int nh = std::min(n_tokens, kSampleMaxHistory);
+    MS_HIP_TRY(hipMemcpyAsync(m->shist + (size_t)seq * kSampleMaxHistory, dtok, (size_t)nh * 4,
+                              hipMemcpyDeviceToDevice, st));
+    MS_HIP_TRY(hipMemcpyAsync(m->shist_n + seq, &nh, 4, hipMemcpyHostToDevice, st));
+    MS_HIP_TRY(hipStreamSynchronize(st));  // nh is a local
+  }
   int rcode = MS_OK;
   std::vector<int32_t> sub;
   for (int c0 = 0; c0 < n_tokens && rcode == MS_OK; c0 += T) {

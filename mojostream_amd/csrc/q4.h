@@ -84,6 +84,8 @@ struct ArgmaxFin {
   int32_t *pos_state;   // [M] or null: incremented
   int32_t *ids_hist;    // [cap][M] or null
   int32_t *step;        // step counter (with ids_hist)
+  const int32_t *ids_in;  // [M] or null: ids already chosen (no reduction)
+  int32_t *draws;         // or null: incremented once per launch (sampler draw counter)
 };
 
 // Prefill GEMM (gemm.hip): the rows of `a` are quantized for

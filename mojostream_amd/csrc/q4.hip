@@ -759,7 +759,13 @@ __global__ __launch_bounds__(1024) void k_argmax_fin(ArgmaxFin f) {
   for (int m = 0; m < f.M; ++m) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int b = threadIdx.x; b < f.n_blocks; b += 1024) {
+    // ids chosen elsewhere (the sampler): only the state updates below
+    const int nb = f.ids_in ? 0 : f.n_blocks;
+    if (f.ids_in && threadIdx.x == 0) {
+      bv = 0.f;
+      bi = f.ids_in[m];
+    }
+    for (int b = threadIdx.x; b < nb; b += 1024) {
       const float v = f.arg_val[(size_t)b * f.M + m];
       const int idx = f.arg_idx[(size_t)b * f.M + m];
       if (v > bv || (v == bv && idx < bi)) {
@@ -791,6 +797,7 @@ __global__ __launch_bounds__(1024) void k_argmax_fin(ArgmaxFin f) {
     __syncthreads();
   }
   if (threadIdx.x == 0 && f.ids_hist) *f.step += 1;
+  if (threadIdx.x == 0 && f.draws) *f.draws += 1;
 }
 
 int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st) {

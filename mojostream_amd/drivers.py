@@ -7,7 +7,8 @@ per-layer CPU loops replaced by calls into the library:
   run_harness          harness.mojo:185-328         (bench; writes bench_result.json)
   run_streaming_bench  stream_runner.mojo:460-562   (stream)
   run_q4_benchmark     benchmark_q4.mojo:121-147    (bench_q4)
-  run_e4b_infer        gemma4_e4b_infer.mojo:57-210 (e4b-infer, greedy branch)
+  run_e4b_infer        gemma4_e4b_infer.mojo:57-210 (e4b-infer; greedy, or
+                       temperature + repetition penalty with a seed)
 
 Inputs are seeded (the reference's fill_random is unseeded, so its runs are
 not repeatable).  Latencies are wall-clock per step, including the copy of
@@ -245,12 +246,18 @@ def run_q4_benchmark(shapes=((4, 1024, 1024), (64, 1024, 1024), (4, 4096, 4096),
 
 def run_e4b_infer(path: Optional[str] = None, lm_head_path: Optional[str] = None,
                   prompt: Sequence[int] = (2, 603, 5012, 575, 4124, 608), n_stream: int = 32,
-                  seed: int = 42, resident: bool = True) -> dict:
-    """E4B inference driver, greedy branch: BOS row + prompt (TTFT), then
-    `n_stream` generated tokens.  Without files it builds the seeded E4B-shaped
-    synthetic model (vocab 262144)."""
+                  seed: int = 42, resident: bool = True, temperature: float = 0.0,
+                  penalty: float = 1.0, sample_seed: int = 0) -> dict:
+    """E4B inference driver: BOS row + prompt (TTFT), then `n_stream`
+    generated tokens, greedy or (temperature > 0.01 or penalty > 1) sampled
+    like the reference's TEMPERATURE / REPETITION_PENALTY run
+    (gemma4_e4b_infer.mojo:38-39,139,179) with `sample_seed` in place of the
+    clock.  Without files it builds the seeded E4B-shaped synthetic model
+    (vocab 262144)."""
     init(0)
-    _banner("Gemma-4 E4B inference (greedy)")
+    sampled = temperature > 0.01 or penalty > 1.0
+    _banner(f"Gemma-4 E4B inference (T={temperature}, penalty={penalty}, seed={sample_seed})"
+            if sampled else "Gemma-4 E4B inference (greedy)")
     t0 = time.perf_counter_ns()
     max_pos = len(prompt) + n_stream + 8
     if path:
@@ -268,6 +275,8 @@ def run_e4b_infer(path: Optional[str] = None, lm_head_path: Optional[str] = None
             model.fill_synthetic(seed)
         else:
             model.fill_synthetic_host(seed)
+    if sampled:
+        model.set_sampling(temperature, penalty, sample_seed)
     init_ms = (time.perf_counter_ns() - t0) / 1e6
     t1 = time.perf_counter_ns()
     first = model.prefill(list(prompt), 0)

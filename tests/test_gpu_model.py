@@ -172,6 +172,53 @@ def test_e4b_small_batch4_vs_single(gpu, fast_oracle):
     m.close()
 
 
+def oracle_sampled(om, oracle, prompt, n_steps, temperature, penalty, seed):
+    """gemma4_e4b_infer.mojo:134-182 with the oracle: the prompt ids open the
+    penalty history, every drawn id joins it, draw k uses seed + k."""
+    hist = list(prompt)
+    h = None
+    for i, t in enumerate(prompt):
+        _, h = om.decode_token(t, i, hidden=True)
+    out = []
+    pos = len(prompt)
+    for k in range(n_steps):
+        if k:
+            _, h = om.decode_token(out[-1], pos, hidden=True)
+            pos += 1
+        tid, _ = oracle.sample(om.logits_for(h[-1]), temperature, hist, penalty, seed + k)
+        out.append(tid)
+        hist.append(tid)
+    return out
+
+
+def test_e4b_small_sampled_decode_vs_oracle(gpu, fast_oracle):
+    """Sampling in prefill and decode (graph and eager) against the oracle's
+    temperature_sampling on its own logits; a low temperature keeps every draw
+    far from the rounding of the cumulative sums."""
+    ms = gpu
+    arch = ms.arch_e4b(max_full_seq=256, n_layers=6, vocab=16384)
+    say("E4B 6 layers, vocab 16384: sampled decode T=0.05, penalty 1.5")
+    om = synthetic_oracle_model(fast_oracle, arch, SEED)
+    prompt = prompt_ids(5, arch.vocab, 30)
+    steps = 12
+    ref = oracle_sampled(om, fast_oracle, prompt, steps, 0.05, 1.5, 1234)
+    for graph in (True, False):
+        m = build(ms, arch, max_seqs=1, max_rows=8, max_pos=256)
+        m.set_sampling(0.05, 1.5, 1234)
+        first = m.prefill(prompt, 0)
+        ids = m.decode([first], [len(prompt)], steps - 1, use_graph=graph)
+        got = [first] + [int(v) for v in ids[:, 0]]
+        print(f"  graph={graph}: {got}")
+        assert got == ref
+        # greedy again after switching sampling off
+        m.reset()
+        m.set_sampling(0.0, 1.0, 0)
+        first = m.prefill(prompt, 0)
+        gids = [first] + [int(v) for v in m.decode([first], [len(prompt)], 3)[:, 0]]
+        assert gids == oracle_greedy(synthetic_oracle_model(fast_oracle, arch, SEED), prompt, 4)
+        m.close()
+
+
 def test_e4b_small_graph_replays_match_eager(gpu, fast_oracle):
     ms = gpu
     arch = ms.arch_e4b(max_full_seq=256, n_layers=6, vocab=16384)
