@@ -160,6 +160,11 @@ int ms_lm_head_argmax(const float *d_x, int M, int D, const uint8_t *d_packed,
  * probabilities in d_logits.  The id goes to *h_id. */
 int ms_sample(float *d_logits, int vocab, float temperature, const int32_t *d_generated,
               int n_generated, float penalty, uint64_t seed, int32_t *h_id);
+/* matmul_fp32_raw (kernels.mojo:616-671): C (+)= A . B with B fp32 row-major
+ * [K][N], A [M][K], M <= 16; N a multiple of 16 (the reference computes whole
+ * 16-column tiles only, :640).  accumulate = 1 keeps the reference's C +=. */
+int ms_matmul_f32(float *d_c, const float *d_a, const float *d_b, int M, int K, int N,
+                  int accumulate);
 /* get_token_embedding Q4 branch (lm_head.mojo:186-195): column `token` of the
  * tied head, dequantized, for each of n tokens -> d_out [n][D]. */
 int ms_embed_q4(const uint8_t *d_packed, int D, int vocab, float scale,
@@ -316,8 +321,18 @@ int ms_file_write_synthetic(const char *path, const ms_file_meta *hdr,
  * every matrix and PLE scale (the load loops of run_harness
  * harness.mojo:80-122 and StreamingRunner stream_runner.mojo:188-270). */
 int ms_model_load_file(ms_model *m, const ms_file *f);
-/* Tied Q4 LM head file, version 1 (load_lm_head lm_head.mojo:61-116): sets
- * the head (gamma = ones) and the BOS row.  The FP32 version 2 is refused. */
+/* FP32 LM head (LMHead version 2, lm_head.mojo:61-116, projected with
+ * matmul_fp32_raw :146-160, embedded by column :179-185): src [hidden][vocab]
+ * fp32 row-major, h_gamma the final-norm weights (NULL = ones).  Replaces the
+ * Q4 head; vocab must be a multiple of 16. */
+int ms_model_set_lm_head_f32(ms_model *m, const float *src, int src_on_device,
+                             const float *h_gamma);
+/* Seeded synthetic version-2 head file: [vocab][scale 1.0][version 2][BOS]
+ * [gamma][weights] (the layout load_lm_head reads, lm_head.mojo:67-104). */
+int ms_lm_head_file_write_synthetic_v2(const char *path, int hidden, int vocab, uint64_t seed);
+/* LM head file (load_lm_head lm_head.mojo:61-116), version 1 (tied Q4) or,
+ * when the file is large enough, version 2 (FP32 + final-norm gamma): sets
+ * the head, its final-norm gamma (ones for version 1) and the BOS row. */
 int ms_model_load_lm_head_file(ms_model *m, const char *path);
 int ms_lm_head_file_write_synthetic(const char *path, int hidden, int vocab,
                                     uint64_t seed);

@@ -131,6 +131,9 @@ _SIGS = {
     "ms_model_load_file": [_P, _P],
     "ms_model_load_lm_head_file": [_P, C.c_char_p],
     "ms_lm_head_file_write_synthetic": [C.c_char_p, _I, _I, _U64],
+    "ms_lm_head_file_write_synthetic_v2": [C.c_char_p, _I, _I, _U64],
+    "ms_matmul_f32": [_P, _P, _P, _I, _I, _I, _I],
+    "ms_model_set_lm_head_f32": [_P, _P, _I, _P],
     "ms_prof_enable": [_I],
     "ms_prof_sweep": [_P, _I, _I, C.POINTER(C.c_double), C.POINTER(C.c_double),
                       C.POINTER(C.c_long)],

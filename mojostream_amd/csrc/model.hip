@@ -26,6 +26,7 @@
 #include "attention.h"
 #include "q4.h"
 #include "rope.h"
+#include "head_f32.h"
 #include "sample.h"
 
 namespace ms {
@@ -88,6 +89,10 @@ struct ms_model {
   int Mmax = 0;
   // LM head
   uint8_t *lm_w = nullptr;
+  // FP32 head (LMHead version 2, lm_head.mojo:61-116): used instead of lm_w
+  float *lm_f32 = nullptr;   // [D][vocab]
+  float *lm_y = nullptr;     // [max_seqs][D] final-normed rows
+  float *lm_part = nullptr;  // projection partial sums
   float lm_scale = 0.f;
   float *gamma = nullptr;
   bool has_lm = false;
@@ -415,6 +420,49 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
 
 // LM head over rows `row0..row0+M-1` of the last layer's output, then the
 // greedy id per row.
+// The draw (sampling) or the first maximum (greedy, temperature 0) of the
+// logits rows of sequences seq0 .. seq0 + M - 1, then the decode-state update.
+static int enqueue_pick(ms_model *m, const RunCfg &rc, int M, ArgmaxFin f, hipStream_t st) {
+  SampleArgs s{};
+  s.logits = m->logits + (size_t)rc.seq0 * m->d.vocab;
+  s.n = m->d.vocab;
+  s.ld = m->d.vocab;
+  s.temperature = m->sampling ? m->samp_temp : 0.f;
+  s.penalty = m->sampling ? m->samp_pen : 1.f;
+  if (m->sampling) {
+    s.hist = m->shist + (size_t)rc.seq0 * kSampleMaxHistory;
+    s.hist_ld = kSampleMaxHistory;
+    s.hist_n = m->shist_n + rc.seq0;
+    s.hist_cap = kSampleMaxHistory;
+    s.hist_append = 1;
+    s.seed = m->samp_seed + (uint64_t)rc.seq0;
+    s.step = m->samp_ctr;
+    f.draws = m->samp_ctr;
+  }
+  s.ids_out = m->samp_ids;
+  if (int r2 = launch_sample(s, M, st)) return r2;
+  f.ids_in = m->samp_ids;
+  return launch_argmax_fin(f, st);
+}
+
+// FP32 head: final norm (y rows), matmul_fp32_raw into the logits, then the pick.
+static int enqueue_lm_f32(ms_model *m, const RunCfg &rc, RowSrc r, int M, const ArgmaxFin &fin,
+                          hipStream_t st) {
+  const int D = m->d.hidden, V = m->d.vocab;
+  r.y_out = m->lm_y;
+  {
+    ProfScope ps(PC_LM, (double)D * V * 4, st);
+    if (int r2 = launch_quant_rows(r, M, D, quant_rows_view(m->quant, M, D), st)) return r2;
+    if (int r2 = launch_mm_f32(m->lm_y, m->lm_f32, m->logits + (size_t)rc.seq0 * V, M, D, V, 0,
+                               m->lm_part, st))
+      return r2;
+  }
+  ArgmaxFin f = fin;
+  f.M = M;
+  ProfScope ps(PC_OTHER, 0.0, st);
+  return enqueue_pick(m, rc, M, f, st);
+}
+
 static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const ArgmaxFin &fin,
                       hipStream_t st) {
   const int D = m->d.hidden;
@@ -427,6 +475,7 @@ static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const Argm
   r.norm = 1;
   r.gamma = m->gamma;
   if (rc.out_rows) r.x_out = rc.out_rows + (size_t)row0 * D;
+  if (m->lm_f32) return enqueue_lm_f32(m, rc, r, M, fin, st);
   GemvArgs a{};
   a.epi = EPI_ARGMAX;
   a.asrc = AS_QUANT;
@@ -452,27 +501,9 @@ static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const Argm
   f.n_blocks = m->lm_blocks;
   f.M = M;
   ProfScope ps(PC_OTHER, 0.0, st);
-  if (m->sampling) {
-    // temperature_sampling (lm_head.mojo:198-254) on the logits rows of
-    // sequences seq0 ..; the draws appended to their histories
-    SampleArgs s{};
-    s.logits = m->logits + (size_t)rc.seq0 * m->d.vocab;
-    s.n = m->d.vocab;
-    s.ld = m->d.vocab;
-    s.temperature = m->samp_temp;
-    s.penalty = m->samp_pen;
-    s.hist = m->shist + (size_t)rc.seq0 * kSampleMaxHistory;
-    s.hist_ld = kSampleMaxHistory;
-    s.hist_n = m->shist_n + rc.seq0;
-    s.hist_cap = kSampleMaxHistory;
-    s.hist_append = 1;
-    s.seed = m->samp_seed + (uint64_t)rc.seq0;
-    s.step = m->samp_ctr;
-    s.ids_out = m->samp_ids;
-    if (int r2 = launch_sample(s, M, st)) return r2;
-    f.ids_in = m->samp_ids;
-    f.draws = m->samp_ctr;
-  }
+  // temperature_sampling (lm_head.mojo:198-254) on the logits rows, the
+  // draws appended to the sequences' histories
+  if (m->sampling) return enqueue_pick(m, rc, M, f, st);
   return launch_argmax_fin(f, st);
 }
 
@@ -888,6 +919,47 @@ extern "C" int ms_model_set_lm_head(ms_model *m, const uint8_t *src, int src_on_
   return MS_OK;
 }
 
+// Buffers of the logits-based pick (sampler, FP32 head), once per model.
+static int alloc_pick(ms_model *m) {
+  const size_t S = (size_t)m->d.max_seqs;
+  if (!m->logits)
+    if (int rc = dmalloc(m, (void **)&m->logits, S * m->d.vocab * 4)) return rc;
+  if (!m->samp_ids)
+    if (int rc = dmalloc(m, (void **)&m->samp_ids, S * 4)) return rc;
+  return MS_OK;
+}
+
+extern "C" int ms_model_set_lm_head_f32(ms_model *m, const float *src, int src_on_device,
+                                        const float *h_gamma) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && src, "set_lm_head_f32: null argument");
+  MS_CHECK_ARG(m->d.vocab > 0 && m->d.vocab % 16 == 0,
+               "set_lm_head_f32: model vocab must be a positive multiple of 16");
+  const size_t D = (size_t)m->d.hidden, V = (size_t)m->d.vocab, S = (size_t)m->d.max_seqs;
+  hipStream_t st = ctx().stream;
+  if (!m->lm_f32) {
+    if (int rc = dmalloc(m, (void **)&m->lm_f32, D * V * 4)) return rc;
+    if (int rc = dmalloc(m, (void **)&m->lm_y, S * D * 4)) return rc;
+    if (int rc = dmalloc(m, (void **)&m->lm_part, mm_f32_part_floats((int)S, (int)V) * 4))
+      return rc;
+  }
+  if (int rc = alloc_pick(m)) return rc;
+  MS_HIP_TRY(hipMemcpyAsync(m->lm_f32, src, D * V * 4,
+                            src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+  if (h_gamma) {
+    if (!m->gamma)
+      if (int r = dmalloc(m, (void **)&m->gamma, D * 4)) return r;
+    MS_HIP_TRY(hipMemcpyAsync(m->gamma, h_gamma, D * 4, hipMemcpyHostToDevice, st));
+  }
+  MS_HIP_TRY(hipStreamSynchronize(st));
+  m->has_lm = true;
+  if (m->gexec) {
+    (void)hipGraphExecDestroy(m->gexec);
+    m->gexec = nullptr;
+  }
+  return MS_OK;
+}
+
 extern "C" int ms_model_reset(ms_model *m) {
   MS_CHECK_ARG(m, "reset: null model");
   std::fill(m->h_pos.begin(), m->h_pos.end(), 0);
@@ -907,15 +979,14 @@ extern "C" int ms_model_set_sampling(ms_model *m, float temperature, float penal
   MS_CHECK_ARG(m, "set_sampling: null model");
   MS_CHECK_ARG(temperature == temperature && penalty == penalty,
                "set_sampling: temperature and penalty must be numbers");
-  MS_CHECK_ARG(m->lm_w, "set_sampling: the model has no LM head");
+  MS_CHECK_ARG(m->has_lm, "set_sampling: the model has no LM head");
   if (int rc = require_init()) return rc;
   const bool on = temperature > 0.01f || penalty > 1.0f;
-  if (on && !m->logits) {
+  if (on && !m->shist) {
     const size_t S = (size_t)m->d.max_seqs;
-    if (int rc = dmalloc(m, (void **)&m->logits, S * m->d.vocab * 4)) return rc;
+    if (int rc = alloc_pick(m)) return rc;
     if (int rc = dmalloc(m, (void **)&m->shist, S * kSampleMaxHistory * 4)) return rc;
     if (int rc = dmalloc(m, (void **)&m->shist_n, S * 4)) return rc;
-    if (int rc = dmalloc(m, (void **)&m->samp_ids, S * 4)) return rc;
     if (int rc = dmalloc(m, (void **)&m->samp_ctr, 4)) return rc;
     MS_HIP_TRY(hipMemset(m->shist_n, 0, S * 4));
   }
@@ -982,8 +1053,10 @@ static int enqueue_decode_step(ms_model *m, int B, hipStream_t st) {
   const int D = m->d.hidden;
   {
     ProfScope ps(PC_PREP, (double)D * B / 2, st);
-    if (int rc = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, m->tok, B, m->x_in, st))
-      return rc;
+    const int rc = m->lm_f32
+                       ? launch_embed_f32(m->lm_f32, D, m->d.vocab, m->tok, B, m->x_in, st)
+                       : launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, m->tok, B, m->x_in, st);
+    if (rc) return rc;
   }
   RunCfg rc{};
   rc.B = B;
@@ -1100,7 +1173,9 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
     for (int r0 = 0; r0 < t; r0 += kPrefillAttnRows) sub.push_back(base + r0);
     MS_HIP_TRY(hipMemcpyAsync(m->ppos, sub.data(), sub.size() * 4, hipMemcpyHostToDevice, st));
     MS_HIP_TRY(hipStreamSynchronize(st));  // `sub` is reused by the next chunk
-    if ((rcode = launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, dtok + c0, t, m->x_in, st)))
+    if ((rcode = m->lm_f32 ? launch_embed_f32(m->lm_f32, D, m->d.vocab, dtok + c0, t, m->x_in, st)
+                           : launch_embed(m->lm_w, D, m->d.vocab, m->lm_scale, dtok + c0, t,
+                                          m->x_in, st)))
       break;
     if (m->bos && base == 0)
       MS_HIP_TRY(hipMemcpyAsync(m->x_in, m->bos, (size_t)D * 4, hipMemcpyDeviceToDevice, st));

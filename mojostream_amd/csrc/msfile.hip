@@ -88,7 +88,7 @@ void expected(const ms_file_meta &m, const ms_file_layer &ld, int type, uint32_t
 // PLE U(0.8,1.2) on stream 0x91E (create_fake_model.py:95,203).
 uint64_t matrix_stream(int layer, int type) { return (uint64_t)(layer + 1) * 16 + (type - 1); }
 constexpr uint64_t kScaleStream = 0x5CA1E, kPleStream = 0x91E, kLmStream = 0xFFFF,
-                   kBosStream = 0xB05;
+                   kBosStream = 0xB05, kGammaStream = 0x6A44A;
 
 int io_fail(const std::string &msg) { return fail(MS_E_IO, msg); }
 
@@ -483,11 +483,22 @@ extern "C" int ms_model_load_lm_head_file(ms_model *model, const char *path) {
   const uint32_t vocab = rd<uint32_t>(raw.data());
   const float scale = rd<float>(raw.data() + 4);
   const size_t D = (size_t)d.hidden;
-  const size_t v2_size = 12 + D * 4 * 2 + D * (size_t)vocab * 4;
-  if (raw.size() >= v2_size) return io_fail("lm_head: FP32 head (version 2) is not supported");
   if (vocab != (uint32_t)d.vocab)
     return io_fail("lm_head: vocab " + std::to_string(vocab) + " != model vocab " +
                    std::to_string(d.vocab));
+  // version 2 when the file holds [version][BOS fp32][gamma fp32][weights fp32]
+  // after vocab and scale (the size test of lm_head.mojo:74-76)
+  const size_t v2_size = 12 + D * 4 * 2 + D * (size_t)vocab * 4;
+  if (raw.size() >= v2_size) {
+    const uint8_t *p = raw.data() + 12;
+    std::vector<float> bos(D), gamma(D);
+    memcpy(bos.data(), p, D * 4);
+    memcpy(gamma.data(), p + D * 4, D * 4);
+    if (int rc = ms_model_set_lm_head_f32(model, reinterpret_cast<const float *>(p + D * 8), 0,
+                                          gamma.data()))
+      return rc;
+    return ms_model_set_bos(model, bos.data());
+  }
   const size_t need = 8 + D * 4 + D * (size_t)vocab / 2;
   if (raw.size() < need)
     return io_fail("lm_head: file has " + std::to_string(raw.size()) + " bytes, version 1 needs " +
@@ -496,6 +507,28 @@ extern "C" int ms_model_load_lm_head_file(ms_model *model, const char *path) {
   memcpy(bos.data(), raw.data() + 8, D * 4);
   if (int rc = ms_model_set_lm_head(model, raw.data() + 8 + D * 4, 0, scale, nullptr)) return rc;
   return ms_model_set_bos(model, bos.data());
+}
+
+extern "C" int ms_lm_head_file_write_synthetic_v2(const char *path, int hidden, int vocab,
+                                                  uint64_t seed) {
+  MS_CHECK_ARG(path && hidden > 0 && vocab > 0, "lm_head_file_write_synthetic_v2: bad arguments");
+  const size_t D = (size_t)hidden, nw = D * (size_t)vocab;
+  std::vector<uint8_t> raw(12 + D * 8 + nw * 4);
+  wr<uint32_t>(raw.data(), (uint32_t)vocab);
+  wr<float>(raw.data() + 4, 1.0f);
+  wr<uint32_t>(raw.data() + 8, 2u);
+  float *bos = reinterpret_cast<float *>(raw.data() + 12);
+  float *gamma = bos + D, *w = gamma + D;
+  ms_host_fill_normal(bos, D, seed, kBosStream);
+  ms_host_fill_normal(gamma, D, seed, kGammaStream);
+  for (size_t i = 0; i < D; ++i) gamma[i] = 1.0f + 0.1f * gamma[i];
+  ms_host_fill_normal(w, nw, seed, kLmStream);
+  for (size_t i = 0; i < nw; ++i) w[i] *= 0.05f;
+  FILE *fp = fopen(path, "wb");
+  if (!fp) return io_fail(std::string("lm_head: cannot create ") + path);
+  bool ok = fwrite(raw.data(), 1, raw.size(), fp) == raw.size();
+  ok = (fclose(fp) == 0) && ok;
+  return ok ? MS_OK : io_fail(std::string("lm_head: write failed for ") + path);
 }
 
 extern "C" int ms_lm_head_file_write_synthetic(const char *path, int hidden, int vocab,

@@ -60,6 +60,7 @@ _SIGS = {
     "or_argmax": ([_P, _I], C.c_int),
     "or_sample": ([_P, _I, _F, _P, _I, _F, C.c_uint64], C.c_int),
     "or_sample_target": ([C.c_uint64], C.c_float),
+    "or_matmul_f32": ([_P, _P, _P, _I, _I, _I], None),
     "or_embed": ([_P, _I, _I, _F, _I, _P], None),
     "or_decode_token": ([C.POINTER(OrLayer), _I, _I, _I, _P, _I, _F, _P, _I, _I, _P],
                         C.c_int),
@@ -151,6 +152,16 @@ class Oracle:
         tid = self.lib.or_sample(v.ctypes.data, v.size, temperature, gp, g.size, penalty,
                                  int(seed) & 0xFFFFFFFFFFFFFFFF)
         return int(tid), v
+
+    def matmul_f32(self, A: np.ndarray, B: np.ndarray, C0: Optional[np.ndarray] = None):
+        """matmul_fp32_raw (kernels.mojo:616-671): C0 + A . B (C0 zeros if None)."""
+        A = np.ascontiguousarray(A, np.float32)
+        B = np.ascontiguousarray(B, np.float32)
+        M, K = A.shape
+        N = B.shape[1]
+        out = np.zeros((M, N), np.float32) if C0 is None else np.array(C0, np.float32, copy=True)
+        self.lib.or_matmul_f32(out.ctypes.data, A.ctypes.data, B.ctypes.data, M, K, N)
+        return out
 
     def sample_target(self, seed: int) -> float:
         return float(self.lib.or_sample_target(int(seed) & 0xFFFFFFFFFFFFFFFF))

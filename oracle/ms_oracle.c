@@ -417,6 +417,20 @@ int or_sample(float *logits, int n, float temperature, const int32_t *generated,
   return n - 1;
 }
 
+/* matmul_fp32_raw, kernels.mojo:616-671 (BK = 128, NR = 16, :636-668) */
+void or_matmul_f32(float *C, const float *A, const float *B, int M, int K, int N) {
+  for (int kt = 0; kt < K; kt += 128) {
+    const int k1 = kt + 128 < K ? kt + 128 : K;
+    for (int nt = 0; nt + 16 <= N; nt += 16)
+      for (int m = 0; m < M; ++m)
+        for (int j = 0; j < 16; ++j) {
+          float acc = 0.0f;
+          for (int k = kt; k < k1; ++k) acc = acc + A[(size_t)m * K + k] * B[(size_t)k * N + nt + j];
+          C[(size_t)m * N + nt + j] = C[(size_t)m * N + nt + j] + acc;
+        }
+  }
+}
+
 void or_embed(const uint8_t *wlm, int D, int vocab, float scale, int token,
               float *out) {
   const int pc = vocab / 2, bc = token / 2, hi = token & 1;

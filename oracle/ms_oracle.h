@@ -33,6 +33,8 @@
  *                          and 5:1, T=1..4 rows.
  *   or_lm_head / argmax    ties resolve to the lowest index; logits against
  *                          or_matmul_q4_f64.
+ *   or_matmul_f32          against an f64 product; the columns of a partial
+ *                          last 16-column tile stay untouched; C += A . B.
  *   or_sample              penalty cases with closed forms (positive divided,
  *                          negative multiplied, repeats applied per
  *                          occurrence, out-of-range ids ignored); greedy
@@ -151,6 +153,11 @@ int or_sample(float *logits, int n, float temperature, const int32_t *generated,
               int n_generated, float penalty, uint64_t seed);
 /* The LCG target of one seed (lm_head.mojo:247-248). */
 float or_sample_target(uint64_t seed);
+/* matmul_fp32_raw (kernels.mojo:616-671): C += A . B, B fp32 row-major [K][N];
+ * per 128 rows of K, per whole 16-column tile (:640; a partial last tile is
+ * left untouched), per row: the products of the tile's rows added in k order,
+ * then added to C. */
+void or_matmul_f32(float *C, const float *A, const float *B, int M, int K, int N);
 /* get_token_embedding Q4 branch, lm_head.mojo:186-195. */
 void or_embed(const uint8_t *wlm, int D, int vocab, float scale, int token,
               float *out);

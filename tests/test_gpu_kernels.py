@@ -340,3 +340,29 @@ def test_sample_rejects_bad_arguments(gpu):
     dl = ms.DeviceBuffer.from_array(np.zeros(16, np.float32))
     out = C.c_int32()
     assert ms.lib().ms_sample(dl.ptr, 16, 0.7, None, 9000, 1.2, 0, C.byref(out)) != 0
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_matmul_f32_vs_f64(gpu, oracle, M):
+    """matmul_fp32_raw (kernels.mojo:616-671) for the FP32 LM head: within 1e-5
+    of the f64 product; accumulate keeps C +=; a width that is not whole
+    16-column tiles is refused."""
+    ms = gpu
+    K, N = 2560, 16384
+    say(f"matmul_f32 M={M} K={K} N={N}")
+    rng = np.random.default_rng(M)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    dA, dB = ms.DeviceBuffer.from_array(A), ms.DeviceBuffer.from_array(B)
+    dC = ms.DeviceBuffer.from_array(C0)
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    ms.check(ms.lib().ms_matmul_f32(dC.ptr, dA.ptr, dB.ptr, M, K, N, 0))
+    assert rel_max(dC.download(np.float32, (M, N)), ref) < 1e-5
+    dC.upload(C0)
+    ms.check(ms.lib().ms_matmul_f32(dC.ptr, dA.ptr, dB.ptr, M, K, N, 1))
+    assert rel_max(dC.download(np.float32, (M, N)), C0 + ref) < 1e-5
+    if M == 1:
+        o = oracle.matmul_f32(A, B)
+        assert rel_max(o, ref) < 1e-5
+        assert ms.lib().ms_matmul_f32(dC.ptr, dA.ptr, dB.ptr, M, K, N - 8, 0) != 0

@@ -219,6 +219,45 @@ def test_e4b_small_sampled_decode_vs_oracle(gpu, fast_oracle):
         m.close()
 
 
+def test_e4b_small_fp32_head_file_greedy(gpu, fast_oracle, tmp_path):
+    """LM head file version 2 (FP32 weights + final-norm gamma + BOS,
+    load_lm_head lm_head.mojo:61-116): column embeddings, the final norm with
+    gamma, matmul_fp32_raw logits and the greedy pick, against the oracle's
+    layers with the same head."""
+    ms = gpu
+    arch = ms.arch_e4b(max_full_seq=256, n_layers=6, vocab=16384)
+    say("E4B 6 layers, FP32 head file (version 2), greedy")
+    path = str(tmp_path / "lm_head_v2.bin")
+    ms.check(ms.lib().ms_lm_head_file_write_synthetic_v2(os.fsencode(path), arch.hidden,
+                                                          arch.vocab, 77))
+    raw = np.fromfile(path, np.uint8)
+    D, V = arch.hidden, arch.vocab
+    f = raw[12:].view(np.float32)
+    bos, gamma, W = f[:D], f[D:2 * D], f[2 * D:].reshape(D, V)
+    m = build(ms, arch, max_seqs=1, max_rows=8, max_pos=256)
+    m.load_lm_head_file(path)
+    prompt = prompt_ids(5, V, 40)
+    steps = 6
+    first = m.prefill(prompt, 0)
+    got = [first] + [int(v) for v in m.decode([first], [len(prompt)], steps - 1)[:, 0]]
+    om = synthetic_oracle_model(fast_oracle, arch, SEED, with_lm=False)
+
+    def pick(x_last):
+        y = fast_oracle.rmsnorm(x_last.reshape(1, -1), gamma)
+        return fast_oracle.argmax(fast_oracle.matmul_f32(y, W)[0])
+
+    x = np.ascontiguousarray(W[:, prompt].T)
+    x[0] = bos  # prompt position 0 takes the BOS row
+    ref = [pick(om.forward(x, 0)[-1])]
+    pos = len(prompt)
+    for _ in range(steps - 1):
+        ref.append(pick(om.forward(np.ascontiguousarray(W[:, [ref[-1]]].T), pos)[-1]))
+        pos += 1
+    print(f"  device {got}\n  oracle {ref}")
+    assert got == ref
+    m.close()
+
+
 def test_e4b_small_graph_replays_match_eager(gpu, fast_oracle):
     ms = gpu
     arch = ms.arch_e4b(max_full_seq=256, n_layers=6, vocab=16384)

@@ -326,3 +326,21 @@ def test_sample_frequencies_match_softmax(oracle):
     # the probabilities are left in the logits, summing to one
     _, out = oracle.sample(v, T, [], 1.0, 0)
     np.testing.assert_allclose(out, p, rtol=1e-6)
+
+
+# ---- FP32 head projection (matmul_fp32_raw, kernels.mojo:616-671) -------------------
+
+def test_matmul_f32_vs_f64_and_tail(oracle):
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((4, 300)).astype(np.float32)
+    B = rng.standard_normal((300, 40)).astype(np.float32)
+    C0 = rng.standard_normal((4, 40)).astype(np.float32)
+    out = oracle.matmul_f32(A, B, C0)
+    ref = C0.astype(np.float64) + A.astype(np.float64) @ B.astype(np.float64)
+    # whole 16-column tiles: C0 + A.B; the partial last tile (columns 32..39) untouched
+    np.testing.assert_allclose(out[:, :32], ref[:, :32], rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(out[:, 32:], C0[:, 32:])
+    # one-hot rows of A select rows of B exactly
+    E = np.zeros((3, 300), np.float32)
+    E[0, 7] = E[1, 150] = E[2, 299] = 1.0
+    np.testing.assert_array_equal(oracle.matmul_f32(E, B)[:, :32], B[[7, 150, 299], :32])
