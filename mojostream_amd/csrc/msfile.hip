@@ -463,9 +463,10 @@ extern "C" int ms_model_load_file(ms_model *model, const ms_file *f) {
   return MS_OK;
 }
 
-// Tied Q4 LM head file, version 1 (load_lm_head, lm_head.mojo:61-116):
-// u32 vocab, f32 scale, hidden fp32 BOS embedding, hidden*vocab/2 Q4 bytes.
-// A file large enough to be the FP32 version 2 is refused.
+// LM head file (load_lm_head, lm_head.mojo:61-116), after u32 vocab and f32 scale:
+//   version 1 (tied Q4)  hidden fp32 BOS embedding, hidden*vocab/2 Q4 bytes;
+//   version 2 (FP32)     u32 version, BOS, final-norm gamma, [hidden][vocab] fp32.
+// A file at least as large as version 2 needs is read as version 2.
 extern "C" int ms_model_load_lm_head_file(ms_model *model, const char *path) {
   MS_CHECK_ARG(model && path, "load_lm_head_file: null argument");
   ms_model_desc d;

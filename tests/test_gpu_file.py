@@ -110,7 +110,7 @@ def test_streaming_pinned_equals_resident(gpu, tmp_path):
 def test_loader_errors(gpu, tmp_path):
     ms = gpu
     from mojostream_amd import streaming as st
-    say("loader errors: shape mismatch, LM head vocab / version / size, pin after bind")
+    say("loader errors: shape mismatch, LM head vocab / size, v2 by size, pin after bind")
     p, lm = hybrid_files(tmp_path, 2048)
     with st.MojoStreamFile(p) as f:
         arch = f.arch(max_len=64, vocab=4096)
@@ -126,8 +126,8 @@ def test_loader_errors(gpu, tmp_path):
         with open(v2, "wb") as g:
             g.write(struct.pack("<IfI", 4096, 0.0, 2))
             g.write(b"\0" * (512 * 4 * 2 + 512 * 4096 * 4))
-        with pytest.raises(ms.MSError, match="version 2"):
-            m.load_lm_head_file(v2)
+        # the version is told by the size alone, as lm_head.mojo:74-76 does
+        m.load_lm_head_file(v2)
         short = str(tmp_path / "short.bin")
         with open(short, "wb") as g:
             g.write(struct.pack("<If", 4096, 0.1) + b"\0" * 1000)
