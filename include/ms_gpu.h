@@ -165,6 +165,14 @@ int ms_sample(float *d_logits, int vocab, float temperature, const int32_t *d_ge
  * 16-column tiles only, :640).  accumulate = 1 keeps the reference's C +=. */
 int ms_matmul_f32(float *d_c, const float *d_a, const float *d_b, int M, int K, int N,
                   int accumulate);
+/* quantize_q4_blockwise (scripts/convert.py:296-323) of a HuggingFace weight
+ * d_w [n_out][n_in] (dtype 0 fp32, 1 bf16, 2 fp16), transposed as the converter
+ * does (convert.py:503-518): d_packed receives the (n_in, n_out) Q4 bytes
+ * [n_in][n_out/2], even columns in the low nibble; *h_scale the global scale
+ * (the largest block scale over blocks of block_size).  n_out must be even; a
+ * weight holding NaN or infinity is refused. */
+int ms_q4_quantize(uint8_t *d_packed, float *h_scale, const void *d_w, int dtype, int n_out,
+                   int n_in, int block_size);
 /* get_token_embedding Q4 branch (lm_head.mojo:186-195): column `token` of the
  * tied head, dequantized, for each of n tokens -> d_out [n][D]. */
 int ms_embed_q4(const uint8_t *d_packed, int D, int vocab, float scale,

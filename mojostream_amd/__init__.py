@@ -133,6 +133,7 @@ _SIGS = {
     "ms_lm_head_file_write_synthetic": [C.c_char_p, _I, _I, _U64],
     "ms_lm_head_file_write_synthetic_v2": [C.c_char_p, _I, _I, _U64],
     "ms_matmul_f32": [_P, _P, _P, _I, _I, _I, _I],
+    "ms_q4_quantize": [_P, _P, _P, _I, _I, _I, _I],
     "ms_model_set_lm_head_f32": [_P, _P, _I, _P],
     "ms_prof_enable": [_I],
     "ms_prof_sweep": [_P, _I, _I, C.POINTER(C.c_double), C.POINTER(C.c_double),
@@ -189,6 +190,20 @@ def device_info():
 
 
 # ---- host-side seeded data (identical to the device generator) -------------
+Q4_DTYPES = {"F32": 0, "BF16": 1, "F16": 2}
+
+
+def q4_quantize(d_w: "DeviceBuffer", dtype: int, n_out: int, n_in: int,
+                block_size: int = 32):
+    """quantize_q4_blockwise (scripts/convert.py:296-323) of a device weight
+    [n_out][n_in] (HuggingFace layout) after the converter's transpose: returns
+    (device buffer of [n_in][n_out/2] Q4 bytes, global scale)."""
+    out = DeviceBuffer(n_in * (n_out // 2))
+    s = C.c_float()
+    check(_lib.ms_q4_quantize(out.ptr, C.byref(s), d_w.ptr, int(dtype), n_out, n_in, block_size))
+    return out, float(s.value)
+
+
 def sample(d_logits: "DeviceBuffer", vocab: int, temperature: float, d_generated,
            n_generated: int, penalty: float, seed: int) -> int:
     """temperature_sampling (lm_head.mojo:198-254) on a device logits row, with

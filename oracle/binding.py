@@ -61,6 +61,7 @@ _SIGS = {
     "or_sample": ([_P, _I, _F, _P, _I, _F, C.c_uint64], C.c_int),
     "or_sample_target": ([C.c_uint64], C.c_float),
     "or_matmul_f32": ([_P, _P, _P, _I, _I, _I], None),
+    "or_q4_quantize": ([_P, _I, _I, _I, _P, _P], None),
     "or_embed": ([_P, _I, _I, _F, _I, _P], None),
     "or_decode_token": ([C.POINTER(OrLayer), _I, _I, _I, _P, _I, _F, _P, _I, _I, _P],
                         C.c_int),
@@ -162,6 +163,17 @@ class Oracle:
         out = np.zeros((M, N), np.float32) if C0 is None else np.array(C0, np.float32, copy=True)
         self.lib.or_matmul_f32(out.ctypes.data, A.ctypes.data, B.ctypes.data, M, K, N)
         return out
+
+    def q4_quantize(self, w_hf: np.ndarray, block_size: int = 32):
+        """quantize_q4_blockwise of w_hf.T (scripts/convert.py:296-323, 503-506):
+        returns (packed [n_in][n_out/2] uint8, scale)."""
+        w = np.ascontiguousarray(w_hf, np.float32)
+        n_out, n_in = w.shape
+        packed = np.empty((n_in, n_out // 2), np.uint8)
+        s = np.zeros(1, np.float32)
+        self.lib.or_q4_quantize(w.ctypes.data, n_out, n_in, block_size, packed.ctypes.data,
+                                s.ctypes.data)
+        return packed, float(s[0])
 
     def sample_target(self, seed: int) -> float:
         return float(self.lib.or_sample_target(int(seed) & 0xFFFFFFFFFFFFFFFF))

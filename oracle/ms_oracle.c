@@ -458,3 +458,43 @@ int or_decode_token(const or_layer *layers, int n_layers, int D, int F,
   free(logits);
   return id;
 }
+
+/* scripts/convert.py:296-323 on the transposed (n_in, n_out) matrix
+ * (convert.py:503-506): block scales over the flat array, in double as Python
+ * computes them (:310-314), their maximum (:316), then float32 division by the
+ * float32 scale, round half to even, clip to [-8, 7], +8, and even columns in
+ * the low nibble (:318-323). */
+void or_q4_quantize(const float *w_hf, int n_out, int n_in, int block_size, uint8_t *packed,
+                    float *scale) {
+  const size_t total = (size_t)n_out * n_in;
+  double gs = 0.0;
+  int any = 0;
+  for (size_t b0 = 0; b0 < total; b0 += (size_t)block_size) {
+    const size_t b1 = b0 + (size_t)block_size < total ? b0 + (size_t)block_size : total;
+    float m = 0.0f;
+    for (size_t i = b0; i < b1; ++i) {
+      const size_t k = i / (size_t)n_out, o = i % (size_t)n_out;
+      const float a = fabsf(w_hf[o * (size_t)n_in + k]);
+      if (a > m) m = a;
+    }
+    const double bs = (double)m > 1e-8 ? (double)m / 7.0 : 1e-8;
+    if (!any || bs > gs) gs = bs;
+    any = 1;
+  }
+  if (!any) gs = 1e-8;
+  const float s = (float)gs;
+  const size_t half = (size_t)n_out / 2;
+  for (int k = 0; k < n_in; ++k)
+    for (size_t j = 0; j < half; ++j) {
+      uint8_t byte = 0;
+      for (int h = 0; h < 2; ++h) {
+        const float x = w_hf[(2 * j + h) * (size_t)n_in + k];
+        float q = nearbyintf(x / s);
+        if (q < -8.0f) q = -8.0f;
+        if (q > 7.0f) q = 7.0f;
+        byte |= (uint8_t)(((int)q + 8) & 0x0F) << (4 * h);
+      }
+      packed[(size_t)k * half + j] = byte;
+    }
+  *scale = s;
+}

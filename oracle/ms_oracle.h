@@ -41,6 +41,12 @@
  *                          branch equals or_argmax; sampled frequencies over
  *                          many seeds against the f64 softmax (chi-square);
  *                          LCG targets uniform on [0, 1].
+ *   or_q4_quantize         weights on the exact grid q * 2^-e come back as q
+ *                          with scale 2^-e; random weights round-trip through
+ *                          or_dequant_q4 within half a scale step, with scale
+ *                          float(max|w| / 7); the tiny-block rule (scale 1e-8)
+ *                          with and without a tiny block; the transposed
+ *                          packing order checked against or_dequant_q4.
  */
 #ifndef MS_ORACLE_H
 #define MS_ORACLE_H
@@ -158,6 +164,11 @@ float or_sample_target(uint64_t seed);
  * left untouched), per row: the products of the tile's rows added in k order,
  * then added to C. */
 void or_matmul_f32(float *C, const float *A, const float *B, int M, int K, int N);
+/* quantize_q4_blockwise (scripts/convert.py:296-323) after the converter's
+ * transpose (convert.py:503-506): w_hf [n_out][n_in] fp32 in, packed
+ * [n_in][n_out/2] and the global scale out. */
+void or_q4_quantize(const float *w_hf, int n_out, int n_in, int block_size, uint8_t *packed,
+                    float *scale);
 /* get_token_embedding Q4 branch, lm_head.mojo:186-195. */
 void or_embed(const uint8_t *wlm, int D, int vocab, float scale, int token,
               float *out);

@@ -344,3 +344,54 @@ def test_matmul_f32_vs_f64_and_tail(oracle):
     E = np.zeros((3, 300), np.float32)
     E[0, 7] = E[1, 150] = E[2, 299] = 1.0
     np.testing.assert_array_equal(oracle.matmul_f32(E, B)[:, :32], B[[7, 150, 299], :32])
+
+
+# ---- converter quantization (quantize_q4_blockwise, scripts/convert.py:296-323) ----
+
+def test_q4_quantize_exact_grid_and_ties(oracle):
+    """Weights q * 2^-5 with max |q| = 7 have scale 2^-5 and come back as q,
+    transposed, even output columns in the low nibble.  Halves round to even."""
+    rng = np.random.default_rng(11)
+    n_out, n_in = 34, 5
+    q = rng.integers(-7, 8, size=(n_out, n_in))
+    q[3, 2] = 7
+    w = (q * 2.0 ** -5).astype(np.float32)
+    packed, s = oracle.q4_quantize(w)
+    assert s == 2.0 ** -5
+    qt = q.T + 8
+    assert np.array_equal(packed, (qt[:, 0::2] | (qt[:, 1::2] << 4)).astype(np.uint8))
+    # ties: 2.5 -> 2, 3.5 -> 4, -2.5 -> -2, -0.5 -> -0
+    w2 = np.zeros((4, 1), np.float32)
+    w2[:, 0] = np.array([2.5, 3.5, -2.5, 7.0]) * 2.0 ** -5
+    p2, s2 = oracle.q4_quantize(w2)
+    assert s2 == 2.0 ** -5
+    assert list(p2[0]) == [(2 + 8) | ((4 + 8) << 4), (-2 + 8) | ((7 + 8) << 4)]
+
+
+def test_q4_quantize_round_trip_through_dequant(oracle):
+    """Random weights: scale float(max|w| / 7) and the pinned dequant returns
+    every transposed weight to within half a scale step."""
+    rng = np.random.default_rng(12)
+    for n_out, n_in in ((64, 48), (130, 7), (2, 1)):
+        w = (0.02 * rng.standard_normal((n_out, n_in))).astype(np.float32)
+        packed, s = oracle.q4_quantize(w)
+        assert s == np.float32(float(np.abs(w).max()) / 7.0)
+        back = oracle.dequant(packed, n_in, n_out, s)
+        err = np.abs(back.astype(np.float64) - w.T.astype(np.float64))
+        assert err.max() <= 0.5 * s * (1 + 1e-6)
+        assert np.all(np.abs(back) <= 8 * s)
+
+
+def test_q4_quantize_tiny_block_rule(oracle):
+    """A block whose max is not above 1e-8 contributes a scale of 1e-8
+    (convert.py:311-314); it wins only when max|w| / 7 is below that."""
+    w = np.zeros((64, 2), np.float32)
+    w[5, 0] = 3e-8                       # column k=0 (first 64 flat values) holds it
+    _, s = oracle.q4_quantize(w, 32)
+    assert s == np.float32(1e-8)         # blocks of k=1 are all zero
+    w[:, :] = 2e-8                        # every block above 1e-8
+    w[5, 0] = 3e-8
+    _, s = oracle.q4_quantize(w, 32)
+    assert s == np.float32(float(np.float32(3e-8)) / 7.0)
+    _, s = oracle.q4_quantize(np.zeros((4, 4), np.float32))
+    assert s == np.float32(1e-8)
