@@ -16,6 +16,7 @@
 //               thread written along the (in, out) rows.  HBM-bound: the
 //               weight once (2 or 4 B per element) plus half a byte written.
 #include "common.h"
+#include "devutil.h"
 
 #include <hip/hip_fp16.h>
 
@@ -36,19 +37,49 @@ __device__ inline float load_w(const void *w, int dtype, size_t i) {
   return __half2float(__ushort_as_half(h));
 }
 
-__global__ __launch_bounds__(256) void k_absmax_part(const void *w, int dtype, size_t n,
+// The 16-byte word v as 4 (fp32) or 8 (bf16, fp16) values.
+template <int DT>
+__device__ inline void unpack16(const u32x4 v, float *o) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (DT == 0) {
+      o[i] = __uint_as_float(u[i]);
+    } else if constexpr (DT == 1) {
+      o[2 * i] = __uint_as_float(u[i] << 16);
+      o[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+    } else {
+      o[2 * i] = __half2float(__ushort_as_half((uint16_t)(u[i] & 0xFFFFu)));
+      o[2 * i + 1] = __half2float(__ushort_as_half((uint16_t)(u[i] >> 16)));
+    }
+  }
+}
+
+// nvec 16-byte words first (the host passes 0 for an unaligned base), then the
+// remaining elements one by one.
+template <int DT>
+__global__ __launch_bounds__(256) void k_absmax_part(const void *w, size_t n, size_t nvec,
                                                      float *part) {
+  constexpr int PER = DT == 0 ? 4 : 8;
   __shared__ float sm[256];
   __shared__ int sb[256];
   const int tid = threadIdx.x;
   float m = 0.f;
   int bad = 0;
-  for (size_t i = (size_t)blockIdx.x * 256 + tid; i < n; i += (size_t)gridDim.x * 256) {
-    const float x = load_w(w, dtype, i);
-    if (!isfinite(x))
-      bad = 1;
-    else
-      m = fmaxf(m, fabsf(x));
+  const size_t g = (size_t)blockIdx.x * 256 + tid, stride = (size_t)gridDim.x * 256;
+  for (size_t v = g; v < nvec; v += stride) {
+    float x[PER];
+    unpack16<DT>(ldg_nt<u32x4>(static_cast<const uint8_t *>(w) + 16 * v), x);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      bad |= !isfinite(x[i]);
+      m = fmaxf(m, fabsf(x[i]));
+    }
+  }
+  for (size_t i = nvec * PER + g; i < n; i += stride) {
+    const float x = load_w(static_cast<const void *>(w), DT, i);
+    bad |= !isfinite(x);
+    m = fmaxf(m, fabsf(x));
   }
   sm[tid] = m;
   sb[tid] = bad;
@@ -111,15 +142,38 @@ __device__ inline uint32_t q4_code(float x, float s) {
   return (uint32_t)(min(7, max(-8, q)) + 8);
 }
 
-__global__ __launch_bounds__(256) void k_q4_pack_t(const void *w, int dtype, int n_out, int n_in,
-                                                   float s, uint8_t *out) {
+// VEC: rows of the weight read as 16-byte words (n_in a multiple of the word's
+// element count, base aligned); else element by element.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void k_q4_pack_t(const void *w, int n_out, int n_in, float s,
+                                                   uint8_t *out) {
+  constexpr int PER = DT == 0 ? 4 : 8, ESZ = DT == 0 ? 4 : 2;
   __shared__ float t[kTk][kTn + 1];
   const int tid = threadIdx.x;
   const int k0 = blockIdx.x * kTk, n0 = blockIdx.y * kTn;
-  for (int e = tid; e < kTk * kTn; e += 256) {
-    const int r = e / kTk, c = e % kTk;  // r: out index in the tile, c: in index
-    const int n = n0 + r, k = k0 + c;
-    t[c][r] = (n < n_out && k < n_in) ? load_w(w, dtype, (size_t)n * n_in + k) : 0.f;
+  if constexpr (VEC) {
+    constexpr int CPR = kTk / PER;  // words per tile row
+#pragma unroll
+    for (int e = tid; e < kTn * CPR; e += 256) {
+      const int r = e / CPR, c = (e % CPR) * PER;
+      const int n = n0 + r, k = k0 + c;
+      float x[PER];
+      if (n < n_out && k < n_in) {
+        const uint8_t *src = static_cast<const uint8_t *>(w) + ((size_t)n * n_in + k) * ESZ;
+        unpack16<DT>(ldg_nt<u32x4>(src), x);
+      } else {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) x[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < PER; ++i) t[c + i][r] = x[i];
+    }
+  } else {
+    for (int e = tid; e < kTk * kTn; e += 256) {
+      const int r = e / kTk, c = e % kTk;  // r: out index in the tile, c: in index
+      const int n = n0 + r, k = k0 + c;
+      t[c][r] = (n < n_out && k < n_in) ? load_w(w, DT, (size_t)n * n_in + k) : 0.f;
+    }
   }
   __syncthreads();
   const int c = tid >> 2, j0 = (tid & 3) * 16;  // 16 bytes = 32 out values of row k
@@ -169,8 +223,16 @@ extern "C" int ms_q4_quantize(uint8_t *d_packed, float *h_scale, const void *d_w
   if (int rc = scratch(kMaxParts * 2 * 4 + 64, &buf)) return rc;
   float *part = static_cast<float *>(buf);
   int *flag = reinterpret_cast<int *>(part + kMaxParts * 2);
-  const int nb = (int)std::min<size_t>(kMaxParts, std::max<size_t>(1, cdiv((long)n, 256 * 16)));
-  hipLaunchKernelGGL(k_absmax_part, dim3(nb), dim3(256), 0, st, d_w, dtype, n, part);
+  const int esz = dtype == 0 ? 4 : 2, per = 16 / esz;
+  const bool aligned = (reinterpret_cast<uintptr_t>(d_w) & 15) == 0;
+  const size_t nvec = aligned ? n / per : 0;
+  const int nb = (int)std::min<size_t>(kMaxParts, std::max<size_t>(1, cdiv((long)n, 256 * 32)));
+  if (dtype == 0)
+    hipLaunchKernelGGL(k_absmax_part<0>, dim3(nb), dim3(256), 0, st, d_w, n, nvec, part);
+  else if (dtype == 1)
+    hipLaunchKernelGGL(k_absmax_part<1>, dim3(nb), dim3(256), 0, st, d_w, n, nvec, part);
+  else
+    hipLaunchKernelGGL(k_absmax_part<2>, dim3(nb), dim3(256), 0, st, d_w, n, nvec, part);
   hipLaunchKernelGGL(k_absmax_fin, dim3(1), dim3(256), 0, st, part, nb);
   MS_HIP_TRY(hipGetLastError());
   float fin[2];
@@ -198,7 +260,17 @@ extern "C" int ms_q4_quantize(uint8_t *d_packed, float *h_scale, const void *d_w
   }
   const float s = (float)gs;
   const dim3 grid(cdiv((long)n_in, kTk), cdiv((long)n_out, kTn));
-  hipLaunchKernelGGL(k_q4_pack_t, grid, dim3(256), 0, st, d_w, dtype, n_out, n_in, s, d_packed);
+  const bool vec = aligned && n_in % per == 0;
+#define MS_PACK(DT, V) \
+  hipLaunchKernelGGL((k_q4_pack_t<DT, V>), grid, dim3(256), 0, st, d_w, n_out, n_in, s, d_packed)
+  if (dtype == 0) {
+    if (vec) MS_PACK(0, true); else MS_PACK(0, false);
+  } else if (dtype == 1) {
+    if (vec) MS_PACK(1, true); else MS_PACK(1, false);
+  } else {
+    if (vec) MS_PACK(2, true); else MS_PACK(2, false);
+  }
+#undef MS_PACK
   MS_HIP_TRY(hipGetLastError());
   MS_HIP_TRY(hipStreamSynchronize(st));
   *h_scale = s;
