@@ -173,6 +173,33 @@ int ms_matmul_f32(float *d_c, const float *d_a, const float *d_b, int M, int K, 
  * weight holding NaN or infinity is refused. */
 int ms_q4_quantize(uint8_t *d_packed, float *h_scale, const void *d_w, int dtype, int n_out,
                    int n_in, int block_size);
+
+/* ---- tokenizers (host only, no device use) ----------------------------------
+ * Strings are byte strings: the reference builds its text from chr(byte), so
+ * each byte is one code point 0..255.  Text outputs take (out, cap) and set *len
+ * to the size; when cap is too small the call fails with *len the size needed. */
+typedef struct ms_tokenizer ms_tokenizer;
+typedef struct ms_token_map ms_token_map;
+/* BPETokenizer.load (src/nlp/tokenizer.mojo:56-101): an .msvocab file. */
+int ms_tokenizer_load(const char *path, ms_tokenizer **out);
+int ms_tokenizer_free(ms_tokenizer *t);
+/* BPETokenizer.n_tokens (:165-166): the largest id + 1. */
+int ms_tokenizer_vocab_size(const ms_tokenizer *t, int *n);
+/* BPETokenizer.encode (:103-150): bytes, then lowest-rank leftmost merges;
+ * unknown strings give id 0.  ids = NULL asks only for the count *n. */
+int ms_tokenizer_encode(const ms_tokenizer *t, const char *text, int len, int32_t *ids,
+                        int cap, int *n);
+/* BPETokenizer.decode (:152-163): BOS 1, EOS 2 and PAD 3 skipped. */
+int ms_tokenizer_decode(const ms_tokenizer *t, const int32_t *ids, int n, char *out, int cap,
+                        int *len);
+/* BPETokenizer.token_str (:168-172): "<unk>" out of range. */
+int ms_tokenizer_token_str(const ms_tokenizer *t, int id, char *out, int cap, int *len);
+/* load_token_map (src/tokenizer/gemma_proto.mojo:59-74): vocab_proto.bin. */
+int ms_token_map_load(const char *path, ms_token_map **out);
+int ms_token_map_free(ms_token_map *m);
+int ms_token_map_size(const ms_token_map *m, int *n);
+/* TokenMap.decode (gemma_proto.mojo:27-37): "[?:id]" out of range. */
+int ms_token_map_decode(const ms_token_map *m, int id, char *out, int cap, int *len);
 /* get_token_embedding Q4 branch (lm_head.mojo:186-195): column `token` of the
  * tied head, dequantized, for each of n tokens -> d_out [n][D]. */
 int ms_embed_q4(const uint8_t *d_packed, int D, int vocab, float scale,
