@@ -134,6 +134,13 @@ _SIGS = {
     "ms_lm_head_file_write_synthetic_v2": [C.c_char_p, _I, _I, _U64],
     "ms_matmul_f32": [_P, _P, _P, _I, _I, _I, _I],
     "ms_q4_quantize": [_P, _P, _P, _I, _I, _I, _I],
+    "ms_tokenizer_load": [C.c_char_p, _P], "ms_tokenizer_free": [_P],
+    "ms_tokenizer_vocab_size": [_P, _P],
+    "ms_tokenizer_encode": [_P, C.c_char_p, _I, _P, _I, _P],
+    "ms_tokenizer_decode": [_P, _P, _I, _P, _I, _P],
+    "ms_tokenizer_token_str": [_P, _I, _P, _I, _P],
+    "ms_token_map_load": [C.c_char_p, _P], "ms_token_map_free": [_P],
+    "ms_token_map_size": [_P, _P], "ms_token_map_decode": [_P, _I, _P, _I, _P],
     "ms_model_set_lm_head_f32": [_P, _P, _I, _P],
     "ms_prof_enable": [_I],
     "ms_prof_sweep": [_P, _I, _I, C.POINTER(C.c_double), C.POINTER(C.c_double),

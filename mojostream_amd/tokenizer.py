@@ -17,19 +17,6 @@ from . import _lib, check
 
 BOS_ID, EOS_ID, UNK_ID, PAD_ID = 1, 2, 0, 3
 
-_P, _I = C.c_void_p, C.c_int
-for _name, _args in {
-    "ms_tokenizer_load": [C.c_char_p, _P], "ms_tokenizer_free": [_P],
-    "ms_tokenizer_vocab_size": [_P, _P],
-    "ms_tokenizer_encode": [_P, C.c_char_p, _I, _P, _I, _P],
-    "ms_tokenizer_decode": [_P, _P, _I, _P, _I, _P],
-    "ms_tokenizer_token_str": [_P, _I, _P, _I, _P],
-    "ms_token_map_load": [C.c_char_p, _P], "ms_token_map_free": [_P],
-    "ms_token_map_size": [_P, _P], "ms_token_map_decode": [_P, _I, _P, _I, _P],
-}.items():
-    getattr(_lib, _name).argtypes = _args
-    getattr(_lib, _name).restype = C.c_int
-
 
 def _text(call) -> str:
     """Run a (out, cap, len) call twice: once for the size, once to fill."""
