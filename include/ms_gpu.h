@@ -160,6 +160,12 @@ int ms_lm_head_argmax(const float *d_x, int M, int D, const uint8_t *d_packed,
  * probabilities in d_logits.  The id goes to *h_id. */
 int ms_sample(float *d_logits, int vocab, float temperature, const int32_t *d_generated,
               int n_generated, float penalty, uint64_t seed, int32_t *h_id);
+/* The seed ms_prefill / ms_decode_run give the LCG step (lm_head.mojo:246-248)
+ * of draw `draw` of sequence `seq` under ms_model_set_sampling(.., seed): a
+ * splitmix64 hash of the three, so that sequences and consecutive draws get
+ * independent targets.  No reference counterpart (the reference reads the
+ * clock); lets a caller reproduce the model's draws with ms_sample. */
+uint64_t ms_sample_seed(uint64_t seed, int seq, uint64_t draw);
 /* matmul_fp32_raw (kernels.mojo:616-671): C (+)= A . B with B fp32 row-major
  * [K][N], A [M][K], M <= 16; N a multiple of 16 (the reference computes whole
  * 16-column tiles only, :640).  accumulate = 1 keeps the reference's C +=. */
@@ -282,10 +288,12 @@ int ms_model_get_desc(const ms_model *m, ms_model_desc *desc, ms_layer_desc *lay
  * (lm_head.mojo:198-254) as gemma4_e4b_infer.mojo:134-182 calls it, in place
  * of the greedy argmax, when temperature > 0.01 or penalty > 1 (else greedy
  * again).  Each sequence's penalty history holds its prompt ids (from
- * ms_prefill) and then every sampled id; ms_model_reset empties it.  The
- * k-th LM head call that draws (counted from this call or ms_model_reset:
- * the prefill's first token, then every decode step) draws for sequence b
- * with seed + b + k, where the reference reads the clock.  Needs an LM head. */
+ * ms_prefill) and then every sampled id, at most 8192 ids (ms_prefill and
+ * ms_decode_run return MS_E_INVALID rather than drop any); ms_model_reset
+ * empties it.  The k-th LM head call that draws (counted from this call or
+ * ms_model_reset: the prefill's first token, then every decode step) draws
+ * for sequence b with ms_sample_seed(seed, b, k), where the reference reads
+ * the clock.  Needs an LM head. */
 int ms_model_set_sampling(ms_model *m, float temperature, float penalty, uint64_t seed);
 /* BOS embedding row (LMHead.bos_emb, lm_head.mojo:41-58).  When set, the row
  * at position 0 of ms_prefill takes it instead of the embedding of its token

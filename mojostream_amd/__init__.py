@@ -162,9 +162,11 @@ _lib.ms_host_uniform.restype = C.c_float
 _lib.ms_host_uniform.argtypes = [_U64, _U64, _U64, _F, _F]
 _lib.ms_host_fill_normal.restype = None
 _lib.ms_host_fill_normal.argtypes = [_P, _SZ, _U64, _U64]
+_lib.ms_sample_seed.restype = _U64
+_lib.ms_sample_seed.argtypes = [_U64, _I, _U64]
 
 EXPORTED = sorted(_SIGS) + ["ms_last_error", "ms_q4_packed_bytes", "ms_host_fill_random_u8",
-                            "ms_host_uniform", "ms_host_fill_normal"]
+                            "ms_host_uniform", "ms_host_fill_normal", "ms_sample_seed"]
 
 
 def lib():
@@ -220,6 +222,12 @@ def sample(d_logits: "DeviceBuffer", vocab: int, temperature: float, d_generated
     check(_lib.ms_sample(d_logits.ptr, vocab, float(temperature), gp, n_generated,
                          float(penalty), int(seed) & 0xFFFFFFFFFFFFFFFF, C.byref(out)))
     return int(out.value)
+
+
+def sample_seed(seed: int, seq: int, draw: int) -> int:
+    """Seed the model's sampler gives the LCG step of draw `draw` of sequence
+    `seq` (ms_sample_seed)."""
+    return int(_lib.ms_sample_seed(int(seed) & 0xFFFFFFFFFFFFFFFF, int(seq), int(draw)))
 
 
 def host_random_u8(n: int, seed: int, stream: int) -> np.ndarray:
@@ -480,7 +488,7 @@ class Model:
         """temperature_sampling (lm_head.mojo:198-254) in prefill and decode
         instead of the greedy argmax when temperature > 0.01 or penalty > 1;
         the k-th drawing LM head call (prefill's first token, then each decode
-        step) draws for sequence b with seed + b + k."""
+        step) draws for sequence b with sample_seed(seed, b, k)."""
         check(_lib.ms_model_set_sampling(self.h, float(temperature), float(penalty),
                                          int(seed) & 0xFFFFFFFFFFFFFFFF))
 

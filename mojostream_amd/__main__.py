@@ -30,10 +30,11 @@ def main(argv=None) -> int:
     e.add_argument("lm_head", nargs="?")
     e.add_argument("--tokens", type=int, default=32)
     e.add_argument("--stream", action="store_true", help="stream weights from pinned host")
-    e.add_argument("--temperature", type=float, default=0.0,
-                   help="sampling temperature (<= 0.01: greedy; the reference runs 0.7)")
-    e.add_argument("--penalty", type=float, default=1.0,
-                   help="repetition penalty (the reference runs 1.2)")
+    e.add_argument("--temperature", type=float, default=0.7,
+                   help="sampling temperature, the reference's 0.7 (<= 0.01 with "
+                        "--penalty 1: greedy)")
+    e.add_argument("--penalty", type=float, default=1.2,
+                   help="repetition penalty, the reference's 1.2")
     e.add_argument("--sample-seed", type=int, default=0, help="seed of the draws")
     g = sub.add_parser("fake-model", help="write a seeded synthetic .mojostream file")
     g.add_argument("out")

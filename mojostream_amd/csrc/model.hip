@@ -137,6 +137,7 @@ struct ms_model {
   int32_t *shist_n = nullptr;   // [max_seqs]
   int32_t *samp_ids = nullptr;  // [max_seqs]
   int32_t *samp_ctr = nullptr;  // LM head calls that drew since set_sampling / reset
+  std::vector<int> h_hist_n;    // host mirror of shist_n (ids in each history)
   // streaming
   uint8_t *slot[2] = {nullptr, nullptr};
   size_t slot_bytes = 0;
@@ -435,7 +436,8 @@ static int enqueue_pick(ms_model *m, const RunCfg &rc, int M, ArgmaxFin f, hipSt
     s.hist_n = m->shist_n + rc.seq0;
     s.hist_cap = kSampleMaxHistory;
     s.hist_append = 1;
-    s.seed = m->samp_seed + (uint64_t)rc.seq0;
+    s.seed = m->samp_seed;
+    s.seq0 = rc.seq0;
     s.step = m->samp_ctr;
     f.draws = m->samp_ctr;
   }
@@ -638,6 +640,7 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   m->d = d;
   m->Mmax = d.max_seqs * d.max_rows;
   m->h_pos.assign(d.max_seqs, 0);
+  m->h_hist_n.assign(d.max_seqs, 0);
   // models with an LM head prefill prompts in chunks of up to kPrefillRows
   if (d.vocab > 0) m->prefill_rows = std::max(m->Mmax, std::min(kPrefillRows, d.max_pos));
   const int M = std::max(m->Mmax, m->prefill_rows);  // workspace rows
@@ -970,6 +973,7 @@ extern "C" int ms_model_reset(ms_model *m) {
   if (int rc = require_init()) return rc;
   MS_HIP_TRY(hipMemset(m->attn_ctr, 0, (size_t)m->d.max_seqs * m->nkv_max * 4));
   if (m->shist_n) MS_HIP_TRY(hipMemset(m->shist_n, 0, (size_t)m->d.max_seqs * 4));
+  std::fill(m->h_hist_n.begin(), m->h_hist_n.end(), 0);
   if (m->samp_ctr) MS_HIP_TRY(hipMemset(m->samp_ctr, 0, 4));
   return MS_OK;
 }
@@ -989,6 +993,7 @@ extern "C" int ms_model_set_sampling(ms_model *m, float temperature, float penal
     if (int rc = dmalloc(m, (void **)&m->shist_n, S * 4)) return rc;
     if (int rc = dmalloc(m, (void **)&m->samp_ctr, 4)) return rc;
     MS_HIP_TRY(hipMemset(m->shist_n, 0, S * 4));
+    std::fill(m->h_hist_n.begin(), m->h_hist_n.end(), 0);
   }
   if (m->samp_ctr) MS_HIP_TRY(hipMemset(m->samp_ctr, 0, 4));
   m->sampling = on;
@@ -1097,6 +1102,11 @@ extern "C" int ms_decode_run(ms_model *m, int n_steps, int use_graph, int32_t *h
   if (int rc = check_ready(m, true)) return rc;
   const int B = m->dec_nseq;
   if (int rc = check_positions(m, m->h_pos.data(), B, 1, n_steps - 1)) return rc;
+  if (m->sampling)
+    for (int b = 0; b < B; ++b)
+      MS_CHECK_ARG(m->h_hist_n[b] + n_steps <= kSampleMaxHistory,
+                   "decode_run: the repetition-penalty history of a sequence would exceed "
+                   "8192 ids (prompt + generated); reset the model first");
   if (!m->d.resident) use_graph = 0;  // streaming runs eagerly (host-side slot logic)
   hipStream_t st = ctx().stream;
   int done = 0;
@@ -1132,7 +1142,10 @@ extern "C" int ms_decode_run(ms_model *m, int n_steps, int use_graph, int32_t *h
     done += chunk;
   }
   if (g_prof.on) prof_collect();
-  for (int b = 0; b < B; ++b) m->h_pos[b] += n_steps;
+  for (int b = 0; b < B; ++b) {
+    m->h_pos[b] += n_steps;
+    if (m->sampling) m->h_hist_n[b] += n_steps;
+  }
   return MS_OK;
 }
 
@@ -1154,8 +1167,12 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
   MS_HIP_TRY(hipMemcpyAsync(dtok, h_tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, st));
   if (m->sampling) {
     // the prompt ids open the sequence's penalty history
-    // (gemma4_e4b_infer.mojo:134-139,157-161)
-    const int nh = std::min(n_tokens, kSampleMaxHistory);
+    // (gemma4_e4b_infer.mojo:134-139,157-161); the history holds at most
+    // kSampleMaxHistory ids (prompt, the first draw, then one per step)
+    MS_CHECK_ARG(n_tokens + 1 <= kSampleMaxHistory,
+                 "prefill: with sampling on, the prompt and the first draw must fit the "
+                 "8192-id repetition-penalty history");
+    const int nh = n_tokens;
     MS_HIP_TRY(hipMemcpyAsync(m->shist + (size_t)seq * kSampleMaxHistory, dtok, (size_t)nh * 4,
                               hipMemcpyDeviceToDevice, st));
     MS_HIP_TRY(hipMemcpyAsync(m->shist_n + seq, &nh, 4, hipMemcpyHostToDevice, st));
@@ -1202,6 +1219,7 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
   MS_HIP_TRY(hipStreamSynchronize(st));
   if (h_first_id) *h_first_id = id;
   m->h_pos[seq] = pos0 + n_tokens;
+  if (m->sampling) m->h_hist_n[seq] = n_tokens + 1;
   return MS_OK;
 }
 

@@ -11,7 +11,8 @@
 //            of operations on that logit.
 //   greedy   temperature <= 0.01: the first index of the maximum (:222-228).
 //   softmax  exp((v - max) / T), the sum, the division (:230-243).
-//   draw     one LCG step of the seed (:246-248); the first index whose
+//   draw     one LCG step of the seed (:246-248; in the model the seed of draw
+//            k of sequence b is draw_seed(seed, b, k)); the first index whose
 //            running sum reaches the target, else n - 1 (:250-254).  Thread t
 //            owns the contiguous slice t of the row; the slices' sums are
 //            added in slice order, then the slice holding the crossing is
@@ -141,7 +142,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
       }
     }
     __syncthreads();
-    const uint64_t seed = a.seed + (a.step ? (uint64_t)sld(a.step) : 0ull) + (uint64_t)row;
+    const uint64_t seed =
+        a.step ? draw_seed(a.seed, (uint64_t)(a.seq0 + row), (uint64_t)sld(a.step)) : a.seed;
     const float target = lcg_target(seed);
     float cdf = rv[tid];
     int found = n;
@@ -201,6 +203,7 @@ extern "C" int ms_sample(float *d_logits, int vocab, float temperature,
   hipStream_t st = ctx().stream;
   void *buf = nullptr;
   if (int rc = scratch(64, &buf)) return rc;
+  // (a single draw: the seed goes to the LCG step as given)
   int32_t *d_n = static_cast<int32_t *>(buf), *d_id = d_n + 4;
   MS_HIP_TRY(hipMemcpyAsync(d_n, &n_generated, 4, hipMemcpyHostToDevice, st));
   SampleArgs a{};
@@ -218,4 +221,8 @@ extern "C" int ms_sample(float *d_logits, int vocab, float temperature,
   MS_HIP_TRY(hipMemcpyAsync(h_id, d_id, 4, hipMemcpyDeviceToHost, st));
   MS_HIP_TRY(hipStreamSynchronize(st));
   return MS_OK;
+}
+
+extern "C" uint64_t ms_sample_seed(uint64_t seed, int seq, uint64_t draw) {
+  return draw_seed(seed, (uint64_t)seq, draw);
 }

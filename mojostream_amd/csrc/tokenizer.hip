@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <algorithm>
 #include <cstring>
+#include <exception>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -36,6 +37,9 @@ namespace {
 
 constexpr uint32_t kVocabMagic = 0x4256534D;  // "MSVB"
 constexpr int kBos = 1, kEos = 2, kUnk = 0, kPad = 3;
+// Largest token id a vocabulary file may use (64 times Gemma's 262,144 ids);
+// the id table holds max id + 1 entries.
+constexpr uint32_t kMaxTokenId = (1u << 24) - 1;
 
 bool read_file(const char *path, std::vector<uint8_t> &raw) {
   FILE *fp = fopen(path, "rb");
@@ -98,20 +102,37 @@ extern "C" int ms_tokenizer_load(const char *path, ms_tokenizer **out) {
   c.u32();
   if (!c.ok || magic != kVocabMagic) return fail(MS_E_IO, "tokenizer: invalid magic number");
   auto *t = new ms_tokenizer;
-  for (uint32_t i = 0; i < n_tokens && c.ok; ++i) {
-    const uint32_t id = c.u32(), len = c.u32();
-    std::string s = c.bytes(len);
-    if (!c.ok) break;
-    // _set_token (:45-52): grow with "<unk>", both directions, vocab = max id + 1
-    if (t->id_to_tok.size() <= id) t->id_to_tok.resize((size_t)id + 1, "<unk>");
-    t->id_to_tok[id] = s;
-    t->tok_to_id[s] = (int)id;
-    t->vocab_size = std::max(t->vocab_size, (int)id + 1);
+  bool bad_id = false;
+  try {
+    for (uint32_t i = 0; i < n_tokens && c.ok; ++i) {
+      const uint32_t id = c.u32(), len = c.u32();
+      std::string s = c.bytes(len);
+      if (!c.ok) break;
+      // ids index a table of id + 1 entries and are returned as int32: a
+      // larger id cannot come from a real vocabulary (the reference would try
+      // to grow its List to that size)
+      if (id > kMaxTokenId) {
+        bad_id = true;
+        break;
+      }
+      // _set_token (:45-52): grow with "<unk>", both directions, vocab = max id + 1
+      if (t->id_to_tok.size() <= id) t->id_to_tok.resize((size_t)id + 1, "<unk>");
+      t->id_to_tok[id] = s;
+      t->tok_to_id[s] = (int)id;
+      t->vocab_size = std::max(t->vocab_size, (int)id + 1);
+    }
+    for (uint32_t r = 0; r < n_merges && c.ok && !bad_id; ++r) {
+      std::string l = c.bytes(c.u32());
+      std::string rr = c.bytes(c.u32());
+      if (c.ok) t->merge_rank[l + "|" + rr] = (int)r;
+    }
+  } catch (const std::exception &e) {  // no C++ exception crosses the ABI
+    delete t;
+    return fail(MS_E_IO, std::string("tokenizer: cannot hold the vocabulary: ") + e.what());
   }
-  for (uint32_t r = 0; r < n_merges && c.ok; ++r) {
-    std::string l = c.bytes(c.u32());
-    std::string rr = c.bytes(c.u32());
-    if (c.ok) t->merge_rank[l + "|" + rr] = (int)r;
+  if (bad_id) {
+    delete t;
+    return fail(MS_E_IO, "tokenizer: token id above " + std::to_string(kMaxTokenId));
   }
   if (!c.ok) {
     delete t;
@@ -182,12 +203,16 @@ extern "C" int ms_tokenizer_decode(const ms_tokenizer *t, const int32_t *ids, in
   return copy_out(s, out, cap, len);
 }
 
-// BPETokenizer.token_str (:168-172)
+// BPETokenizer.token_str (:168-172): "<unk>" at or past the end of the table;
+// a negative id counts from the end, as in decode (List indexing).
 extern "C" int ms_tokenizer_token_str(const ms_tokenizer *t, int id, char *out, int cap,
                                       int *len) {
   MS_CHECK_ARG(t && len, "tokenizer_token_str: null argument");
-  const bool in = id >= 0 && (size_t)id < t->id_to_tok.size();
-  return copy_out(in ? t->id_to_tok[(size_t)id] : std::string("<unk>"), out, cap, len);
+  const long sz = (long)t->id_to_tok.size();
+  long i = id;
+  if (i < 0) i += sz;
+  const bool in = i >= 0 && i < sz && id < sz;
+  return copy_out(in ? t->id_to_tok[(size_t)i] : std::string("<unk>"), out, cap, len);
 }
 
 extern "C" int ms_token_map_load(const char *path, ms_token_map **out) {

@@ -29,6 +29,9 @@ from . import (DeviceBuffer, Model, check, demo_layer, device_info, host_normal,
                host_random_u8, init, lib, Arch)
 from . import streaming as st
 
+# TokenMap.is_eos (gemma_proto.mojo:51-52)
+EOS_ID = 1
+
 BENCH_STEPS = 100   # harness.mojo:30
 BENCH_BATCH = 4     # harness.mojo:31
 KV_MAX_SEQ = 512    # harness.mojo:32
@@ -246,13 +249,15 @@ def run_q4_benchmark(shapes=((4, 1024, 1024), (64, 1024, 1024), (4, 4096, 4096),
 
 def run_e4b_infer(path: Optional[str] = None, lm_head_path: Optional[str] = None,
                   prompt: Sequence[int] = (2, 603, 5012, 575, 4124, 608), n_stream: int = 32,
-                  seed: int = 42, resident: bool = True, temperature: float = 0.0,
-                  penalty: float = 1.0, sample_seed: int = 0) -> dict:
-    """E4B inference driver: BOS row + prompt (TTFT), then `n_stream`
-    generated tokens, greedy or (temperature > 0.01 or penalty > 1) sampled
-    like the reference's TEMPERATURE / REPETITION_PENALTY run
-    (gemma4_e4b_infer.mojo:38-39,139,179) with `sample_seed` in place of the
-    clock.  Without files it builds the seeded E4B-shaped synthetic model
+                  seed: int = 42, resident: bool = True, temperature: float = 0.7,
+                  penalty: float = 1.2, sample_seed: int = 0) -> dict:
+    """E4B inference driver: BOS row + prompt (TTFT), then up to `n_stream`
+    generated tokens, sampled like the reference's run with its TEMPERATURE 0.7
+    and REPETITION_PENALTY 1.2 (gemma4_e4b_infer.mojo:38-39,139,179), with
+    `sample_seed` in place of the clock, or greedy (temperature <= 0.01 and
+    penalty 1).  Like the reference, generation stops after an EOS id (1,
+    TokenMap.is_eos gemma_proto.mojo:51-52; :184-185), which is kept in the
+    list.  Without files it builds the seeded E4B-shaped synthetic model
     (vocab 262144)."""
     init(0)
     sampled = temperature > 0.01 or penalty > 1.0
@@ -284,12 +289,18 @@ def run_e4b_infer(path: Optional[str] = None, lm_head_path: Optional[str] = None
     print(f"  init {init_ms:.0f} ms | TTFT ({len(prompt)} prompt tokens) {ttft_ms:.2f} ms "
           f"-> token {first}")
     t2 = time.perf_counter_ns()
-    ids = model.decode([first], [len(prompt)], n_stream) if n_stream else np.zeros((0, 1))
+    gen = [first]
+    # one step per call (one graph replay each), so that an EOS ends the run
+    for k in range(n_stream):
+        ids = (model.decode([gen[-1]], [len(prompt)], 1) if k == 0
+               else model.decode_continue(1, 1))
+        gen.append(int(ids[0, 0]))
+        if gen[-1] == EOS_ID:
+            break
     stream_ms = (time.perf_counter_ns() - t2) / 1e6
-    gen = [first] + [int(v) for v in ids[:, 0]]
     model.close()
-    avg = stream_ms / max(n_stream, 1)
+    avg = stream_ms / max(len(gen) - 1, 1)
     print(f"  generated ids: {gen}")
-    print(f"  streaming {n_stream} tokens: {stream_ms:.1f} ms, {avg:.3f} ms/token, "
+    print(f"  streaming {len(gen) - 1} tokens: {stream_ms:.1f} ms, {avg:.3f} ms/token, "
           f"{1000.0 / avg:.1f} t/s")
     return dict(init_ms=init_ms, ttft_ms=ttft_ms, ids=gen, ms_per_token=avg)

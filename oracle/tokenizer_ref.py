@@ -37,3 +37,37 @@ def decode(ids: Sequence[int], id_to_tok: Sequence[bytes]) -> bytes:
             continue
         out += id_to_tok[i]
     return out
+
+
+def load(path: str):
+    """An .msvocab file (BPETokenizer.load :56-101; format of
+    scripts/create_vocab.py:7-21): header magic "MSVB", n_tokens, n_merges,
+    reserved; n_tokens (id, len, bytes); n_merges (len, left, len, right) in
+    rank order.  Returns (vocab bytes -> id, id table with "<unk>" in the gaps,
+    merges)."""
+    import struct
+    raw = open(path, "rb").read()
+    magic, n_tok, n_merge, _ = struct.unpack_from("<IIII", raw, 0)
+    if magic != 0x4256534D:
+        raise ValueError("invalid magic")
+    pos = 16
+    vocab, table = {}, []
+    for _ in range(n_tok):
+        i, n = struct.unpack_from("<II", raw, pos)
+        pos += 8
+        s = raw[pos:pos + n]
+        pos += n
+        while len(table) <= i:
+            table.append(b"<unk>")
+        table[i] = s
+        vocab[s] = i
+    merges = []
+    for _ in range(n_merge):
+        (n,) = struct.unpack_from("<I", raw, pos)
+        left = raw[pos + 4:pos + 4 + n]
+        pos += 4 + n
+        (n,) = struct.unpack_from("<I", raw, pos)
+        right = raw[pos + 4:pos + 4 + n]
+        pos += 4 + n
+        merges.append((left, right))
+    return vocab, table, merges

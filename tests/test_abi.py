@@ -91,3 +91,29 @@ def test_arch_presets_match_reference_sizes():
     assert [l for l in range(42) if ms.e4b_is_full(l)] == [5, 11, 17, 23, 29, 35, 41]
     assert ms.arch_14b().weight_bytes() == 6606028800
     assert ms.arch_demo().weight_bytes() == 304087040
+
+
+def test_sampler_draw_seeds_are_independent():
+    """The model's draw seeds (ms_sample_seed: a splitmix64 hash of seed,
+    sequence and draw count, fed to the reference's LCG step
+    lm_head.mojo:246-248) must not repeat across sequences with a lag, and
+    consecutive LCG targets must not be an evenly spaced series."""
+    from oracle.binding import Oracle
+    o = Oracle()
+    n = 2048
+    seeds = {b: [ms.sample_seed(1234, b, k) for k in range(n)] for b in range(4)}
+    flat = [s for b in seeds for s in seeds[b]]
+    assert len(set(flat)) == len(flat)
+    tg = {b: np.array([o.sample_target(s) for s in seeds[b]]) for b in range(4)}
+    for lag in range(0, 8):  # sequence 1 is no shifted copy of sequence 0
+        assert not np.any(tg[1][: n - lag] == tg[0][lag:])
+    for b in range(4):
+        t = tg[b]
+        assert 0.45 < t.mean() < 0.55 and 0.07 < t.var() < 0.097   # U(0,1): 0.5, 1/12
+        r = np.corrcoef(t[:-1], t[1:])[0, 1]
+        assert abs(r) < 0.1
+        d = np.diff(t) % 1.0                      # a single LCG step per draw from
+        assert np.std(d) > 0.2                    # seed + k would make this constant
+    # the formula of the former scheme (seed + sequence + draw) has that flaw
+    old = np.array([o.sample_target(1234 + k) for k in range(n)])
+    assert np.std(np.diff(old) % 1.0) < 1e-3

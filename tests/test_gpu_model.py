@@ -174,7 +174,9 @@ def test_e4b_small_batch4_vs_single(gpu, fast_oracle):
 
 def oracle_sampled(om, oracle, prompt, n_steps, temperature, penalty, seed):
     """gemma4_e4b_infer.mojo:134-182 with the oracle: the prompt ids open the
-    penalty history, every drawn id joins it, draw k uses seed + k."""
+    penalty history, every drawn id joins it, draw k of sequence 0 uses
+    sample_seed(seed, 0, k)."""
+    import mojostream_amd as ms
     hist = list(prompt)
     h = None
     for i, t in enumerate(prompt):
@@ -185,7 +187,8 @@ def oracle_sampled(om, oracle, prompt, n_steps, temperature, penalty, seed):
         if k:
             _, h = om.decode_token(out[-1], pos, hidden=True)
             pos += 1
-        tid, _ = oracle.sample(om.logits_for(h[-1]), temperature, hist, penalty, seed + k)
+        tid, _ = oracle.sample(om.logits_for(h[-1]), temperature, hist, penalty,
+                               ms.sample_seed(seed, 0, k))
         out.append(tid)
         hist.append(tid)
     return out
@@ -217,6 +220,47 @@ def test_e4b_small_sampled_decode_vs_oracle(gpu, fast_oracle):
         gids = [first] + [int(v) for v in m.decode([first], [len(prompt)], 3)[:, 0]]
         assert gids == oracle_greedy(synthetic_oracle_model(fast_oracle, arch, SEED), prompt, 4)
         m.close()
+
+
+def test_e4b_small_sampled_decode_two_sequences(gpu, fast_oracle):
+    """Two sequences with the same prompt sampled together: each draws with
+    its own seeds sample_seed(seed, b, k) and matches the oracle's run for that
+    sequence."""
+    import ctypes as C
+    ms = gpu
+    arch = ms.arch_e4b(max_full_seq=256, n_layers=6, vocab=16384)
+    say("E4B 6 layers, vocab 16384: two sequences sampled together, T=0.05, penalty 1.5")
+    prompt = prompt_ids(5, arch.vocab, 31)
+    steps = 10
+    m = build(ms, arch, max_seqs=2, max_rows=8, max_pos=256)
+    m.set_sampling(0.05, 1.5, 99)
+    t = np.asarray(prompt, np.int32)
+    firsts = []
+    for b in range(2):
+        f = C.c_int32()
+        ms.check(ms.lib().ms_prefill(m.h, b, t.ctypes.data, len(t), 0, C.byref(f)))
+        firsts.append(int(f.value))
+    ids = m.decode(firsts, [len(prompt)] * 2, steps - 1)
+    m.close()
+    for b in range(2):
+        got = [firsts[b]] + [int(v) for v in ids[:, b]]
+        om = synthetic_oracle_model(fast_oracle, arch, SEED)
+        # the draw counter counts LM head calls: both prefills, then the steps
+        hist = list(prompt)
+        _, h = None, None
+        for i, tok in enumerate(prompt):
+            _, h = om.decode_token(tok, i, hidden=True)
+        ref = []
+        for k in range(steps):
+            if k:
+                _, h = om.decode_token(ref[-1], len(prompt) + k - 1, hidden=True)
+            draw = b if k == 0 else k + 1
+            tid, _ = fast_oracle.sample(om.logits_for(h[-1]), 0.05, hist, 1.5,
+                                        ms.sample_seed(99, b, draw))
+            ref.append(tid)
+            hist.append(tid)
+        print(f"  seq {b}: {got}")
+        assert got == ref, (b, got, ref)
 
 
 def test_e4b_small_fp32_head_file_greedy(gpu, fast_oracle, tmp_path):

@@ -7,6 +7,7 @@
 - The reference's round trip "Hallo Mojo" (tokenizer_test.mojo:75).
 - File errors: wrong magic, truncation; TokenMap's "[?:id]".
 """
+import os
 import random
 import struct
 
@@ -73,6 +74,9 @@ def test_unknown_specials_and_token_str(tmp_path):
     assert t.decode([-1]) == "ab"                # a negative id counts from the end
     assert t.token_str(5) == "<unk>" and t.token_str(99) == "<unk>"
     assert t.token_str(12) == "ab"
+    # a negative id counts from the end in token_str as in decode
+    assert t.token_str(-1) == "ab" and t.token_str(-13) == "<unk>"
+    assert t.token_str(-14) == "<unk>"           # before the start of the table
     assert t.n_tokens() == 13
     t.close()
 
@@ -128,6 +132,50 @@ def test_file_errors(tmp_path):
         BPETokenizer(p)
     with pytest.raises(ms.MSError, match="cannot read"):
         TokenMap(str(tmp_path / "missing.bin"))
+    # a corrupt id would size the id table to 2^32 entries: refused
+    write_msvocab(p, SPECIAL + [(0xFFFFFFFF, b"x")], [])
+    with pytest.raises(ms.MSError, match="token id above"):
+        BPETokenizer(p)
+    write_msvocab(p, SPECIAL + [((1 << 24) - 1, b"x")], [])  # the largest id accepted
+    t = BPETokenizer(p)
+    assert t.n_tokens() == 1 << 24 and t.token_str((1 << 24) - 1) == "x"
+    t.close()
+
+
+GOLDEN_VOCAB = os.path.join(os.path.dirname(__file__), "golden", "vocab.msvocab")
+
+
+def test_reference_vocab_fixture():
+    """vocab.msvocab as the reference ships it (scripts/create_vocab.py:28-80:
+    4 special tokens, printable ASCII 32..126 under their byte values, 15
+    merged tokens with ids 256..270, 15 merges in rank order).  tokenizer_test.mojo
+    encodes "Hallo Mojo" and expects the round trip.  By hand: H+a (rank 0),
+    Ha+l (1), Hal+l (2), Hall+o (3) give "Hallo"; of the pairs left, M+o (rank
+    4) beats " "+M (rank 7), then Mo+j (5) and Moj+o (6) give "Mojo"; no rank
+    joins " " with "Mojo".  So the ids are [Hallo 259, " " 32, Mojo 262]."""
+    from mojostream_amd.tokenizer import BPETokenizer
+    raw = open(GOLDEN_VOCAB, "rb").read()
+    assert len(raw) == 1252
+    magic, n_tok, n_merge, _ = struct.unpack_from("<IIII", raw, 0)
+    assert (magic, n_tok, n_merge) == (0x4256534D, 114, 15)
+    t = BPETokenizer(GOLDEN_VOCAB)
+    assert t.n_tokens() == 271
+    ids = t.encode("Hallo Mojo")
+    assert ids == [259, 32, 262]
+    assert [t.token_str(i) for i in ids] == ["Hallo", " ", "Mojo"]
+    assert t.decode(ids) == "Hallo Mojo"
+    assert t.decode([1] + ids + [2]) == "Hallo Mojo"      # BOS / EOS skipped
+    for c in range(32, 127):
+        assert t.encode(chr(c)) == [c]
+    assert t.token_str(100) == "d" and t.token_str(200) == "<unk>"  # gap 127..255
+    assert t.token_str(-1) == "oj"                        # id 270, the last one
+    assert t.encode("Hello") == [72, 101, 269]            # l+l (rank 11), then ll+o (13)
+    assert t.encode("é") == [0, 0]                         # two UTF-8 bytes, both unknown
+    # the restatement reads the same file the same way
+    vocab, id_to_tok, merges = ref.load(GOLDEN_VOCAB)
+    for text in ("Hallo Mojo", " Mojo Hallo", "llo all Mo", "HaHal Hall", ""):
+        assert t.encode(text) == ref.encode(text.encode(), merges, vocab)
+    t.close()
 
 
 def test_token_map(tmp_path):
