@@ -39,6 +39,9 @@ Ctx &ctx();
 int require_init();
 // Grows the kernel-level scratch buffer (eager use only, never under capture).
 int scratch(size_t bytes, void **out);
+// Device address of the no-allocation scratch array on `device` (the current
+// device), taken once (q4.hip); called by ms_init.
+int q4_noalloc_init(int device);
 
 // ---- vector types -------------------------------------------------------------
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));

@@ -946,18 +946,44 @@ extern "C" int ms_dequant_q4_packed(float *d_out, const uint8_t *d_packed, int K
   return MS_OK;
 }
 
-extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
-                            int K, int N, float scale, int accumulate) {
-  if (int rc = require_init()) return rc;
-  if (int rc = check_q4_shape(K, N)) return rc;
-  MS_CHECK_ARG(M >= 1, "matmul: M must be >= 1");
-  MS_CHECK_ARG(K <= kQuantMaxK, "matmul: K must be <= 16384");
+// ------------------------------------------------------------------------------
+// No-allocation scratch: the quantized activation rows of
+// ms_q4_matmul_noalloc live in this file-scope device array (one copy per GPU
+// the library runs on, held until the process ends).  Its device address is
+// taken once per device by q4_noalloc_init (from ms_init, with that device
+// current); host code uses that address, never the array's name.
+// ------------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;  // 4 MiB
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace ms {
+
+constexpr int kNoAllocMaxDevices = 64;
+static void *g_noalloc_ptr[kNoAllocMaxDevices] = {};
+
+int q4_noalloc_init(int device) {
+  MS_CHECK_ARG(device >= 0 && device < kNoAllocMaxDevices, "no-alloc scratch: device index");
+  if (g_noalloc_ptr[device]) return MS_OK;
+  void *p = nullptr;
+  MS_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch)));
+  MS_CHECK_ARG(p != nullptr, "no-alloc scratch: no device address");
+  g_noalloc_ptr[device] = p;
+  return MS_OK;
+}
+
+// Scratch bytes a q4 matmul of M rows of length K uses for its quantized rows.
+static size_t q4_matmul_scratch_bytes(int M, int K) {
+  return M > kGemvMaxM ? quant_rows_bytes(gemm_row_pad(M), K)
+                       : quant_rows_bytes(kGemvMaxM, K);
+}
+
+// C (+)= A . deq(W) with the quantized rows in `buf` (q4_matmul_scratch_bytes).
+static int q4_matmul_impl(float *d_C, const float *d_A, const uint8_t *d_packed, int M, int K,
+                          int N, float scale, int accumulate, void *buf) {
   hipStream_t st = ctx().stream;
   if (M > kGemvMaxM) {
     // many rows: quantize all of them once, then the MFMA GEMM
     const int Mp = gemm_row_pad(M);
-    void *buf = nullptr;
-    if (int rc = scratch(quant_rows_bytes(Mp, K), &buf)) return rc;
     GemmArgs g{};
     g.epi = accumulate ? EPI_ACCUMULATE : EPI_STORE;
     g.M = M;
@@ -976,8 +1002,6 @@ extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packe
   }
   const int chunk = kGemvMaxM;
   const int P = (N / 16) % 4 == 0 && N >= 4 * 16 * 512 ? 4 : 1;
-  void *buf = nullptr;
-  if (int rc = scratch(quant_rows_bytes(chunk, K), &buf)) return rc;
   const QuantRows q = quant_rows_view(buf, chunk, K);
   for (int m0 = 0; m0 < M; m0 += chunk) {
     const int mm = (M - m0 < chunk) ? M - m0 : chunk;
@@ -1002,3 +1026,38 @@ extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packe
   }
   return MS_OK;
 }
+
+static int q4_matmul_check(int M, int K, int N) {
+  if (int rc = check_q4_shape(K, N)) return rc;
+  MS_CHECK_ARG(M >= 1, "matmul: M must be >= 1");
+  MS_CHECK_ARG(K <= kQuantMaxK, "matmul: K must be <= 16384");
+  return MS_OK;
+}
+
+}  // namespace ms
+
+extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
+                            int K, int N, float scale, int accumulate) {
+  using namespace ms;
+  if (int rc = require_init()) return rc;
+  if (int rc = q4_matmul_check(M, K, N)) return rc;
+  void *buf = nullptr;
+  if (int rc = ms::scratch(q4_matmul_scratch_bytes(M, K), &buf)) return rc;
+  return q4_matmul_impl(d_C, d_A, d_packed, M, K, N, scale, accumulate, buf);
+}
+
+extern "C" int ms_q4_matmul_noalloc(float *d_C, const float *d_A, const uint8_t *d_packed,
+                                    int M, int K, int N, float scale, int accumulate) {
+  using namespace ms;
+  if (int rc = require_init()) return rc;
+  if (int rc = q4_matmul_check(M, K, N)) return rc;
+  const size_t need = q4_matmul_scratch_bytes(M, K);
+  if (need > kNoAllocScratchBytes)
+    return fail(MS_E_INVALID, "q4_matmul_noalloc: " + std::to_string(M) + " rows of " +
+                                  std::to_string(K) + " need " + std::to_string(need) +
+                                  " bytes of scratch, above its 4 MiB maximum");
+  void *buf = g_noalloc_ptr[ctx().device];
+  if (!buf) return fail(MS_E_STATE, "q4_matmul_noalloc: scratch address not set up");
+  return q4_matmul_impl(d_C, d_A, d_packed, M, K, N, scale, accumulate, buf);
+}
+

@@ -70,6 +70,7 @@ extern "C" int ms_init(int device) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(MS_E_STATE, std::string("ms_init: built for gfx950, device is ") +
                                 prop.gcnArchName);
+  if (int rc = q4_noalloc_init(device)) return rc;
   MS_HIP_TRY(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
   MS_HIP_TRY(hipStreamCreateWithFlags(&g_ctx.copy_stream, hipStreamNonBlocking));
   g_ctx.n_cu = prop.multiProcessorCount;
