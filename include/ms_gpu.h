@@ -76,6 +76,17 @@ int ms_host_free(void *h_ptr);
 int ms_fill_random_u8(uint8_t *d_dst, size_t n, uint64_t seed, uint64_t stream);
 void ms_host_fill_random_u8(uint8_t *h_dst, size_t n, uint64_t seed,
                             uint64_t stream);
+/* The same bytes, or with balanced != 0 every zero nibble replaced by 8.  No
+ * reference counterpart.  Uniform nibbles (the reference's synthetic weights)
+ * have mean 7.5 against the zero point 8, so every weight has mean -scale/2;
+ * through the layers this common component drives every hidden state to one
+ * direction, and the model's greedy output no longer depends on its input.
+ * Balanced nibbles (1..15, mean 8) give zero-mean weights and a model whose
+ * output does; parity checks use them where token ids must discriminate. */
+int ms_fill_random_q4(uint8_t *d_dst, size_t n, uint64_t seed, uint64_t stream,
+                      int balanced);
+void ms_host_fill_random_q4(uint8_t *h_dst, size_t n, uint64_t seed, uint64_t stream,
+                            int balanced);
 /* Uniform [lo,hi) float for (seed, stream, index) (scales: U(0.04,0.15),
  * PLE: U(0.8,1.2), create_fake_model.py:95,203). */
 float ms_host_uniform(uint64_t seed, uint64_t stream, uint64_t index, float lo,
@@ -313,6 +324,17 @@ int ms_model_set_sampling(ms_model *m, float temperature, float penalty, uint64_
  * gemma4_e4b_infer.mojo:94,116-117).  h_bos NULL clears it. */
 int ms_model_set_bos(ms_model *m, const float *h_bos);
 
+/* Taps for parity checks (the per-layer comparison of validate_layer.mojo
+ * :138-154 needs each layer's output; the reference's loops hold them in host
+ * memory).  With d_hidden set, every decode step of ms_decode_run writes each
+ * layer's output rows to d_hidden [n_layers][n_seqs][hidden], and ms_prefill
+ * writes each layer's output for the prompt's last row to d_hidden
+ * [n_layers][hidden].  With d_logits set, every LM head call writes its raw
+ * logits (before any sampling) to d_logits [rows][vocab] (decode: one row per
+ * sequence; prefill: the last prompt row).  Each call overwrites the taps.
+ * NULL switches a tap off. */
+int ms_model_set_taps(ms_model *m, float *d_hidden, float *d_logits);
+
 /* ---- .mojostream weight files (host side) -------------------------------- */
 /* MojoStreamMeta (mojostream.mojo:47-69) plus the fields the reference parses
  * but does not keep, and the Engram extension of format tag 2
@@ -416,7 +438,8 @@ int ms_prof_get(int cls, const char **name, long *launches, double *total_ms,
  * profiling was enabled is re-launched back to back `passes` times over every
  * layer with the same shapes, each launch on that layer's weights (so weights
  * come from HBM as in a decode step), between two HIP events on the library
- * stream.  Outputs average microseconds and bytes of Q4 weights per launch.
+ * stream.  passes < 0 re-launches it -passes times on its own layer's weights
+ * (cache-hot after the first launch).  Outputs average microseconds and bytes of Q4 weights per launch.
  * The re-launches overwrite only per-step scratch rows (recomputed by the next
  * decode step); KV caches and positions are untouched.  No reference
  * counterpart: measurement support. */

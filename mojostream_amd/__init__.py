@@ -92,6 +92,7 @@ _SIGS = {
     "ms_memcpy_d2d": [_P, _P, _SZ], "ms_memset": [_P, _I, _SZ],
     "ms_host_alloc": [C.POINTER(C.c_void_p), _SZ], "ms_host_free": [_P],
     "ms_fill_random_u8": [_P, _SZ, _U64, _U64],
+    "ms_fill_random_q4": [_P, _SZ, _U64, _U64, _I],
     "ms_q4_pack": [_P, _P, _I, _I], "ms_host_q4_pack": [_P, _P, _I, _I],
     "ms_dequant_q4": [_P, _P, _I, _I, _F], "ms_dequant_q4_packed": [_P, _P, _I, _I, _F],
     "ms_q4_matmul": [_P, _P, _P, _I, _I, _I, _F, _I],
@@ -119,6 +120,7 @@ _SIGS = {
     "ms_model_set_bos": [_P, _P],
     "ms_model_set_sampling": [_P, _F, _F, _U64],
     "ms_model_set_pinned": [_P, _P],
+    "ms_model_set_taps": [_P, _P, _P],
     "ms_file_open": [C.c_char_p, C.POINTER(C.c_void_p)], "ms_file_close": [_P],
     "ms_file_get_meta": [_P, C.POINTER(FileMeta)],
     "ms_file_get_entry": [_P, _I, C.POINTER(FileEntry)],
@@ -159,6 +161,8 @@ _lib.ms_q4_packed_bytes.restype = C.c_size_t
 _lib.ms_q4_packed_bytes.argtypes = [_I, _I]
 _lib.ms_host_fill_random_u8.restype = None
 _lib.ms_host_fill_random_u8.argtypes = [_P, _SZ, _U64, _U64]
+_lib.ms_host_fill_random_q4.restype = None
+_lib.ms_host_fill_random_q4.argtypes = [_P, _SZ, _U64, _U64, _I]
 _lib.ms_host_uniform.restype = C.c_float
 _lib.ms_host_uniform.argtypes = [_U64, _U64, _U64, _F, _F]
 _lib.ms_host_fill_normal.restype = None
@@ -167,7 +171,8 @@ _lib.ms_sample_seed.restype = _U64
 _lib.ms_sample_seed.argtypes = [_U64, _I, _U64]
 
 EXPORTED = sorted(_SIGS) + ["ms_last_error", "ms_q4_packed_bytes", "ms_host_fill_random_u8",
-                            "ms_host_uniform", "ms_host_fill_normal", "ms_sample_seed"]
+                            "ms_host_fill_random_q4", "ms_host_uniform",
+                            "ms_host_fill_normal", "ms_sample_seed"]
 
 
 def lib():
@@ -231,9 +236,11 @@ def sample_seed(seed: int, seq: int, draw: int) -> int:
     return int(_lib.ms_sample_seed(int(seed) & 0xFFFFFFFFFFFFFFFF, int(seq), int(draw)))
 
 
-def host_random_u8(n: int, seed: int, stream: int) -> np.ndarray:
+def host_random_u8(n: int, seed: int, stream: int, balanced: bool = False) -> np.ndarray:
+    """Seeded bytes (identical to the device generator); balanced: every zero
+    nibble becomes 8 (zero-mean Q4 weights, ms_fill_random_q4)."""
     out = np.empty(n, dtype=np.uint8)
-    _lib.ms_host_fill_random_u8(out.ctypes.data, n, seed, stream)
+    _lib.ms_host_fill_random_q4(out.ctypes.data, n, seed, stream, 1 if balanced else 0)
     return out
 
 
@@ -365,8 +372,39 @@ def matrix_stream(layer: int, mat: int) -> int:
 LM_STREAM = 0xFFFF
 
 
-def matrix_scale(seed: int, layer: int, mat: int) -> float:
-    """Per-tensor scale U(0.04, 0.15) (create_fake_model.py:95)."""
+# Standard deviation of a balanced nibble minus the zero point: values 1..15
+# with 8 twice, sum (n - 8)^2 / 16 = 280 / 16.
+BALANCED_NIBBLE_STD = 17.5 ** 0.5
+
+
+# Gains of the balanced matrices: Q and K 1.0 (attention scores of unit
+# spread), V, O, Gate, Up, Down 0.65.
+BALANCED_GAINS = (1.0, 1.0, 0.65, 0.65, 0.65, 0.65, 0.65)
+
+
+def unit_gain_scale(seed: int, stream: int, K: int, gain: float = 1.0) -> float:
+    """Scale of a balanced synthetic matrix with K input rows:
+    gain * u / (std * sqrt(K)), u ~ U(0.8, 1.2), so a projection scales the
+    RMS of its input by about `gain`.
+    - With the reference's scale range on zero-mean weights the activations
+      grow to the hundreds, attention softmax turns into a near-argmax over
+      ties, and fp32 rounding decides which key wins: the model is chaotic and
+      no fp32 implementation tracks another.
+    - At gain 1 on every matrix a relative perturbation of 1e-6 still grows to
+      3e-4 over 42 layers, and the output follows the context, not the token.
+    - At 0.5 the network is near the identity and the tied head returns the
+      input token.
+    The gains of BALANCED_GAINS keep a 1e-6 perturbation near 2e-6 after 42
+    layers while the greedy id depends on the token and its context."""
+    u = host_uniform(seed, 0x6A1, stream, 0.8, 1.2)
+    return float(np.float32(gain * u / (BALANCED_NIBBLE_STD * float(K) ** 0.5)))
+
+
+def matrix_scale(seed: int, layer: int, mat: int, K: int = 0, balanced: bool = False) -> float:
+    """Per-tensor scale U(0.04, 0.15) (create_fake_model.py:95); balanced
+    matrices (K input rows) take unit_gain_scale instead."""
+    if balanced:
+        return unit_gain_scale(seed, matrix_stream(layer, mat), K, BALANCED_GAINS[mat])
     return host_uniform(seed, 0x5CA1E, matrix_stream(layer, mat), 0.04, 0.15)
 
 
@@ -375,17 +413,21 @@ def layer_ple(seed: int, layer: int) -> float:
     return host_uniform(seed, 0x91E, layer, 0.8, 1.2)
 
 
-def lm_scale(seed: int) -> float:
+def lm_scale(seed: int, D: int = 0, balanced: bool = False) -> float:
+    if balanced:
+        return unit_gain_scale(seed, LM_STREAM, D)
     return host_uniform(seed, 0x5CA1E, LM_STREAM, 0.04, 0.15)
 
 
-def host_matrix(seed: int, layer: int, mat: int, K: int, N: int) -> np.ndarray:
+def host_matrix(seed: int, layer: int, mat: int, K: int, N: int,
+                balanced: bool = False) -> np.ndarray:
     """Row-major Q4 bytes [K][N/2] of one synthetic matrix (host copy)."""
-    return host_random_u8(K * N // 2, seed, matrix_stream(layer, mat)).reshape(K, N // 2)
+    return host_random_u8(K * N // 2, seed, matrix_stream(layer, mat),
+                          balanced).reshape(K, N // 2)
 
 
-def host_lm_head(seed: int, D: int, vocab: int) -> np.ndarray:
-    return host_random_u8(D * vocab // 2, seed, LM_STREAM).reshape(D, vocab // 2)
+def host_lm_head(seed: int, D: int, vocab: int, balanced: bool = False) -> np.ndarray:
+    return host_random_u8(D * vocab // 2, seed, LM_STREAM, balanced).reshape(D, vocab // 2)
 
 
 class Model:
@@ -449,8 +491,9 @@ class Model:
             q4 = np.ascontiguousarray(q4, dtype=np.uint8)
             check(_lib.ms_model_set_lm_head(self.h, q4.ctypes.data, 0, scale, gp))
 
-    def fill_synthetic(self, seed: int) -> None:
-        """Seeded random Q4 weights generated on the device (no host copy)."""
+    def fill_synthetic(self, seed: int, balanced: bool = False) -> None:
+        """Seeded random Q4 weights generated on the device (no host copy);
+        balanced: zero-mean nibbles (ms_fill_random_q4) and unit-gain scales."""
         arch = self.arch
         biggest = max(max(k * n // 2 for k, n in arch.matrix_shapes(l))
                       for l in range(arch.n_layers))
@@ -460,27 +503,35 @@ class Model:
         try:
             for l in range(arch.n_layers):
                 for i, (K, N) in enumerate(arch.matrix_shapes(l)):
-                    check(_lib.ms_fill_random_u8(tmp.ptr, K * N // 2, seed,
-                                                 matrix_stream(l, i)))
-                    self.set_matrix_device(l, i, tmp.ptr, matrix_scale(seed, l, i))
+                    check(_lib.ms_fill_random_q4(tmp.ptr, K * N // 2, seed,
+                                                 matrix_stream(l, i), int(balanced)))
+                    self.set_matrix_device(l, i, tmp.ptr, matrix_scale(seed, l, i, K, balanced))
                 self.set_ple(l, layer_ple(seed, l))
             if arch.vocab:
-                check(_lib.ms_fill_random_u8(tmp.ptr, arch.hidden * arch.vocab // 2, seed,
-                                             LM_STREAM))
-                self.set_lm_head(None, lm_scale(seed), dptr=tmp.ptr)
+                check(_lib.ms_fill_random_q4(tmp.ptr, arch.hidden * arch.vocab // 2, seed,
+                                             LM_STREAM, int(balanced)))
+                self.set_lm_head(None, lm_scale(seed, arch.hidden, balanced), dptr=tmp.ptr)
             synchronize()
         finally:
             tmp.free()
 
-    def fill_synthetic_host(self, seed: int) -> None:
+    def fill_synthetic_host(self, seed: int, balanced: bool = False) -> None:
         """Same weights passed from host memory (streaming models)."""
         arch = self.arch
         for l in range(arch.n_layers):
             for i, (K, N) in enumerate(arch.matrix_shapes(l)):
-                self.set_matrix(l, i, host_matrix(seed, l, i, K, N), matrix_scale(seed, l, i))
+                self.set_matrix(l, i, host_matrix(seed, l, i, K, N, balanced),
+                                matrix_scale(seed, l, i, K, balanced))
             self.set_ple(l, layer_ple(seed, l))
         if arch.vocab:
-            self.set_lm_head(host_lm_head(seed, arch.hidden, arch.vocab), lm_scale(seed))
+            self.set_lm_head(host_lm_head(seed, arch.hidden, arch.vocab, balanced),
+                             lm_scale(seed, arch.hidden, balanced))
+
+    def set_taps(self, hidden: Optional["DeviceBuffer"], logits: Optional["DeviceBuffer"]) -> None:
+        """Per-layer output rows and raw logits of decode steps and of a prompt's
+        last row written to these device buffers (ms_model_set_taps)."""
+        check(_lib.ms_model_set_taps(self.h, hidden.ptr if hidden else None,
+                                     logits.ptr if logits else None))
 
     def reset(self) -> None:
         check(_lib.ms_model_reset(self.h))
@@ -552,10 +603,10 @@ class Model:
         check(_lib.ms_decode_run(self.h, n_steps, 1 if use_graph else 0, out.ctypes.data))
         return out
 
-    def prefill(self, tokens: Sequence[int], pos0: int = 0) -> int:
+    def prefill(self, tokens: Sequence[int], pos0: int = 0, seq: int = 0) -> int:
         t = np.asarray(tokens, dtype=np.int32)
         first = C.c_int32()
-        check(_lib.ms_prefill(self.h, 0, t.ctypes.data, len(t), pos0, C.byref(first)))
+        check(_lib.ms_prefill(self.h, seq, t.ctypes.data, len(t), pos0, C.byref(first)))
         return int(first.value)
 
     def stream_stats(self) -> dict:

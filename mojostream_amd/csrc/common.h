@@ -59,6 +59,13 @@ __host__ __device__ inline uint64_t rand_word(uint64_t seed, uint64_t stream,
                                               uint64_t i) {
   return mix64(mix64(seed ^ mix64(stream)) + i);
 }
+// Balanced Q4 bytes: every zero nibble of the word becomes 8, so a nibble is
+// 1..15 (8 twice as often) with mean 8, the zero point: zero-mean weights.
+__host__ __device__ inline uint64_t balance_q4_word(uint64_t r) {
+  uint64_t t = r | (r >> 1);
+  t |= t >> 2;  // bit 4i: OR of the four bits of nibble i
+  return r | ((~t & 0x1111111111111111ull) << 3);
+}
 
 // ---- Q4 panel layout ---------------------------------------------------------
 // A [K][N] Q4 matrix is stored as N/16 column panels of 16 columns; panel nb

@@ -138,6 +138,9 @@ struct ms_model {
   int32_t *samp_ids = nullptr;  // [max_seqs]
   int32_t *samp_ctr = nullptr;  // LM head calls that drew since set_sampling / reset
   std::vector<int> h_hist_n;    // host mirror of shist_n (ids in each history)
+  // taps (ms_model_set_taps): per-layer output rows and raw logits of every
+  // decode step and of a prompt's last row, for parity checks
+  float *tap_hidden = nullptr, *tap_logits = nullptr;
   // streaming
   uint8_t *slot[2] = {nullptr, nullptr};
   size_t slot_bytes = 0;
@@ -223,6 +226,7 @@ struct RunCfg {
   int seq0;                 // first sequence (caches / positions offset)
   int plan_pos;             // first row's position as the host knows it (B = 1);
                             // sizes the prefill attention's key split only
+  float *tap_last;          // optional [n_layers][D]: each layer's last output row
 };
 
 // Launch a projection of rows r: quantized in the kernel's prologue with
@@ -447,6 +451,16 @@ static int enqueue_pick(ms_model *m, const RunCfg &rc, int M, ArgmaxFin f, hipSt
   return launch_argmax_fin(f, st);
 }
 
+// Raw logits of the call's rows into the logits tap (before the sampler
+// rewrites them in place).
+static int tap_logits(ms_model *m, const RunCfg &rc, int M, hipStream_t st) {
+  if (!m->tap_logits) return MS_OK;
+  const size_t V = (size_t)m->d.vocab;
+  MS_HIP_TRY(hipMemcpyAsync(m->tap_logits, m->logits + (size_t)rc.seq0 * V, (size_t)M * V * 4,
+                            hipMemcpyDeviceToDevice, st));
+  return MS_OK;
+}
+
 // FP32 head: final norm (y rows), matmul_fp32_raw into the logits, then the pick.
 static int enqueue_lm_f32(ms_model *m, const RunCfg &rc, RowSrc r, int M, const ArgmaxFin &fin,
                           hipStream_t st) {
@@ -462,6 +476,7 @@ static int enqueue_lm_f32(ms_model *m, const RunCfg &rc, RowSrc r, int M, const 
   ArgmaxFin f = fin;
   f.M = M;
   ProfScope ps(PC_OTHER, 0.0, st);
+  if (int r2 = tap_logits(m, rc, M, st)) return r2;
   return enqueue_pick(m, rc, M, f, st);
 }
 
@@ -488,7 +503,7 @@ static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const Argm
   a.nseg = 1;
   a.P = 4;
   a.waves = 4;
-  a.out = m->sampling ? m->logits + (size_t)rc.seq0 * m->d.vocab : nullptr;
+  a.out = m->sampling ? m->logits + (size_t)rc.seq0 * m->d.vocab : m->tap_logits;
   a.ldo = m->d.vocab;
   a.arg_val = m->arg_val;
   a.arg_idx = m->arg_idx;
@@ -503,6 +518,8 @@ static int enqueue_lm(ms_model *m, const RunCfg &rc, int row0, int M, const Argm
   f.n_blocks = m->lm_blocks;
   f.M = M;
   ProfScope ps(PC_OTHER, 0.0, st);
+  if (m->sampling)
+    if (int r2 = tap_logits(m, rc, M, st)) return r2;
   // temperature_sampling (lm_head.mojo:198-254) on the logits rows, the
   // draws appended to the sequences' histories
   if (m->sampling) return enqueue_pick(m, rc, M, f, st);
@@ -532,6 +549,16 @@ static int stream_prefetch(ms_model *m, int l, int s, hipEvent_t a, hipEvent_t b
   return MS_OK;
 }
 
+// Copy of layer l's last output row into the prefill tap.
+static int tap_last_row(ms_model *m, const RunCfg &rc, int l, hipStream_t st) {
+  if (!rc.tap_last) return MS_OK;
+  const size_t D = (size_t)m->d.hidden;
+  MS_HIP_TRY(hipMemcpyAsync(rc.tap_last + (size_t)(l - rc.first_layer) * D,
+                            m->xs + (size_t)(rc.B * rc.T - 1) * D, D * 4,
+                            hipMemcpyDeviceToDevice, st));
+  return MS_OK;
+}
+
 static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
   const bool streaming = !m->d.resident;
   const int l0 = rc.first_layer, l1 = rc.first_layer + rc.n_layers;
@@ -556,6 +583,7 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
         // weights already in HBM; the copy stream moves on to the next
         // streamed layer while this one computes
         if (int r = enqueue_layer(m, l, rc, st)) return r;
+        if (int r = tap_last_row(m, rc, l, st)) return r;
         continue;
       }
       const int s = n_streamed++ & 1;
@@ -571,6 +599,7 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
       w1.push_back(e);
       for (int i = 0; i < 7; ++i) m->L[l].w[i] = m->slot[s] + m->L[l].off[i];
       if (int r = enqueue_layer(m, l, rc, st)) return r;
+      if (int r = tap_last_row(m, rc, l, st)) return r;
       MS_HIP_TRY(hipEventRecord(m->ev_free[s], st));
     }
     MS_HIP_TRY(hipStreamSynchronize(st));
@@ -593,8 +622,10 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
     m->stats.compute_ms = total - wait;
     return MS_OK;
   }
-  for (int l = l0; l < l1; ++l)
+  for (int l = l0; l < l1; ++l) {
     if (int r = enqueue_layer(m, l, rc, st)) return r;
+    if (int r = tap_last_row(m, rc, l, st)) return r;
+  }
   return MS_OK;
 }
 
@@ -728,6 +759,7 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   if ((rc = dmalloc(m, (void **)&m->qkv, (size_t)M * m->qkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_ctr, (size_t)d.max_seqs * m->nkv_max * 4)) ||
+
       (rc = dmalloc(m, (void **)&m->pos, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->tok, 64 * 4)) ||
       (rc = dmalloc(m, (void **)&m->step, 64 * 4)) ||
@@ -1069,6 +1101,7 @@ static int enqueue_decode_step(ms_model *m, int B, hipStream_t st) {
   rc.in_rows = m->x_in;
   rc.first_layer = 0;
   rc.n_layers = (int)m->L.size();
+  rc.hidden = m->tap_hidden;
   if (int r = run_layers(m, rc, st)) return r;
   ArgmaxFin f{};
   f.tok_state = m->tok;
@@ -1204,6 +1237,7 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
     rc.first_layer = 0;
     rc.n_layers = (int)m->L.size();
     rc.plan_pos = base;
+    if (c0 + t >= n_tokens) rc.tap_last = m->tap_hidden;
     if ((rcode = run_layers(m, rc, st))) break;
     if (c0 + t >= n_tokens) {
       // LM head on the last prompt row only
@@ -1220,6 +1254,18 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
   if (h_first_id) *h_first_id = id;
   m->h_pos[seq] = pos0 + n_tokens;
   if (m->sampling) m->h_hist_n[seq] = n_tokens + 1;
+  return MS_OK;
+}
+
+extern "C" int ms_model_set_taps(ms_model *m, float *d_hidden, float *d_logits) {
+  MS_CHECK_ARG(m, "set_taps: null model");
+  MS_CHECK_ARG(!d_logits || m->d.vocab > 0, "set_taps: logits need an LM head");
+  m->tap_hidden = d_hidden;
+  m->tap_logits = d_logits;
+  if (m->gexec) {  // the captured step holds the former targets
+    (void)hipGraphExecDestroy(m->gexec);
+    m->gexec = nullptr;
+  }
   return MS_OK;
 }
 
@@ -1253,7 +1299,7 @@ extern "C" int ms_prof_get(int cls, const char **name, long *launches, double *t
 extern "C" int ms_prof_sweep(ms_model *m, int cls, int passes, double *avg_us,
                              double *bytes_per_launch, long *launches) {
   if (int rc = require_init()) return rc;
-  MS_CHECK_ARG(m && avg_us && passes >= 1, "prof_sweep: bad arguments");
+  MS_CHECK_ARG(m && avg_us && passes != 0, "prof_sweep: bad arguments");
   MS_CHECK_ARG(cls == PC_QKV || cls == PC_O || cls == PC_GATEUP || cls == PC_DOWN,
                "prof_sweep: class must be a layer projection");
   MS_CHECK_ARG(g_prof.have[cls], "prof_sweep: no launch of this class recorded while profiling");
@@ -1269,6 +1315,10 @@ extern "C" int ms_prof_sweep(ms_model *m, int cls, int passes, double *avg_us,
                       (d.q_dim == d0.q_dim && d.kv_dim == d0.kv_dim);
     if (same) layers.push_back(l);
   }
+  // passes < 0: the recorded layer only, -passes times (its weights stay in
+  // the caches after the first launch: the cache-hot duration)
+  if (passes < 0) layers.assign(-passes, g_prof.last_layer[cls]);
+  if (passes < 0) passes = 1;
   hipStream_t st = ctx().stream;
   hipEvent_t e0, e1;
   MS_HIP_TRY(hipEventCreate(&e0));

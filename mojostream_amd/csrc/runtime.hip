@@ -38,11 +38,13 @@ int scratch(size_t bytes, void **out) {
   return MS_OK;
 }
 
-__global__ void k_fill_random(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream) {
+__global__ void k_fill_random(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream,
+                              int balanced) {
   const size_t w = (size_t)blockIdx.x * kBlock + threadIdx.x;
   const size_t i0 = w * 8;
   if (i0 >= n) return;
-  const uint64_t r = rand_word(seed, stream, w);
+  uint64_t r = rand_word(seed, stream, w);
+  if (balanced) r = balance_q4_word(r);
   if (i0 + 8 <= n && ((reinterpret_cast<uintptr_t>(dst) & 7) == 0)) {
     *reinterpret_cast<uint64_t *>(dst + i0) = r;
   } else {
@@ -163,20 +165,26 @@ extern "C" int ms_host_free(void *h_ptr) {
   return MS_OK;
 }
 
-extern "C" int ms_fill_random_u8(uint8_t *d_dst, size_t n, uint64_t seed, uint64_t stream) {
+extern "C" int ms_fill_random_q4(uint8_t *d_dst, size_t n, uint64_t seed, uint64_t stream,
+                                 int balanced) {
   if (int rc = require_init()) return rc;
   const size_t words = (n + 7) / 8;
   hipLaunchKernelGGL(k_fill_random, dim3(cdiv((long)words, kBlock)), dim3(kBlock), 0,
-                     g_ctx.stream, d_dst, n, seed, stream);
+                     g_ctx.stream, d_dst, n, seed, stream, balanced ? 1 : 0);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }
 
-extern "C" void ms_host_fill_random_u8(uint8_t *h_dst, size_t n, uint64_t seed,
-                                       uint64_t stream) {
+extern "C" int ms_fill_random_u8(uint8_t *d_dst, size_t n, uint64_t seed, uint64_t stream) {
+  return ms_fill_random_q4(d_dst, n, seed, stream, 0);
+}
+
+extern "C" void ms_host_fill_random_q4(uint8_t *h_dst, size_t n, uint64_t seed,
+                                       uint64_t stream, int balanced) {
   const size_t words = (n + 7) / 8;
   for (size_t w = 0; w < words; ++w) {
-    const uint64_t r = rand_word(seed, stream, w);
+    uint64_t r = rand_word(seed, stream, w);
+    if (balanced) r = balance_q4_word(r);
     const size_t i0 = w * 8;
     if (i0 + 8 <= n) {
       std::memcpy(h_dst + i0, &r, 8);  // little-endian host, same as the device
@@ -184,6 +192,11 @@ extern "C" void ms_host_fill_random_u8(uint8_t *h_dst, size_t n, uint64_t seed,
       for (int b = 0; b < 8 && i0 + b < n; ++b) h_dst[i0 + b] = (uint8_t)(r >> (8 * b));
     }
   }
+}
+
+extern "C" void ms_host_fill_random_u8(uint8_t *h_dst, size_t n, uint64_t seed,
+                                       uint64_t stream) {
+  ms_host_fill_random_q4(h_dst, n, seed, stream, 0);
 }
 
 extern "C" float ms_host_uniform(uint64_t seed, uint64_t stream, uint64_t index, float lo,

@@ -253,19 +253,53 @@ class OracleModel:
         x = self.o.rmsnorm(x_final.reshape(1, -1), self.gamma)
         return self.o.lm_head(x, self.lm_w, self.arch.vocab, self.lm_scale)[0]
 
+    def logits_rows(self, x_final: np.ndarray) -> np.ndarray:
+        """Final norm + LM head of many rows [T][D] -> [T][vocab]
+        (apply_final_norm + project_lm_head, lm_head.mojo:119-168)."""
+        x = self.o.rmsnorm(np.ascontiguousarray(x_final, np.float32), self.gamma)
+        return self.o.lm_head(x, self.lm_w, self.arch.vocab, self.lm_scale)
 
-def synthetic_oracle_model(oracle: Oracle, arch, seed: int, with_lm: bool = True):
+    def embed_rows(self, tokens: Sequence[int]) -> np.ndarray:
+        """Embedding rows of tokens (get_token_embedding, lm_head.mojo:186-195)."""
+        return np.stack([self.o.embed(self.lm_w, self.D, self.arch.vocab, self.lm_scale, int(t))
+                         for t in tokens])
+
+    def forward_keep(self, x: np.ndarray, base: int, keep: Sequence[int]):
+        """All layers over rows x [T][D] at positions base..base+T-1 (one causal
+        call per layer); returns the last layer's rows and each layer's output
+        for the rows `keep` ([n_layers][len(keep)][D])."""
+        keep = list(keep)
+        hs = np.empty((self.arch.n_layers, len(keep), self.D), np.float32)
+        for l in range(self.arch.n_layers):
+            x = self.layer_forward(l, x, base)
+            hs[l] = x[keep]
+        return x, hs
+
+
+class HostWeights:
+    """Seeded synthetic weights generated once on the host and shared by any
+    number of OracleModels (each with its own KV caches)."""
+
+    def __init__(self, arch, seed: int, balanced: bool = False, with_lm: bool = True):
+        import mojostream_amd as ms
+        self.arch = arch
+        self.weights, self.scales, self.ples = [], [], []
+        for l in range(arch.n_layers):
+            self.weights.append([ms.host_matrix(seed, l, i, K, N, balanced)
+                                 for i, (K, N) in enumerate(arch.matrix_shapes(l))])
+            self.scales.append([ms.matrix_scale(seed, l, i, K, balanced)
+                                for i, (K, N) in enumerate(arch.matrix_shapes(l))])
+            self.ples.append(ms.layer_ple(seed, l))
+        self.lm = (ms.host_lm_head(seed, arch.hidden, arch.vocab, balanced)
+                   if (with_lm and arch.vocab) else None)
+        self.lm_scale = ms.lm_scale(seed, arch.hidden, balanced) if self.lm is not None else 0.0
+
+    def model(self, oracle: Oracle) -> OracleModel:
+        return OracleModel(oracle, self.arch, self.weights, self.scales, self.ples, self.lm,
+                           self.lm_scale)
+
+
+def synthetic_oracle_model(oracle: Oracle, arch, seed: int, with_lm: bool = True,
+                           balanced: bool = False):
     """The same seeded weights the device generator produces (host copies)."""
-    import mojostream_amd as ms
-    weights, scales, ples = [], [], []
-    for l in range(arch.n_layers):
-        ws, ss = [], []
-        for i, (K, N) in enumerate(arch.matrix_shapes(l)):
-            ws.append(ms.host_matrix(seed, l, i, K, N))
-            ss.append(ms.matrix_scale(seed, l, i))
-        weights.append(ws)
-        scales.append(ss)
-        ples.append(ms.layer_ple(seed, l))
-    lm = ms.host_lm_head(seed, arch.hidden, arch.vocab) if (with_lm and arch.vocab) else None
-    return OracleModel(oracle, arch, weights, scales, ples, lm,
-                       ms.lm_scale(seed) if lm is not None else 0.0)
+    return HostWeights(arch, seed, balanced, with_lm).model(oracle)

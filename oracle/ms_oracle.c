@@ -116,7 +116,7 @@ void or_matmul_q4(float *C, const float *A, const uint8_t *wq, int M, int K,
   /* parallelize over BM=64-row blocks (kernels.mojo:212,266): decode shapes
    * (M <= 64) are one work item, i.e. single-threaded, as here by default. */
   int nt = g_threads;
-  if (nt > 1 && N >= nt * NR * 4) {
+  if (nt > 1 && N >= nt * NR) {
     pthread_t th[64];
     mm_job jobs[64];
     const int tiles = (N + NR - 1) / NR;
@@ -241,15 +241,26 @@ void or_kv_write(const or_layer *L, const float *knew, const float *vnew,
   }
 }
 
-/* ---- a10/a11: attention ---- */
-void or_attention(const or_layer *L, const float *q, const float *knew,
-                  const float *vnew, int T, int base, int mode, float *out) {
+/* ---- a10/a11: attention ----
+ * Rows are independent given the cache and the fresh K/V, so the checker may
+ * split them over threads (or_set_threads); each row's arithmetic is the same
+ * for any split. */
+typedef struct {
+  const or_layer *L;
+  const float *q, *knew, *vnew;
+  int r0, r1, base, mode;
+  float *out;
+} attn_job;
+
+static void attention_rows(const or_layer *L, const float *q, const float *knew,
+                           const float *vnew, int r0, int r1, int base, int mode,
+                           float *out) {
   const int hd = L->head_dim, kvd = L->kv_dim, qd = L->q_dim;
   const int ratio = L->n_heads / L->n_kv_heads;
   const float scale = 1.0f / sqrtf((float)hd);
-  int max_keys = base + T;
+  int max_keys = base + r1;
   float *sp = (float *)malloc(sizeof(float) * (size_t)(max_keys > 0 ? max_keys : 1));
-  for (int r = 0; r < T; ++r) {
+  for (int r = r0; r < r1; ++r) {
     const int p = base + r;
     int k0, k1; /* attended absolute positions [k0, k1) */
     if (L->cache_kind == OR_CACHE_CIRCULAR) {
@@ -273,12 +284,18 @@ void or_attention(const or_layer *L, const float *q, const float *knew,
           kh = knew + (size_t)(t - base) * kvd + (size_t)hkv * hd;
         else
           kh = L->kc + (size_t)cache_slot(L, t) * kvd + (size_t)hkv * hd;
-        float lanes[SIMD_W] = {0};
+        /* SIMD_W-lane partial sums (lane l takes dims j + l), then reduce_add */
+        v8f lanes = {0, 0, 0, 0, 0, 0, 0, 0};
         int j = 0;
-        for (; j + SIMD_W <= hd; j += SIMD_W)
-          for (int l = 0; l < SIMD_W; ++l)
-            lanes[l] = lanes[l] + qh[j + l] * kh[j + l];
-        float s = reduce_add8(lanes) * scale;
+        for (; j + SIMD_W <= hd; j += SIMD_W) {
+          v8f qv, kv;
+          memcpy(&qv, qh + j, sizeof qv);
+          memcpy(&kv, kh + j, sizeof kv);
+          lanes = lanes + qv * kv;
+        }
+        float l8[SIMD_W];
+        memcpy(l8, &lanes, sizeof l8);
+        float s = reduce_add8(l8) * scale;
         for (; j < hd; ++j) s = s + qh[j] * kh[j] * scale;
         sp[n] = s;
       }
@@ -308,6 +325,44 @@ void or_attention(const or_layer *L, const float *q, const float *knew,
     }
   }
   free(sp);
+}
+
+static void *attn_worker(void *p) {
+  attn_job *j = (attn_job *)p;
+  attention_rows(j->L, j->q, j->knew, j->vnew, j->r0, j->r1, j->base, j->mode, j->out);
+  return NULL;
+}
+
+void or_attention(const or_layer *L, const float *q, const float *knew,
+                  const float *vnew, int T, int base, int mode, float *out) {
+  int nt = g_threads < T ? g_threads : T;
+  if (nt > 1 && T >= 8) {
+    pthread_t th[64];
+    attn_job jobs[64];
+    /* causal rows attend to more keys the later they are: cut the rows into
+     * ranges of about equal key counts */
+    double total = 0;
+    for (int r = 0; r < T; ++r) {
+      const int p = base + r + 1;
+      total += (L->cache_kind == OR_CACHE_CIRCULAR && p > L->cache_len) ? L->cache_len : p;
+    }
+    int r = 0;
+    double acc = 0;
+    for (int t = 0; t < nt; ++t) {
+      const int r0 = r;
+      const double goal = total * (t + 1) / nt;
+      while (r < T && (acc < goal || t == nt - 1)) {
+        const int p = base + r + 1;
+        acc += (L->cache_kind == OR_CACHE_CIRCULAR && p > L->cache_len) ? L->cache_len : p;
+        ++r;
+      }
+      jobs[t] = (attn_job){L, q, knew, vnew, r0, r, base, mode, out};
+      pthread_create(&th[t], NULL, attn_worker, &jobs[t]);
+    }
+    for (int t = 0; t < nt; ++t) pthread_join(th[t], NULL);
+    return;
+  }
+  attention_rows(L, q, knew, vnew, 0, T, base, mode, out);
 }
 
 /* ---- a12: one layer (gemma4_e4b.mojo:459-540; main.mojo:538-613) ---- */

@@ -395,3 +395,78 @@ def test_q4_quantize_tiny_block_rule(oracle):
     assert s == np.float32(float(np.float32(3e-8)) / 7.0)
     _, s = oracle.q4_quantize(np.zeros((4, 4), np.float32))
     assert s == np.float32(1e-8)
+
+
+# ---- whole-model token step and the checker's threading ------------------------------
+def _small_model(o, n_layers=3, D=128, F=256, V=512, seed=5):
+    """A 3-layer model mixing a circular window (6 slots), a linear cache with
+    partial RoPE and GQA 2:1, and its tied Q4 head."""
+    rng = np.random.default_rng(seed)
+    descs = []
+    for l in range(n_layers):
+        if l % 2 == 0:
+            descs.append(_Desc(q_dim=128, kv_dim=64, head_dim=32, n_heads=4, n_kv_heads=2,
+                               rot_dim=32, theta=1e4, cache_kind=OR_CACHE_CIRCULAR,
+                               cache_len=6, clamp_reads=0))
+        else:
+            descs.append(_Desc(q_dim=128, kv_dim=64, head_dim=32, n_heads=4, n_kv_heads=2,
+                               rot_dim=8, theta=1e6, cache_kind=OR_CACHE_LINEAR,
+                               cache_len=64, clamp_reads=1))
+    ws, sc, ples = [], [], []
+    for d in descs:
+        shapes = [(D, d.q_dim), (D, d.kv_dim), (D, d.kv_dim), (d.q_dim, D), (D, F), (D, F),
+                  (F, D)]
+        ws.append([rng.integers(0, 256, size=(k, n // 2), dtype=np.uint8) for k, n in shapes])
+        sc.append([float(np.float32(rng.uniform(0.04, 0.15))) for _ in range(7)])
+        ples.append(float(np.float32(rng.uniform(0.8, 1.2))))
+    lm = rng.integers(0, 256, size=(D, V // 2), dtype=np.uint8)
+    lm_scale = float(np.float32(0.08))
+    gamma = rng.uniform(0.5, 1.5, D).astype(np.float32)
+
+    class A:
+        hidden, ffn, vocab = D, F, V
+        layers = descs
+    A.n_layers = n_layers
+    om = OracleModel(o, A, ws, sc, ples, lm, lm_scale, gamma)
+    refs = [RefLayer(d, D, F, w, s, p) for d, w, s, p in zip(descs, ws, sc, ples)]
+    return om, refs, lm, lm_scale, gamma
+
+
+def test_decode_token_vs_f64_model(oracle):
+    """or_decode_token (embedding column -> layers -> final norm with gamma ->
+    logits -> first maximum) against the independent f64 layers and head, over
+    10 positions so the 6-slot window wraps."""
+    om, refs, lm, lm_scale, gamma = _small_model(oracle)
+    D = om.D
+    W = deq(lm, lm_scale)
+    tok = 7
+    for pos in range(10):
+        tid, hid = om.decode_token(tok, pos, hidden=True)
+        x = W[:, tok][None, :]
+        for l, ref in enumerate(refs):
+            x = ref.forward(x, pos)
+            assert rel_rmse(hid[l], x[0]) < 1e-5, (pos, l)
+        lg = lm_logits(x, lm, lm_scale, gamma.astype(np.float64))[0]
+        order = np.argsort(lg)[::-1]
+        # the f64 argmax, unless the top two are closer than fp32 rounding
+        if lg[order[0]] - lg[order[1]] > 1e-4 * np.abs(lg).max():
+            assert tid == int(order[0]), (pos, tid, int(order[0]))
+        tok = tid
+
+
+def test_threaded_checker_is_bit_identical(oracle):
+    """The checker's thread split (columns of a matmul, rows of attention)
+    keeps every element's summation order."""
+    # one loaded library: the thread count is switched between the two runs
+    try:
+        outs = []
+        for n in (1, 8):
+            oracle.set_threads(n)
+            om, _, _, _, _ = _small_model(oracle)
+            x = np.random.default_rng(3).standard_normal((40, om.D)).astype(np.float32)
+            y = om.forward(x[:24], 0)           # 24 rows: wraps the 6-slot window
+            z = om.forward(x[24:], 24)
+            outs.append((y, z))
+        assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    finally:
+        oracle.set_threads(1)
