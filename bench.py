@@ -163,6 +163,77 @@ def measure_ttft(ms, prompts, seed):
     return ttft
 
 
+def host_link_gbps(ms, nbytes=1 << 30):
+    """Pinned host -> HBM copy rate of one large copy (the streaming bound)."""
+    import ctypes as C
+    h = C.c_void_p()
+    ms.check(ms.lib().ms_host_alloc(C.byref(h), nbytes))
+    d = ms.DeviceBuffer(nbytes)
+    try:
+        ms.check(ms.lib().ms_memcpy_h2d(d.ptr, h.value, nbytes))  # warm-up
+        best = 1e30
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ms.check(ms.lib().ms_memcpy_h2d(d.ptr, h.value, nbytes))
+            best = min(best, time.perf_counter() - t0)
+    finally:
+        d.free()
+        ms.lib().ms_host_free(h.value)
+    return nbytes / best / 1e9
+
+
+def bench_c5(ms, seed, steps, prompt_len):
+    """14B-class streaming decode (config 5): 48 layers of 6.6 GB Q4 weights in
+    pinned host memory, streamed layer by layer into two HBM slots on the copy
+    stream (StreamingRunner semantics, stream_runner.mojo:460-562); tied Q4
+    head (vocab 262144) resident.  A seeded prompt of prompt_len ids, then
+    `steps` greedy steps; per step the copy time (io), the time compute waited
+    for a copy (wait) and the rest (compute), as run_streaming_bench reports
+    them (:503-546)."""
+    import numpy as np
+    arch = ms.arch_14b(max_len=prompt_len + steps + 8)
+    m = ms.Model(arch, max_seqs=1, max_rows=4, max_pos=prompt_len + steps + 8, resident=False)
+    t0 = time.perf_counter()
+    m.fill_synthetic(seed)
+    log(f"c5: 14B weights generated into pinned memory in {time.perf_counter() - t0:.1f}s")
+    link = host_link_gbps(ms)
+    log(f"c5: pinned host -> HBM copy {link:.1f} GB/s")
+    prompt = [int(v % arch.vocab) for v in ms.host_random_u8(4 * prompt_len, 9, 50).view(np.uint32)]
+    ms.synchronize()
+    t0 = time.perf_counter()
+    tok = m.prefill(prompt, 0)
+    ttft = (time.perf_counter() - t0) * 1e3
+    log(f"c5: prefill of {prompt_len} tokens {ttft:.0f} ms")
+    io = wait = total = 0.0
+    t0 = time.perf_counter()
+    for k in range(steps):
+        out = (m.decode([tok], [prompt_len], 1, use_graph=False) if k == 0
+               else m.decode_continue(1, 1, use_graph=False))
+        tok = int(out[0, 0])
+        st = m.stream_stats()
+        io += st["io_ms"]
+        wait += st["wait_ms"]
+        total += st["total_ms"]
+        if (k + 1) % 32 == 0:
+            log(f"c5: step {k + 1}/{steps}: {total / (k + 1):.1f} ms/step, io {io / (k + 1):.1f} ms")
+    dt = time.perf_counter() - t0
+    layer_bytes = arch.weight_bytes()
+    m.close()
+    ms_step = dt * 1e3 / steps
+    return {"workload": "14B-class streaming decode: D=5120, 48 layers, 40q/8kv heads, hd 128, "
+                        "FFN 13824, all full attention; layers streamed from pinned host memory "
+                        "through 2 HBM slots; tied Q4 head resident",
+            "prompt_tokens": prompt_len, "decode_steps": steps, "context_end": prompt_len + steps,
+            "tokens_per_s": round(1e3 / ms_step, 3), "ms_per_token": round(ms_step, 2),
+            "io_ms_per_token": round(io / steps, 2), "wait_ms_per_token": round(wait / steps, 2),
+            "compute_ms_per_token": round((total - wait) / steps, 2),
+            "streamed_bytes_per_token": layer_bytes,
+            "stream_gbps": round(layer_bytes / (io / steps * 1e-3) / 1e9, 1),
+            "host_link_gbps_measured": round(link, 1),
+            "stream_frac_of_link": round(layer_bytes / (io / steps * 1e-3) / 1e9 / link, 3),
+            "prefill_ms": round(ttft, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -173,8 +244,9 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time the decode with eager launches")
-    ap.add_argument("--only", choices=["all", "decode", "ttft"], default="all",
-                    help="decode: batch-1 decode only; ttft: prefill (TTFT) only")
+    ap.add_argument("--only", choices=["all", "decode", "ttft", "c5"], default="all",
+                    help="decode: batch-1 decode only; ttft: prefill (TTFT) only; c5: the 14B "
+                         "streaming section only")
     ap.add_argument("--prof-tokens", type=int, default=16)
     ap.add_argument("--rocpd-summary", metavar="DB", help="summarize a rocprofv3 database and exit")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -182,6 +254,9 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="HBM traffic of the Gate|Up GEMV from two --pmc runs and exit")
     ap.add_argument("--seed", type=int, default=42)
+    ap.add_argument("--c5-steps", type=int, default=256,
+                    help="decode steps of the 14B streaming section (0: skip it)")
+    ap.add_argument("--c5-prompt", type=int, default=3840)
     args = ap.parse_args()
     if args.rocpd_summary:
         print(rocpd_summary(args.rocpd_summary, args.steps))
@@ -206,6 +281,10 @@ def main():
     ms.init(0)
     name, ncu, hbm = ms.device_info()
     log(f"device {name} CUs={ncu}")
+    if args.only == "c5":
+        print(json.dumps({"c5_streaming_14b": bench_c5(ms, args.seed, args.c5_steps,
+                                                         args.c5_prompt), "device": name}))
+        return
     if args.only == "ttft":
         ttft = measure_ttft(ms, sorted({args.ttft_prompt, 2048}), args.seed)
         print(json.dumps({"ttft_ms": {str(k): round(v, 2) for k, v in ttft.items()},
@@ -310,6 +389,8 @@ def main():
 
         ttft = measure_ttft(ms, sorted({args.ttft_prompt, 2048}), args.seed)
         out["ttft_ms"] = {str(k): round(v, 2) for k, v in ttft.items()}
+        if args.c5_steps > 0:
+            out["c5_streaming_14b"] = bench_c5(ms, args.seed, args.c5_steps, args.c5_prompt)
     else:
         m.close()
 

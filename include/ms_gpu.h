@@ -259,8 +259,8 @@ int ms_model_destroy(ms_model *m);
 /* Binds one of the 7 matrices (0 Q,1 K,2 V,3 O,4 Gate,5 Up,6 Down -- the
  * .mojostream type tag minus one, mojostream.mojo:21-28) of a layer.
  * `src` is row-major reference Q4, on the device if src_on_device else host.
- * Resident models pack it into HBM; streaming models take host memory and
- * keep a packed copy in pinned host memory.
+ * Resident models pack it into HBM; streaming models keep a packed copy in
+ * pinned host memory (packed on the device when src is there).
  * Replaces load_weights_from_ms (harness.mojo:80-122) and
  * get_layer_ref (sparse_pin.mojo:295-330). */
 int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_t *src,
@@ -334,6 +334,13 @@ int ms_model_set_bos(ms_model *m, const float *h_bos);
  * sequence; prefill: the last prompt row).  Each call overwrites the taps.
  * NULL switches a tap off. */
 int ms_model_set_taps(ms_model *m, float *d_hidden, float *d_logits);
+/* Rows of positions pos0..pos0+n-1 of a layer's KV cache for one sequence
+ * (K after RoPE, V), into d_k / d_v [n][kv_dim] (either may be NULL).  A
+ * circular cache holds position p in slot p % window (write_kv_sliding
+ * gemma4_e4b.mojo:211-228), so n is at most the window and only the last
+ * window positions are meaningful.  No reference counterpart (the reference's
+ * caches are host Lists its tests read directly). */
+int ms_model_read_kv(ms_model *m, int layer, int seq, int pos0, int n, float *d_k, float *d_v);
 
 /* ---- .mojostream weight files (host side) -------------------------------- */
 /* MojoStreamMeta (mojostream.mojo:47-69) plus the fields the reference parses
@@ -394,6 +401,31 @@ int ms_file_tensor_guard(const ms_file *f);
  * for the same seed. */
 int ms_file_write_synthetic(const char *path, const ms_file_meta *hdr,
                             const uint8_t *is_full, uint64_t seed);
+/* compute_dir_checksum (src/tests/validate_real.mojo:78-83): XOR of the
+ * 32-bit words at byte 16 of every directory entry (the scale fields). */
+int ms_file_dir_checksum(const ms_file *f, uint32_t *out);
+/* Structural validation of a converted file, run_validation
+ * (src/tests/validate_real.mojo:110-260): magic, architecture fields, Engram
+ * extension, n_tensors == n_layers * 8, directory offsets inside the file,
+ * non-zero directory checksum, and spot checks of the Q and Gate tensors of
+ * layers 0, 20 and 41 (first 64 bytes not all 0x00 nor all 0xFF).  Like the
+ * reference it reports rather than fails: MS_OK with the counts, a bit per
+ * failed check and the first failure's text. */
+#define MS_VALIDATE_MAGIC 0
+#define MS_VALIDATE_ARCH 1
+#define MS_VALIDATE_ENGRAM 2
+#define MS_VALIDATE_TENSORS 3
+#define MS_VALIDATE_OFFSETS 4
+#define MS_VALIDATE_CHECKSUM 5
+#define MS_VALIDATE_SPOT 6 /* bits 6..11: layer 0 Q, Gate; layer 20 Q, Gate; 41 Q, Gate */
+typedef struct {
+  int passed, n_checks, n_failed;
+  uint32_t failed_mask;
+  uint32_t dir_checksum;
+  uint64_t file_bytes;
+  char message[256];
+} ms_file_validation;
+int ms_file_validate(const ms_file *f, ms_file_validation *out);
 /* Runs both guards, checks the model's shapes against the file and binds
  * every matrix and PLE scale (the load loops of run_harness
  * harness.mojo:80-122 and StreamingRunner stream_runner.mojo:188-270). */

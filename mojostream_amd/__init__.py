@@ -72,6 +72,14 @@ class FileEntry(C.Structure):
                 ("data_offset", C.c_uint64)]
 
 
+class FileValidation(C.Structure):
+    """ms_file_validation: the structural checks of run_validation
+    (src/tests/validate_real.mojo:110-260)."""
+    _fields_ = [("passed", C.c_int), ("n_checks", C.c_int), ("n_failed", C.c_int),
+                ("failed_mask", C.c_uint32), ("dir_checksum", C.c_uint32),
+                ("file_bytes", C.c_uint64), ("message", C.c_char * 256)]
+
+
 class FileLayer(C.Structure):
     _fields_ = [("is_full", C.c_int), ("head_dim", C.c_int), ("q_dim", C.c_int),
                 ("kv_dim", C.c_int)]
@@ -121,6 +129,7 @@ _SIGS = {
     "ms_model_set_sampling": [_P, _F, _F, _U64],
     "ms_model_set_pinned": [_P, _P],
     "ms_model_set_taps": [_P, _P, _P],
+    "ms_model_read_kv": [_P, _I, _I, _I, _I, _P, _P],
     "ms_file_open": [C.c_char_p, C.POINTER(C.c_void_p)], "ms_file_close": [_P],
     "ms_file_get_meta": [_P, C.POINTER(FileMeta)],
     "ms_file_get_entry": [_P, _I, C.POINTER(FileEntry)],
@@ -130,6 +139,8 @@ _SIGS = {
                        C.POINTER(C.c_size_t)],
     "ms_file_ple_scale": [_P, _I, C.POINTER(C.c_float)],
     "ms_file_shape_guard": [_P], "ms_file_tensor_guard": [_P],
+    "ms_file_dir_checksum": [_P, C.POINTER(C.c_uint32)],
+    "ms_file_validate": [_P, C.POINTER(FileValidation)],
     "ms_file_write_synthetic": [C.c_char_p, C.POINTER(FileMeta), _P, _U64],
     "ms_model_load_file": [_P, _P],
     "ms_model_load_lm_head_file": [_P, C.c_char_p],
@@ -358,10 +369,13 @@ def arch_e4b(max_full_seq: int = 4096, n_layers: int = 42, vocab: int = 262144) 
                 vocab)
 
 
-def arch_14b(max_len: int = 4096, n_layers: int = 48) -> Arch:
-    """14B-class: D=5120, 40q/8kv heads, hd 128, F=13824, theta 1e6."""
+def arch_14b(max_len: int = 4096, n_layers: int = 48, vocab: int = 262144) -> Arch:
+    """14B-class: D=5120, 40q/8kv heads, hd 128, F=13824, theta 1e6, all full
+    attention; a tied Q4 head of `vocab` ids (0: none).  The layers hold
+    6,606,028,800 bytes of Q4 weights, the head 671,088,640 at vocab 262144:
+    7.28 GB in all, the "about 7.5 GB" of the 14B configuration."""
     return Arch("14b", 5120, 13824,
-                [demo_layer(5120, 40, 8, max_len, theta=1e6) for _ in range(n_layers)])
+                [demo_layer(5120, 40, 8, max_len, theta=1e6) for _ in range(n_layers)], vocab)
 
 
 # ---- synthetic model (seeded) ------------------------------------------------------
@@ -526,6 +540,14 @@ class Model:
         if arch.vocab:
             self.set_lm_head(host_lm_head(seed, arch.hidden, arch.vocab, balanced),
                              lm_scale(seed, arch.hidden, balanced))
+
+    def read_kv(self, layer: int, seq: int, pos0: int, n: int):
+        """K and V rows of positions pos0..pos0+n-1 of a layer's cache (host
+        arrays [n][kv_dim])."""
+        kvd = self.arch.layers[layer].kv_dim
+        dk, dv = DeviceBuffer(max(n, 1) * kvd * 4), DeviceBuffer(max(n, 1) * kvd * 4)
+        check(_lib.ms_model_read_kv(self.h, layer, seq, pos0, n, dk.ptr, dv.ptr))
+        return dk.download(np.float32, (n, kvd)), dv.download(np.float32, (n, kvd))
 
     def set_taps(self, hidden: Optional["DeviceBuffer"], logits: Optional["DeviceBuffer"]) -> None:
         """Per-layer output rows and raw logits of decode steps and of a prompt's

@@ -6,6 +6,9 @@
   python -m mojostream_amd bench_q4
   python -m mojostream_amd e4b-infer  [FILE LM_HEAD] [--tokens N] [--stream]
   python -m mojostream_amd fake-model OUT [--e4b] [--layers N] [--seed S]
+  python -m mojostream_amd validate   [FILE [LAYER0_REF]]     (validate.mojo)
+  python -m mojostream_amd validate-real [FILE [LAYER0_REF]]  (validate_real.mojo)
+  python -m mojostream_amd tensorguard [FILE]  (src/tests/validate_real.mojo)
 """
 import argparse
 import sys
@@ -36,6 +39,14 @@ def main(argv=None) -> int:
     e.add_argument("--penalty", type=float, default=1.2,
                    help="repetition penalty, the reference's 1.2")
     e.add_argument("--sample-seed", type=int, default=0, help="seed of the draws")
+    v = sub.add_parser("validate", help="layer 0 against a layer0_ref.bin (REFB)")
+    v.add_argument("file", nargs="?", default="model.mojostream")
+    v.add_argument("ref", nargs="?", default="layer0_ref.bin")
+    vr = sub.add_parser("validate-real", help="guards, NaN/Inf scan, optional REFB compare")
+    vr.add_argument("file", nargs="?", default="model_converted.mojostream")
+    vr.add_argument("ref", nargs="?", default="layer0_ref.bin")
+    tg = sub.add_parser("tensorguard", help="structural checks and directory checksum")
+    tg.add_argument("file", nargs="?", default="models/gemma4_e4b_q4.mojostream")
     g = sub.add_parser("fake-model", help="write a seeded synthetic .mojostream file")
     g.add_argument("out")
     g.add_argument("--e4b", action="store_true", help="E4B shapes (default: demo shapes)")
@@ -61,6 +72,16 @@ def main(argv=None) -> int:
         drivers.run_e4b_infer(a.file, a.lm_head, n_stream=a.tokens, resident=not a.stream,
                               temperature=a.temperature, penalty=a.penalty,
                               sample_seed=a.sample_seed)
+    elif a.cmd == "validate":
+        from . import validate
+        return 0 if validate.run_validation(a.file, a.ref)["passed"] else 1
+    elif a.cmd == "validate-real":
+        from . import validate
+        r = validate.run_real_validation(a.file, a.ref)
+        return 0 if r["stable"] and r.get("ref_passed", True) else 1
+    elif a.cmd == "tensorguard":
+        from . import validate
+        return 0 if validate.tensorguard_report(a.file)["passed"] else 1
     elif a.cmd == "fake-model":
         if a.e4b:
             streaming.write_synthetic_e4b(a.out, a.layers or 42, a.seed)

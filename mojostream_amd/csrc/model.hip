@@ -855,12 +855,25 @@ extern "C" int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_
     }
     if (rc) return rc;
   } else {
-    MS_CHECK_ARG(!src_on_device, "set_matrix: streaming models take host weights");
     if (!Ly.h_packed[mat])
       if (hipHostMalloc((void **)&Ly.h_packed[mat], Ly.bytes[mat], hipHostMallocDefault) !=
           hipSuccess)
         return fail(MS_E_NOMEM, "set_matrix: pinned allocation failed");
-    if (int rc = ms_host_q4_pack(Ly.h_packed[mat], src, K[mat], N[mat])) return rc;
+    if (src_on_device) {
+      // pack on the device, then keep the packed bytes in pinned host memory
+      void *tmp = nullptr;
+      MS_HIP_TRY(hipMalloc(&tmp, Ly.bytes[mat]));
+      int rc = pack_device(static_cast<uint8_t *>(tmp), src, K[mat], N[mat], st);
+      if (rc == MS_OK &&
+          hipMemcpyAsync(Ly.h_packed[mat], tmp, Ly.bytes[mat], hipMemcpyDeviceToHost, st) !=
+              hipSuccess)
+        rc = fail(MS_E_HIP, "set_matrix: copy of the packed weights to pinned memory failed");
+      (void)hipStreamSynchronize(st);
+      (void)hipFree(tmp);
+      if (rc) return rc;
+    } else if (int rc = ms_host_q4_pack(Ly.h_packed[mat], src, K[mat], N[mat])) {
+      return rc;
+    }
   }
   Ly.scale[mat] = scale;
   Ly.set_mask |= 1 << mat;
@@ -1266,6 +1279,36 @@ extern "C" int ms_model_set_taps(ms_model *m, float *d_hidden, float *d_logits) 
     (void)hipGraphExecDestroy(m->gexec);
     m->gexec = nullptr;
   }
+  return MS_OK;
+}
+
+extern "C" int ms_model_read_kv(ms_model *m, int layer, int seq, int pos0, int n, float *d_k,
+                                float *d_v) {
+  if (int rc = require_init()) return rc;
+  MS_CHECK_ARG(m && layer >= 0 && layer < (int)m->L.size(), "read_kv: bad layer");
+  MS_CHECK_ARG(seq >= 0 && seq < m->d.max_seqs, "read_kv: bad sequence");
+  MS_CHECK_ARG(pos0 >= 0 && n >= 0 && (d_k || d_v), "read_kv: bad range");
+  const Layer &Ly = m->L[layer];
+  const int L = Ly.d.cache_len;
+  const bool circ = Ly.d.cache_kind == MS_CACHE_CIRCULAR;
+  MS_CHECK_ARG(circ ? n <= L : pos0 + n <= L, "read_kv: positions outside the cache");
+  const size_t row = (size_t)Ly.d.kv_dim * 4;
+  hipStream_t st = ctx().stream;
+  const float *kb = Ly.kc + (size_t)seq * Ly.cache_seq_stride;
+  const float *vb = Ly.vc + (size_t)seq * Ly.cache_seq_stride;
+  // slot of position p: p % window (circular, write_kv_sliding) or p (linear)
+  for (int i = 0; i < n;) {
+    const int slot = circ ? (pos0 + i) % L : pos0 + i;
+    const int run = std::min(n - i, L - slot);  // rows contiguous in the cache
+    if (d_k)
+      MS_HIP_TRY(hipMemcpyAsync(d_k + (size_t)i * Ly.d.kv_dim, kb + (size_t)slot * Ly.d.kv_dim,
+                                (size_t)run * row, hipMemcpyDeviceToDevice, st));
+    if (d_v)
+      MS_HIP_TRY(hipMemcpyAsync(d_v + (size_t)i * Ly.d.kv_dim, vb + (size_t)slot * Ly.d.kv_dim,
+                                (size_t)run * row, hipMemcpyDeviceToDevice, st));
+    i += run;
+  }
+  MS_HIP_TRY(hipStreamSynchronize(st));
   return MS_OK;
 }
 

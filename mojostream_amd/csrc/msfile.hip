@@ -249,6 +249,87 @@ extern "C" int ms_file_ple_scale(const ms_file *f, int layer, float *out) {
   return MS_OK;
 }
 
+// compute_dir_checksum (src/tests/validate_real.mojo:78-83): the XOR of the
+// 32-bit words at byte 16 of every directory entry, i.e. of the scale fields'
+// bit patterns.
+extern "C" int ms_file_dir_checksum(const ms_file *f, uint32_t *out) {
+  MS_CHECK_ARG(f && out, "dir_checksum: null argument");
+  uint32_t acc = 0;
+  const uint8_t *b = f->raw.data();
+  for (uint64_t i = 0; i < f->meta.n_tensors; ++i) acc ^= rd<uint32_t>(b + kHdr + i * kDirEntry + 16);
+  *out = acc;
+  return MS_OK;
+}
+
+// run_validation (src/tests/validate_real.mojo:110-260): the structural checks
+// of a converted file, counted like the reference (one check each; a spot
+// check per tensor).  Like the reference it reports instead of failing: the
+// return value is MS_OK unless the arguments are bad.
+extern "C" int ms_file_validate(const ms_file *f, ms_file_validation *out) {
+  MS_CHECK_ARG(f && out, "file_validate: null argument");
+  ms_file_validation &r = *out;
+  r = ms_file_validation{};
+  const ms_file_meta &m = f->meta;
+  const uint8_t *b = f->raw.data();
+  r.file_bytes = m.file_bytes;
+  auto check = [&](bool ok, int bit, const std::string &msg) {
+    r.n_checks += 1;
+    if (ok) return;
+    r.n_failed += 1;
+    r.failed_mask |= 1u << bit;
+    if (!r.message[0]) snprintf(r.message, sizeof r.message, "%s", msg.c_str());
+  };
+  // [2] magic: the first word "MOJO" (:130-135), then the architecture fields
+  // (:144-155)
+  check(rd<uint32_t>(b) == 0x4F4A4F4Du, MS_VALIDATE_MAGIC, "magic: expected 'MOJO...'");
+  const bool arch_ok = m.n_layers > 0 && m.hidden > 0 && m.ffn_dim > 0 && m.n_heads > 0 &&
+                       !(m.n_kv_heads > 0 && m.kv_dim % m.n_kv_heads != 0);
+  check(arch_ok, MS_VALIDATE_ARCH,
+        "architecture fields: n_layers, hidden, ffn_dim, n_heads must be positive and kv_dim a "
+        "multiple of n_kv_heads");
+  // [3] Engram extension at byte 64 (:158-176)
+  check(rd<uint32_t>(b + 64) == 0x52474E45u, MS_VALIDATE_ENGRAM, "Engram magic 'ENGR' missing");
+  // [4] n_tensors == n_layers * 8 (:179-190), offsets inside the file (:192-205)
+  check(m.n_tensors == (uint64_t)m.n_layers * kPerLayer, MS_VALIDATE_TENSORS,
+        "n_tensors=" + std::to_string(m.n_tensors) + " != n_layers*8=" +
+            std::to_string((uint64_t)m.n_layers * kPerLayer));
+  bool off_ok = true;
+  for (const auto &e : f->dir)
+    if (e.data_offset > 0 && e.data_offset >= m.file_bytes) off_ok = false;
+  check(off_ok, MS_VALIDATE_OFFSETS, "a directory offset lies outside the file");
+  // [5] directory checksum, zero counts as a failure (:207-217)
+  uint32_t chk = 0;
+  ms_file_dir_checksum(f, &chk);
+  r.dir_checksum = chk;
+  check(chk != 0, MS_VALIDATE_CHECKSUM, "directory checksum is 0 (all scales zero?)");
+  // [6] spot checks of Q and Gate in layers 0, 20, 41 (:219-232): the first 64
+  // bytes neither all 0x00 nor all 0xFF
+  int bit = MS_VALIDATE_SPOT;
+  for (uint32_t layer : {0u, 20u, 41u}) {
+    if (layer >= m.n_layers && layer != 0) continue;
+    for (int type : {1, 5}) {
+      const uint8_t *ptr = nullptr;
+      float sc = 0.f;
+      size_t nb = 0;
+      bool ok = ms_file_tensor(f, (int)layer, type, &ptr, &sc, &nb) == MS_OK && nb >= 64;
+      if (ok) {
+        bool zero = true, ff = true;
+        for (int i = 0; i < 64; ++i) {
+          zero = zero && ptr[i] == 0;
+          ff = ff && ptr[i] == 0xFF;
+        }
+        ok = !zero && !ff;
+      }
+      check(ok, bit, "layer " + std::to_string(layer) + (type == 1 ? " Q" : " Gate") +
+                         ": first 64 bytes all 0x00 or all 0xFF, or the tensor is missing");
+      if (bit < 31) ++bit;
+    }
+  }
+  r.passed = r.n_failed == 0;
+  set_error("");
+  return MS_OK;
+}
+
 // ShapeGuard: the invariants of validate_gemma4_shape (mojostream.mojo:190-219)
 // plus the head-size checks per layer type.
 extern "C" int ms_file_shape_guard(const ms_file *f) {

@@ -22,7 +22,7 @@ from typing import List, Optional, Sequence
 import numpy as np
 
 from . import (MS_CACHE_CIRCULAR, MS_CACHE_LINEAR, Arch, FileEntry, FileLayer, FileMeta,
-               LayerDesc, Model, MSError, check, lib)
+               FileValidation, LayerDesc, Model, MSError, check, lib)
 
 MS_PLE, MS_Q, MS_K, MS_V, MS_O, MS_GATE, MS_UP, MS_DOWN = range(8)
 TENSORS_PER_LAYER = 8
@@ -114,6 +114,26 @@ class MojoStreamFile:
     def validate_tensor_entries(self) -> None:
         """TensorGuard: order, shapes per layer type, alignment, bounds, scale."""
         check(_lib.ms_file_tensor_guard(self.h))
+
+    def dir_checksum(self) -> int:
+        """compute_dir_checksum (src/tests/validate_real.mojo:78-83): XOR of
+        the scale fields' 32-bit patterns over the directory."""
+        v = C.c_uint32()
+        check(_lib.ms_file_dir_checksum(self.h, C.byref(v)))
+        return int(v.value)
+
+    def validate(self) -> dict:
+        """The structural checks of run_validation (src/tests/validate_real.mojo
+        :110-260): counts, the failed checks and the directory checksum."""
+        v = FileValidation()
+        check(_lib.ms_file_validate(self.h, C.byref(v)))
+        names = ["magic", "architecture", "engram", "n_tensors", "offsets", "checksum",
+                 "spot L0 Q", "spot L0 Gate", "spot L20 Q", "spot L20 Gate", "spot L41 Q",
+                 "spot L41 Gate"]
+        return dict(passed=bool(v.passed), n_checks=v.n_checks, n_failed=v.n_failed,
+                    failed=[n for i, n in enumerate(names) if v.failed_mask >> i & 1],
+                    checksum=int(v.dir_checksum), checksum_hex=f"0x{v.dir_checksum:08X}",
+                    file_bytes=int(v.file_bytes), message=v.message.decode(errors="replace"))
 
     def set_layer_types(self, is_full: Optional[Sequence[bool]]) -> None:
         if is_full is None:

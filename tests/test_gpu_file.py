@@ -140,3 +140,37 @@ def test_loader_errors(gpu, tmp_path):
         with pytest.raises(ms.MSError, match="pin layers before binding"):
             ms.check(ms.lib().ms_model_set_pinned(s.h, flags.ctypes.data))
         s.close()
+
+
+def test_validate_layer0_against_refb(gpu, tmp_path):
+    """validate.mojo (validate_layer.run_validation :159-233) on a synthetic
+    demo file: the REFB reference is written as scripts/gen_reference.py
+    writes it (layer 0 in float64 numpy on 0.1 * N(0,1) rows of seed 1234),
+    here by the independent f64 layer of tests/golden/layer_ref.py.  Passes at
+    relative RMSE < 1e-4; a reference output off by 1 % fails."""
+    import numpy as np
+    from mojostream_amd import streaming as st
+    from mojostream_amd import validate as val
+    from mojostream_amd.__main__ import main as cli
+    from tests.golden.layer_ref import RefLayer
+    say("validate: layer 0 of a demo file against a layer0_ref.bin")
+    p = str(tmp_path / "model.mojostream")
+    ref = str(tmp_path / "layer0_ref.bin")
+    st.write_synthetic(p, 2, 512, 128, 1024, 8, 2, seed=21)
+    with st.MojoStreamFile(p) as f:
+        desc = f.arch(max_len=8).layers[0]
+        ws = [f.tensor_array(0, t) for t in range(1, 8)]
+        sc = [f.tensor_ptr(0, t).scale for t in range(1, 8)]
+        layer = RefLayer(desc, 512, 1024, ws, sc, f.ple_scale(0))
+    x = (np.random.default_rng(1234).standard_normal((4, 512)) * 0.1).astype(np.float32)
+    val.write_ref(ref, x, layer.forward(x, 0).astype(np.float32))
+    r = val.run_validation(p, ref)
+    print(f"  rel RMSE {r['rel_rmse']:.2e}")
+    assert r["passed"] and r["rel_rmse"] < 1e-5
+    assert cli(["validate", p, ref]) == 0
+    rr = val.run_real_validation(p, ref)
+    assert rr["stable"] and rr["ref_passed"]
+    off = val.read_ref(ref)
+    val.write_ref(ref, off.input, off.output * np.float32(1.01))
+    assert not val.run_validation(p, ref)["passed"]
+    assert cli(["validate", p, ref]) == 1
