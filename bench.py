@@ -47,24 +47,147 @@ def decode_bytes_per_token(arch, ctx_len):
     return b
 
 
-def cpu_baseline(arch, seed, n_tokens):
-    """The oracle (C restatement of the reference CPU path, B-pack blocking,
-    single thread like the reference's decode, AVX2 build when the host has
-    it) timed on a bounded sample: n_tokens decode tokens of the full model."""
-    from oracle.binding import Oracle, synthetic_oracle_model
+def host_cpu():
+    """CPU model name and the cores this process may use."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, usable
+
+
+def native_oracle():
+    """The oracle compiled with -march=native for this host, in a temporary
+    directory (None if the compiler is missing or the build fails)."""
+    import subprocess
+    import tempfile
+    from oracle.binding import Oracle
+    out = os.path.join(tempfile.mkdtemp(prefix="oracle_native_"), "liboracle_native.so")
+    src = os.path.join(ROOT, "oracle", "ms_oracle.c")
+    try:
+        subprocess.run(["gcc", "-O3", "-fPIC", "-std=c11", "-ffp-contract=off", "-fno-fast-math",
+                        "-march=native", "-shared", "-o", out, src, "-lm", "-lpthread"],
+                       check=True, capture_output=True, timeout=120)
+        return Oracle(path=out)
+    except Exception as e:  # noqa: BLE001 - the variant is optional
+        log(f"cpu baseline: no native build ({e})")
+        return None
+
+
+def cpu_baseline(arch, seed, prompt, n_tokens, all_threads):
+    """The oracle (C restatement of the reference CPU path with its B-pack
+    blocking) timed on the host on a bounded sample of the bench's own
+    workload: the 128-token prompt runs untimed (all threads), then n_tokens
+    batch-1 decode tokens at positions 128.. are timed.  Headline: the AVX2
+    build (-mavx2 -mfma, the reference's target) on 1 thread, as the
+    reference's decode runs (one 64-row block, kernels.mojo:212,266).  Also
+    reported: the same on a -march=native build, and the AVX2 build split
+    over all usable cores (a column split the reference does not have)."""
+    import numpy as np
+    from oracle.binding import HostWeights, Oracle
+    model_name, n_cpu, usable = host_cpu()
     o = Oracle(avx2=True)
-    o.set_threads(1)
-    log(f"cpu baseline: building host weights ({o.name})")
-    om = synthetic_oracle_model(o, arch, seed)
-    tok = 11
+    log(f"cpu baseline: host weights, {model_name}, {usable} usable of {n_cpu} cores ({o.name})")
+    om = HostWeights(arch, seed).model(o)
+    o.set_threads(min(16, usable))
     t0 = time.perf_counter()
-    for p in range(n_tokens):
-        tok = om.decode_token(tok, p)
-        log(f"cpu baseline: token {p + 1}/{n_tokens} {time.perf_counter() - t0:.1f}s")
-    dt = time.perf_counter() - t0
-    return {"value": n_tokens / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{n_tokens} batch-1 decode tokens of the full E4B-shape model "
-                      f"(positions 0..{n_tokens - 1}), oracle/{o.name}, 1 thread"}
+    y, _ = om.forward_keep(om.embed_rows(prompt), 0, [len(prompt) - 1])
+    first = int(np.argmax(om.logits_rows(y[-1:])[0]))
+    log(f"cpu baseline: {len(prompt)}-token prompt (untimed) {time.perf_counter() - t0:.1f}s")
+    res = {}
+    variants = [("avx2_1_thread", o, 1), ("native_1_thread", native_oracle(), 1),
+                (f"avx2_{all_threads}_threads", o, all_threads)]
+    for label, orc, threads in variants:
+        if orc is None:
+            continue
+        # every variant decodes the same tokens from the prompt's caches (the
+        # rows it writes at 128.. are the same each time)
+        om.o = orc
+        orc.set_threads(threads)
+        tok = first
+        t0 = time.perf_counter()
+        for k in range(n_tokens):
+            tok = om.decode_token(tok, len(prompt) + k)
+        dt = time.perf_counter() - t0
+        res[label] = n_tokens / dt
+        log(f"cpu baseline {label}: {n_tokens / dt:.3f} tok/s")
+    o.set_threads(1)
+    return {"value": res["avx2_1_thread"], "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n_tokens} batch-1 greedy decode tokens of the full E4B-shape model at "
+                      f"positions {len(prompt)}..{len(prompt) + n_tokens - 1} after the bench's "
+                      f"{len(prompt)}-token prompt; oracle AVX2 build, 1 thread",
+            "host_cpu": model_name, "nproc": n_cpu, "usable_cores": usable,
+            "variants_tokens_per_s": {k: round(v, 4) for k, v in res.items()},
+            "variants_note": "native_1_thread: -march=native build, 1 thread; "
+                             f"avx2_{all_threads}_threads: the AVX2 build split over "
+                             "columns on all usable cores, not the reference's threading"}
+
+
+def bench_c2(ms, seed=3, rotate_bytes=512 << 20):
+    """Isolated Q4 matmul (config 2): C = A . deq(W), A fp32 [M][K] N(0,1),
+    W Q4 [K][N] with K = N in {1024, 4096}, M in {1, 4, 64}.  Device time per
+    call (ms_bench_q4_matmul), the weights rotated over more than
+    rotate_bytes of HBM so that every call reads them from memory
+    (run_q4_benchmark, benchmark_q4.mojo:121-147).  Bytes: K*N/2 of weights
+    + 4MK + 4MN; FLOPs 2MKN."""
+    import ctypes as C
+    import numpy as np
+    L = ms.lib()
+    out = []
+    for K in (1024, 4096):
+        N = K
+        wb = K * N // 2
+        n_w = rotate_bytes // wb + 1
+        w = ms.DeviceBuffer(n_w * wb)
+        ms.check(L.ms_fill_random_u8(w.ptr, n_w * wb, seed, K))  # any bytes are valid panels
+        for M in (1, 4, 64):
+            a = ms.DeviceBuffer.from_array(ms.host_normal(M * K, seed, M).reshape(M, K))
+            c = ms.DeviceBuffer(M * N * 4)
+            avg = C.c_double()
+            ms.check(L.ms_bench_q4_matmul(c.ptr, a.ptr, w.ptr, wb, n_w, M, K, N, C.c_float(0.1),
+                                          2 * n_w, C.byref(avg)))
+            t = avg.value * 1e-6
+            by = wb + 4 * M * K + 4 * M * N
+            out.append({"M": M, "K": K, "N": N, "us": round(avg.value, 3),
+                        "gb_per_s": round(by / t / 1e9, 1),
+                        "hbm_frac": round(by / t / 1e9 / HBM_PEAK_GBPS, 4),
+                        "gflops": round(2.0 * M * K * N / t / 1e9, 1)})
+            log(f"c2: M={M} K=N={K}: {avg.value:.2f} us, {by / t / 1e9:.0f} GB/s, "
+                f"{2.0 * M * K * N / t / 1e9:.0f} GFLOPS")
+            a.free()
+            c.free()
+        w.free()
+    return out
+
+
+def bench_c1(ms, seed=42, steps=100):
+    """Demo decode harness (config 1, bench.mojo -> run_harness harness.mojo:185-328):
+    a seeded synthetic demo file (D=1024, 40 layers, 8q/2kv heads, hd 128,
+    FFN 4096), 4 rows of one sequence per step, 100 steps, the sequence growing
+    by 4 a step; a step is the input rows uploaded plus the 40 layers
+    (ms_forward).  P50 / P95 and tokens/s as the reference's JSON reports them."""
+    import contextlib
+    import tempfile
+    from mojostream_amd import drivers, streaming as st
+    path = os.path.join(tempfile.mkdtemp(prefix="c1_"), "demo.mojostream")
+    st.write_synthetic(path, 40, 1024, 256, 4096, 8, 2, seed=seed)
+    with contextlib.redirect_stdout(sys.stderr):
+        r = drivers.run_harness(path, steps=steps, batch=4, out_json=None)
+    os.remove(path)
+    keys = ("latency_p50_ms", "latency_p95_ms", "latency_p99_ms", "latency_best_ms",
+            "latency_worst_ms", "tokens_per_sec_p50", "tokens_per_sec_best", "ttft_ms")
+    res = {k: r[k] for k in keys}
+    res["workload"] = "demo model D=1024, 40 layers, batch-4 rows, 100 steps (harness)"
+    log(f"c1: {res}")
+    return res
 
 
 def rocpd_summary(db, steps, marker="k_embed", end_marker="k_argmax_fin"):
@@ -241,7 +364,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--ttft-prompt", type=int, default=512)
-    ap.add_argument("--cpu-tokens", type=int, default=2)
+    ap.add_argument("--cpu-tokens", type=int, default=8)
+    ap.add_argument("--c2", action=argparse.BooleanOptionalAction, default=True,
+                    help="isolated Q4 matmul section (config 2)")
+    ap.add_argument("--c1", action=argparse.BooleanOptionalAction, default=True,
+                    help="demo decode harness section (config 1)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time the decode with eager launches")
     ap.add_argument("--only", choices=["all", "decode", "ttft", "c5"], default="all",
@@ -332,7 +459,7 @@ def main():
     log(f"per-class (eager + events, {args.prof_tokens} tokens): " + ", ".join(
         f"{k} {v['ms'] / args.prof_tokens:.3f}ms" for k, v in prof.items() if v["launches"]))
     sweeps = {}
-    for cls in ("qkv_gemv", "o_gemv", "gateup_gemv", "down_gemv"):
+    for cls in ("qkv_gemv", "attention", "o_gemv", "gateup_gemv", "down_gemv"):
         sw = ms.prof_sweep(m, cls, passes=2)
         sw["gbps"] = sw["bytes_per_launch"] / (sw["avg_us"] * 1e-6) / 1e9
         sweeps[cls] = {k: round(v, 3) for k, v in sw.items()}
@@ -344,6 +471,8 @@ def main():
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "traffic": traffic_from_profile(),
             "avg_launch_us": gu["avg_us"], "bytes_per_launch": gu["bytes_per_launch"]}
     roof["frac"] = roof["achieved"] / roof["peak"]
+    for sw in sweeps.values():
+        sw["hbm_frac"] = round(sw["gbps"] / HBM_PEAK_GBPS, 4)
 
     out = {
         "metric": METRIC, "value": round(tps1, 2), "unit": "tokens/s", "n_gpus": 1,
@@ -389,6 +518,10 @@ def main():
 
         ttft = measure_ttft(ms, sorted({args.ttft_prompt, 2048}), args.seed)
         out["ttft_ms"] = {str(k): round(v, 2) for k, v in ttft.items()}
+        if args.c2:
+            out["c2_q4_matmul"] = bench_c2(ms)
+        if args.c1:
+            out["c1_harness"] = bench_c1(ms)
         if args.c5_steps > 0:
             out["c5_streaming_14b"] = bench_c5(ms, args.seed, args.c5_steps, args.c5_prompt)
     else:
@@ -406,7 +539,8 @@ def main():
         dst.free()
 
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(arch, args.seed, args.cpu_tokens)
+        out["cpu_baseline"] = cpu_baseline(arch, args.seed, prompt, args.cpu_tokens,
+                                           min(16, host_cpu()[2]))
     print(json.dumps(out))
 
 

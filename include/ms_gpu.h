@@ -129,6 +129,15 @@ int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
 int ms_q4_matmul_noalloc(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
                          int K, int N, float scale, int accumulate);
 
+/* Device time of ms_q4_matmul (overwriting C): `reps` calls back to back
+ * between two HIP events on the library stream, call r reading the weights at
+ * d_w0 + (r % n_w) * w_stride (panel layout), so that weights rotated over
+ * more memory than the caches hold come from HBM.  *avg_us: microseconds per
+ * call.  Measurement support for run_q4_benchmark (benchmark_q4.mojo:121-147),
+ * whose CPU timing has no device counterpart. */
+int ms_bench_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_w0, size_t w_stride,
+                       int n_w, int M, int K, int N, float scale, int reps, double *avg_us);
+
 /* ---- elementwise kernels ------------------------------------------------ */
 /* rmsnorm_inplace, kernels.mojo:474-489 */
 int ms_rmsnorm(float *d_x, int rows, int cols);
@@ -465,7 +474,11 @@ int ms_model_stream_stats(ms_model *m, ms_stream_stats *out);
 int ms_prof_enable(int on);
 int ms_prof_get(int cls, const char **name, long *launches, double *total_ms,
                 double *bytes);
-/* Kernel duration of one projection class (0 QKV, 2 O, 3 Gate|Up, 4 Down)
+/* Class 1 (attention): the last decode attention launch recorded while
+ * profiling (of a circular cache if any, else a linear one) re-launched over
+ * every layer of that kind, each on its own cache; bytes are the K/V rows
+ * attended at the current position plus the appended row.
+ * Kernel duration of one projection class (0 QKV, 2 O, 3 Gate|Up, 4 Down)
  * measured on the device: the last launch of that class recorded while
  * profiling was enabled is re-launched back to back `passes` times over every
  * layer with the same shapes, each launch on that layer's weights (so weights

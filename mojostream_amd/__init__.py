@@ -105,6 +105,7 @@ _SIGS = {
     "ms_dequant_q4": [_P, _P, _I, _I, _F], "ms_dequant_q4_packed": [_P, _P, _I, _I, _F],
     "ms_q4_matmul": [_P, _P, _P, _I, _I, _I, _F, _I],
     "ms_q4_matmul_noalloc": [_P, _P, _P, _I, _I, _I, _F, _I],
+    "ms_bench_q4_matmul": [_P, _P, _P, _SZ, _I, _I, _I, _I, _F, _I, C.POINTER(C.c_double)],
     "ms_rmsnorm": [_P, _I, _I], "ms_rmsnorm_weighted": [_P, _P, _I, _I],
     "ms_ple_scale": [_P, _SZ, _F], "ms_swiglu": [_P, _P, _SZ],
     "ms_rope": [_P, _I, _I, _I, _I, _I, _F, _I],

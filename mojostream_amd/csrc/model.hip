@@ -75,6 +75,10 @@ struct Prof {
   GemvArgs last[MS_PROF_CLASSES] = {};          // last GEMV launch per class
   int last_layer[MS_PROF_CLASSES] = {};
   bool have[MS_PROF_CLASSES] = {};
+  // last decode attention launch per cache kind (0 linear, 1 circular)
+  AttnArgs last_attn[2] = {};
+  int last_attn_layer[2] = {};
+  bool have_attn[2] = {};
   int layer = -1;
 };
 static Prof g_prof;
@@ -346,6 +350,12 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
       if (int rc2 = launch_attention_prefill(a, m->fq, m->fk, m->fpart, m->fpart_floats, st))
         return rc2;
     } else if (rc.T <= kPrefillAttnRows || rc.B != 1) {
+      if (g_prof.on && rc.T == 1) {
+        const int k = d.cache_kind == MS_CACHE_CIRCULAR ? 1 : 0;
+        g_prof.last_attn[k] = a;
+        g_prof.last_attn_layer[k] = l;
+        g_prof.have_attn[k] = true;
+      }
       if (int rc2 = launch_attention(a, st)) return rc2;
     } else {
       // a prefill chunk: consecutive row groups, each attending to the cache
@@ -1339,12 +1349,78 @@ extern "C" int ms_prof_get(int cls, const char **name, long *launches, double *t
   return MS_OK;
 }
 
+// Decode attention re-launched back to back over every layer of the recorded
+// launch's cache kind (circular if one was recorded, else linear) and head
+// size, each on its own layer's cache of the recorded sequences.  The
+// launches attend the recorded fresh row without appending it (write_cache
+// 0), so the caches are left as they were.  Bytes: the K and V rows of every
+// attended key (the fresh one read from the projection rows).
+static int attn_sweep(ms_model *m, int passes, double *avg_us, double *bytes_per_launch,
+                      long *launches) {
+  const int k = g_prof.have_attn[1] ? 1 : 0;
+  MS_CHECK_ARG(g_prof.have_attn[k], "prof_sweep: no decode attention recorded while profiling");
+  MS_CHECK_ARG(m->d.resident, "prof_sweep: resident models only");
+  const AttnArgs base = g_prof.last_attn[k];
+  std::vector<int> layers;
+  for (int l = 0; l < (int)m->L.size(); ++l)
+    if ((m->L[l].d.cache_kind == MS_CACHE_CIRCULAR) == (k == 1) &&
+        m->L[l].d.head_dim == m->L[g_prof.last_attn_layer[k]].d.head_dim)
+      layers.push_back(l);
+  if (passes < 0) layers.assign(-passes, g_prof.last_attn_layer[k]);
+  if (passes < 0) passes = 1;
+  const Layer &Lr = m->L[g_prof.last_attn_layer[k]];
+  const size_t seq0 = (size_t)(base.kc - Lr.kc) / Lr.cache_seq_stride;
+  hipStream_t st = ctx().stream;
+  std::vector<int32_t> pos(base.B);
+  MS_HIP_TRY(hipMemcpyAsync(pos.data(), base.pos, 4 * base.B, hipMemcpyDeviceToHost, st));
+  MS_HIP_TRY(hipStreamSynchronize(st));
+  hipEvent_t e0, e1;
+  MS_HIP_TRY(hipEventCreate(&e0));
+  MS_HIP_TRY(hipEventCreate(&e1));
+  double bytes = 0;
+  long n = 0;
+  int rc = MS_OK;
+  MS_HIP_TRY(hipEventRecord(e0, st));
+  for (int p = 0; p < passes && rc == MS_OK; ++p)
+    for (int l : layers) {
+      const Layer &Ly = m->L[l];
+      AttnArgs a = base;
+      a.kc = Ly.kc + seq0 * Ly.cache_seq_stride;
+      a.vc = Ly.vc + seq0 * Ly.cache_seq_stride;
+      a.cos_t = m->ropes[Ly.rope].cs;
+      a.sin_t = m->ropes[Ly.rope].sn;
+      a.n_chunks = Ly.n_chunks;
+      a.cache_len = Ly.d.cache_len;
+      a.clamp = Ly.d.clamp_reads;
+      a.write_cache = 0;
+      if ((rc = launch_attention(a, st))) break;
+      for (int b = 0; b < a.B; ++b) {
+        const int keys = std::min(pos[b] + 1, Ly.d.cache_len);
+        bytes += 2.0 * keys * Ly.d.kv_dim * 4;
+      }
+      ++n;
+    }
+  (void)hipEventRecord(e1, st);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  *avg_us = n ? (double)ms * 1e3 / n : 0.0;
+  if (bytes_per_launch) *bytes_per_launch = n ? bytes / n : 0.0;
+  if (launches) *launches = n;
+  return MS_OK;
+}
+
 extern "C" int ms_prof_sweep(ms_model *m, int cls, int passes, double *avg_us,
                              double *bytes_per_launch, long *launches) {
   if (int rc = require_init()) return rc;
   MS_CHECK_ARG(m && avg_us && passes != 0, "prof_sweep: bad arguments");
-  MS_CHECK_ARG(cls == PC_QKV || cls == PC_O || cls == PC_GATEUP || cls == PC_DOWN,
-               "prof_sweep: class must be a layer projection");
+  MS_CHECK_ARG(cls == PC_QKV || cls == PC_ATTN || cls == PC_O || cls == PC_GATEUP ||
+                   cls == PC_DOWN,
+               "prof_sweep: class must be a layer projection or attention");
+  if (cls == PC_ATTN) return attn_sweep(m, passes, avg_us, bytes_per_launch, launches);
   MS_CHECK_ARG(g_prof.have[cls], "prof_sweep: no launch of this class recorded while profiling");
   MS_CHECK_ARG(m->d.resident, "prof_sweep: resident models only");
   const GemvArgs base = g_prof.last[cls];

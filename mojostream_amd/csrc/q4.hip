@@ -1046,6 +1046,37 @@ extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packe
   return q4_matmul_impl(d_C, d_A, d_packed, M, K, N, scale, accumulate, buf);
 }
 
+extern "C" int ms_bench_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_w0,
+                                  size_t w_stride, int n_w, int M, int K, int N, float scale,
+                                  int reps, double *avg_us) {
+  using namespace ms;
+  if (int rc = require_init()) return rc;
+  if (int rc = q4_matmul_check(M, K, N)) return rc;
+  MS_CHECK_ARG(d_C && d_A && d_w0 && n_w >= 1 && reps >= 1 && avg_us, "bench_q4_matmul: bad args");
+  MS_CHECK_ARG(n_w == 1 || w_stride >= (size_t)K * N / 2, "bench_q4_matmul: stride < matrix bytes");
+  void *buf = nullptr;
+  if (int rc = ms::scratch(q4_matmul_scratch_bytes(M, K), &buf)) return rc;
+  hipStream_t st = ctx().stream;
+  // one untimed call (code objects, caches of the activations)
+  if (int rc = q4_matmul_impl(d_C, d_A, d_w0, M, K, N, scale, 0, buf)) return rc;
+  hipEvent_t e0, e1;
+  MS_HIP_TRY(hipEventCreate(&e0));
+  MS_HIP_TRY(hipEventCreate(&e1));
+  MS_HIP_TRY(hipEventRecord(e0, st));
+  int rc = MS_OK;
+  for (int r = 0; r < reps && rc == MS_OK; ++r)
+    rc = q4_matmul_impl(d_C, d_A, d_w0 + (size_t)(r % n_w) * w_stride, M, K, N, scale, 0, buf);
+  (void)hipEventRecord(e1, st);
+  (void)hipEventSynchronize(e1);
+  float ms_ = 0.f;
+  (void)hipEventElapsedTime(&ms_, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  *avg_us = (double)ms_ * 1e3 / reps;
+  return MS_OK;
+}
+
 extern "C" int ms_q4_matmul_noalloc(float *d_C, const float *d_A, const uint8_t *d_packed,
                                     int M, int K, int N, float scale, int accumulate) {
   using namespace ms;

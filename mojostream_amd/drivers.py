@@ -146,10 +146,13 @@ def run_harness(path: str, steps: int = BENCH_STEPS, batch: int = BENCH_BATCH,
     print(f"[4/4] latency over {steps} steps, batch={batch} ...")
     lat: List[int] = []
     pos = batch
+    dx = DeviceBuffer(batch * D * 4)   # the step's input rows, uploaded per step
     for s in range(steps):
         x = host_normal(batch * D, seed, 1 + s).reshape(batch, D)
+        base = (C.c_int * 1)(pos)
         t0 = time.perf_counter_ns()
-        model.forward(x, [pos], T=batch)
+        dx.upload(x)
+        check(lib().ms_forward(model.h, dx.ptr, 1, batch, base, None))
         lat.append(time.perf_counter_ns() - t0)
         pos += batch
         if s % 20 == 19:

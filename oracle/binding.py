@@ -69,10 +69,16 @@ _SIGS = {
 
 
 class Oracle:
-    def __init__(self, avx2: bool = False):
-        name = "liboracle_avx2.so" if (avx2 and cpu_has_avx2()) else "liboracle.so"
-        self.name = name
-        self.lib = _load(name)
+    def __init__(self, avx2: bool = False, path: Optional[str] = None):
+        """avx2 picks the -mavx2 -mfma build when the host has it; path loads
+        another build of ms_oracle.c (e.g. one made with -march=native)."""
+        if path is not None:
+            self.name = os.path.basename(path)
+            self.lib = C.CDLL(path)
+        else:
+            name = "liboracle_avx2.so" if (avx2 and cpu_has_avx2()) else "liboracle.so"
+            self.name = name
+            self.lib = _load(name)
         for fn, (args, res) in _SIGS.items():
             f = getattr(self.lib, fn)
             f.argtypes = args
