@@ -28,6 +28,12 @@ struct AttnArgs {
   // prefill: first position of the rows as the host expects it; it sizes the
   // key split and nothing else (the kernels read pos)
   int plan_pos;
+  // decode: every sequence's position is below pos_bound (0: no bound).  Only
+  // the chunks below it are launched, and they load their cached rows before
+  // the position arrives.  A position at or past the bound loses its keys
+  // beyond the launched chunks: the host must keep the bound.
+  int pos_bound;
+  int grid_chunks;  // set by the launcher
 };
 
 constexpr int kAttnChunk = 16;

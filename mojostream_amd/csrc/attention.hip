@@ -48,7 +48,7 @@ __device__ inline T keep(T v) {
 
 struct AttnP {
   int T, q_dim, kv_dim, n_heads, n_kv, G, rot, half, circular, cache_len, clamp, ld, apply_rope,
-      n_chunks, write_cache;
+      n_chunks, write_cache, grid_chunks;
   float scale;
   const float *qkv, *cos_t, *sin_t;
   const int32_t *pos;
@@ -74,6 +74,7 @@ __device__ inline AttnP load_params(const AttnArgs &a) {
   p.apply_rope = keep(a.apply_rope);
   p.n_chunks = keep(a.n_chunks);
   p.write_cache = keep(a.write_cache);
+  p.grid_chunks = keep(a.grid_chunks);
   p.scale = keep(a.scale);
   p.qkv = keep(a.qkv);
   p.cos_t = keep(a.cos_t);
@@ -1013,8 +1014,16 @@ __device__ inline float rope_mix(const AttnP &p, int d, float x, float y, float 
   return d < p.half ? x * c - y * s : y * s + x * c;
 }
 
-constexpr int kDecMergeChunks = 16;  // chunk partials per merge load batch
-constexpr int kSc1 = 16;             // buffer cache policy: sc1 (agent-coherent)
+constexpr int kSc1 = 16;  // buffer cache policy: sc1 (agent-coherent)
+
+// Merge units (float4 of one head) per thread: a power of two, so that a
+// thread's units share one head (HD / 4 is a multiple of it).
+constexpr int dec_units_per_thread(int HD, int TGM) {
+  const int n = (TGM * HD / 4 + 255) / 256;
+  return n <= 1 ? 1 : (n <= 2 ? 2 : (n <= 4 ? 4 : 8));
+}
+// Chunks per merge batch: 128 registers of o partials in flight per thread.
+constexpr int dec_merge_batch(int upt) { return 32 / upt < 4 ? 4 : 32 / upt; }
 
 template <int HD, int TGM>
 __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
@@ -1044,25 +1053,23 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
   const size_t cbase = (size_t)b * p.cache_seq_stride;
   const float *qrow = p.qkv + (size_t)b * p.ld;
 
-  // ---- loads that do not depend on the position: the position itself, a
-  // circular cache's rows, the raw q of the first batch, the fresh k and v
+  // ---- loads that do not depend on the position: the position itself, the
+  // chunk's cached rows, the raw q of the first batch, the fresh k and v.  The
+  // host launches only the chunks its bound on the position can reach, so
+  // the rows are loaded before the position arrives (slots past it are
+  // zeroed below).
   const int base = aldg<int32_t>(p.pos + b);
   float4 kr[F4], vr[F4];
 #pragma unroll
   for (int j = 0; j < F4; ++j) {
     kr[j] = float4{0.f, 0.f, 0.f, 0.f};
     vr[j] = float4{0.f, 0.f, 0.f, 0.f};
-  }
-  if (p.circular) {
-#pragma unroll
-    for (int j = 0; j < F4; ++j) {
-      const int f = tid + 256 * j;
-      const int slot = c * CH + f / (HD / 4), d4 = f % (HD / 4);
-      if (slot < L) {
-        const size_t off = cbase + (size_t)slot * p.kv_dim + h * HD + 4 * d4;
-        kr[j] = aldg<float4>(p.kc + off);
-        vr[j] = aldg<float4>(p.vc + off);
-      }
+    const int f = tid + 256 * j;
+    const int slot = c * CH + f / (HD / 4), d4 = f % (HD / 4);
+    if (slot < L) {
+      const size_t off = cbase + (size_t)slot * p.kv_dim + h * HD + 4 * d4;
+      kr[j] = aldg<float4>(p.kc + off);
+      vr[j] = aldg<float4>(p.vc + off);
     }
   }
   float qx[kRopeBatch], qy[kRopeBatch];
@@ -1094,22 +1101,11 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
   int lo, hi;
   key_range(p, base, &lo, &hi);
   const int nslots = p.circular ? min(L, base + 1) : min(hi + 1, L);
-  const int n_active = (nslots + CH - 1) / CH;
+  // (clamped to the launched chunks, so the counter stays consistent)
+  const int n_active = min((nslots + CH - 1) / CH, p.grid_chunks);
   if (c >= n_active) return;
   const int fslot = p.circular ? base % L : base;
   const bool fresh_here = fslot < nslots && fslot / CH == c;
-  if (!p.circular) {
-#pragma unroll
-    for (int j = 0; j < F4; ++j) {
-      const int f = tid + 256 * j;
-      const int slot = c * CH + f / (HD / 4), d4 = f % (HD / 4);
-      if (slot < nslots) {
-        const size_t off = cbase + (size_t)slot * p.kv_dim + h * HD + 4 * d4;
-        kr[j] = aldg<float4>(p.kc + off);
-        vr[j] = aldg<float4>(p.vc + off);
-      }
-    }
-  }
   float qc[kRopeBatch], qs[kRopeBatch];
 #pragma unroll
   for (int u = 0; u < kRopeBatch; ++u) {
@@ -1267,7 +1263,35 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
   __syncthreads();
   if (!s_last) return;
 
-  // chunk weights exp(m_c - M) / L per query head: wave w takes heads w, w+4..
+  // The merge.  Each thread owns UPT float4 units (head t, dims 4d4..) and
+  // issues the loads of its o partials for the first CB chunks before the
+  // (max, sum) pairs are read (device-coherent buffer loads), so both arrive
+  // in one memory round trip.  Wave w turns the pairs of heads w, w+4, .. into
+  // chunk weights e^(m_c - M) / sum_c e^(m_c - M) l_c (lanes over chunks),
+  // shared through LDS; then o = sum_c w_c o_c.  Chunks past the first CB (long
+  // linear caches) follow in further batches.
+  constexpr int UPT = dec_units_per_thread(HD, TGM);
+  constexpr int CB = dec_merge_batch(UPT);
+  const int u0 = tid * UPT;
+  const int t0 = u0 / H4, d40 = u0 % H4;
+  const bool owner = u0 < nu;
+  af32x4 ov[CB][UPT];
+  auto load_o = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      // (block-uniform condition: chunks past the last are not loaded and
+      // get weight 0)
+      const int cc = c0 + j;
+#pragma unroll
+      for (int k = 0; k < UPT; ++k)
+        ov[j][k] = cc < n_active ? __builtin_amdgcn_raw_buffer_load_b128(
+                                       rs_o, ((cc * G + t0) * HD + 4 * (d40 + k)) * 4, 0, kSc1)
+                                 : af32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  if (owner) load_o(0);
+  const __amdgpu_buffer_rsrc_t rs_ml =
+      __builtin_amdgcn_make_buffer_rsrc(pml, 0, p.n_chunks * G * 2 * 4, 0x00020000);
   const int wave = tid >> 6, lane = tid & 63;
   constexpr int MPL = kAttnMaxChunks / 64;  // chunks per lane
   for (int g = wave; g < G; g += 4) {
@@ -1278,8 +1302,10 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
       mc[i] = -INFINITY;
       lc[i] = 0.f;
       if (cc < n_active) {
-        mc[i] = ld_agent(pml + (cc * G + g) * 2);
-        lc[i] = ld_agent(pml + (cc * G + g) * 2 + 1);
+        const float2 v = __builtin_bit_cast(
+            float2, __builtin_amdgcn_raw_buffer_load_b64(rs_ml, (cc * G + g) * 8, 0, kSc1));
+        mc[i] = v.x;
+        lc[i] = v.y;
       }
     }
     float mx = -INFINITY;
@@ -1300,30 +1326,27 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
     }
   }
   __syncthreads();
-  // o = sum_c w_c o_c, 16-byte agent-coherent loads in batches of CB chunks
-  constexpr int CB = kDecMergeChunks;
-  for (int u = tid; u < nu; u += 256) {
-    const int t = u / H4, d4 = u % H4;
-    float4 o = float4{0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < n_active; c0 += CB) {
-      af32x4 v[CB];
+  if (!owner) return;
+  float4 oacc[UPT];
 #pragma unroll
-      for (int j = 0; j < CB; ++j) {
-        const int cc = min(c0 + j, n_active - 1);
-        v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs_o, ((cc * G + t) * HD + 4 * d4) * 4, 0,
-                                                     kSc1);
-      }
+  for (int k = 0; k < UPT; ++k) oacc[k] = float4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < n_active; c0 += CB) {
+    if (c0 > 0) load_o(c0);
 #pragma unroll
-      for (int j = 0; j < CB; ++j) {
-        const float w = c0 + j < n_active ? wsh[(c0 + j) * G + t] : 0.f;
-        o.x += v[j].x * w;
-        o.y += v[j].y * w;
-        o.z += v[j].z * w;
-        o.w += v[j].w * w;
+    for (int j = 0; j < CB; ++j) {
+      const float w = c0 + j < n_active ? wsh[(c0 + j) * G + t0] : 0.f;
+#pragma unroll
+      for (int k = 0; k < UPT; ++k) {
+        oacc[k].x += w * ov[j][k].x;
+        oacc[k].y += w * ov[j][k].y;
+        oacc[k].z += w * ov[j][k].z;
+        oacc[k].w += w * ov[j][k].w;
       }
     }
-    *reinterpret_cast<float4 *>(orow + 4 * u) = o;
   }
+#pragma unroll
+  for (int k = 0; k < UPT; ++k)
+    if (u0 + k < nu) *reinterpret_cast<float4 *>(orow + 4 * (u0 + k)) = oacc[k];
 }
 
 static size_t attn_decode_lds(const AttnArgs &a, int tgm) {
@@ -1336,15 +1359,18 @@ static int launch_attention_decode(const AttnArgs &a, hipStream_t st) {
   MS_CHECK_ARG(a.ctr, "attention: decode needs the chunk counters");
   const int G = a.n_heads / a.n_kv;
   const int tgm = G <= 4 ? 4 : (G <= 8 ? 8 : kAttnMaxTG);
-  const dim3 grid(a.n_chunks, a.B * a.n_kv);
+  AttnArgs a2 = a;
+  const int reach = a.pos_bound > 0 ? std::min(a.pos_bound, a.cache_len) : a.cache_len;
+  a2.grid_chunks = std::max(1, std::min(a.n_chunks, (reach + kAttnChunk - 1) / kAttnChunk));
+  const dim3 grid(a2.grid_chunks, a.B * a.n_kv);
   const size_t shmem = attn_decode_lds(a, tgm);
 #define MS_DEC(HDV)                                                                        \
   if (tgm == 4)                                                                            \
-    hipLaunchKernelGGL((k_attn_decode<HDV, 4>), grid, dim3(256), shmem, st, a);           \
+    hipLaunchKernelGGL((k_attn_decode<HDV, 4>), grid, dim3(256), shmem, st, a2);          \
   else if (tgm == 8)                                                                       \
-    hipLaunchKernelGGL((k_attn_decode<HDV, 8>), grid, dim3(256), shmem, st, a);           \
+    hipLaunchKernelGGL((k_attn_decode<HDV, 8>), grid, dim3(256), shmem, st, a2);          \
   else                                                                                     \
-    hipLaunchKernelGGL((k_attn_decode<HDV, kAttnMaxTG>), grid, dim3(256), shmem, st, a)
+    hipLaunchKernelGGL((k_attn_decode<HDV, kAttnMaxTG>), grid, dim3(256), shmem, st, a2)
   switch (a.hd) {
     case 64: MS_DEC(64); break;
     case 128: MS_DEC(128); break;

@@ -197,6 +197,7 @@ extern "C" int ms_attention(const ms_layer_desc *L, const float *d_q, const floa
   a.cache_seq_stride = 0;
   a.out = d_out;
   a.plan_pos = base;
+  a.pos_bound = base + T;
   if (int rc = attn_check(a)) return rc;
   const int G = a.n_heads / a.n_kv;
   // many rows: the flash-attention prefill path (needs no chunk partials, but

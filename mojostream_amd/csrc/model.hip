@@ -129,7 +129,8 @@ struct ms_model {
   std::vector<int> h_pos;
   int dec_nseq = 0;
   // graph
-  hipGraphExec_t gexec = nullptr;
+  // captured decode steps, one per position bound (see decode_bound)
+  std::vector<std::pair<int, hipGraphExec_t>> graphs;
   int g_nseq = 0;
   // sampling (ms_model_set_sampling): temperature_sampling in place of the
   // greedy argmax, over a per-sequence history of prompt and generated ids
@@ -230,6 +231,8 @@ struct RunCfg {
   int seq0;                 // first sequence (caches / positions offset)
   int plan_pos;             // first row's position as the host knows it (B = 1);
                             // sizes the prefill attention's key split only
+  int pos_bound;            // every row's position is below it (decode attention
+                            // launches only the key chunks below it)
   float *tap_last;          // optional [n_layers][D]: each layer's last output row
 };
 
@@ -343,6 +346,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.out = m->aO;
     a.write_cache = 1;
     a.plan_pos = rc.plan_pos;
+    a.pos_bound = rc.pos_bound;
     // KV bytes read at the current position are counted by bench.py
     ProfScope ps(PC_ATTN, 0.0, st);
     if (rc.B == 1 && rc.T > kGemvMaxM && m->fq && prefill_flash_ok(a)) {
@@ -816,11 +820,16 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   return MS_OK;
 }
 
+static void drop_graphs(ms_model *m) {
+  for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.second);
+  m->graphs.clear();
+}
+
 extern "C" int ms_model_destroy(ms_model *m) {
   if (!m) return MS_OK;
   (void)hipStreamSynchronize(ctx().stream);
   (void)hipStreamSynchronize(ctx().copy_stream);
-  if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+  drop_graphs(m);
   for (auto &Ly : m->L)
     for (int i = 0; i < 7; ++i)
       if (Ly.h_packed[i]) (void)hipHostFree(Ly.h_packed[i]);
@@ -887,10 +896,7 @@ extern "C" int ms_model_set_matrix(ms_model *m, int layer, int mat, const uint8_
   }
   Ly.scale[mat] = scale;
   Ly.set_mask |= 1 << mat;
-  if (m->gexec) {
-    (void)hipGraphExecDestroy(m->gexec);
-    m->gexec = nullptr;
-  }
+  drop_graphs(m);
   return MS_OK;
 }
 
@@ -909,10 +915,7 @@ extern "C" int ms_model_set_ple(ms_model *m, int layer, float ple) {
   MS_CHECK_ARG(m && layer >= 0 && layer < (int)m->L.size(), "set_ple: bad layer");
   MS_CHECK_ARG(ple > 0.f && std::isfinite(ple), "set_ple: PLE scale must be > 0");
   m->L[layer].ple = ple;
-  if (m->gexec) {
-    (void)hipGraphExecDestroy(m->gexec);
-    m->gexec = nullptr;
-  }
+  drop_graphs(m);
   return MS_OK;
 }
 
@@ -970,10 +973,7 @@ extern "C" int ms_model_set_lm_head(ms_model *m, const uint8_t *src, int src_on_
   }
   m->lm_scale = scale;
   m->has_lm = true;
-  if (m->gexec) {
-    (void)hipGraphExecDestroy(m->gexec);
-    m->gexec = nullptr;
-  }
+  drop_graphs(m);
   return MS_OK;
 }
 
@@ -1011,10 +1011,7 @@ extern "C" int ms_model_set_lm_head_f32(ms_model *m, const float *src, int src_o
   }
   MS_HIP_TRY(hipStreamSynchronize(st));
   m->has_lm = true;
-  if (m->gexec) {
-    (void)hipGraphExecDestroy(m->gexec);
-    m->gexec = nullptr;
-  }
+  drop_graphs(m);
   return MS_OK;
 }
 
@@ -1055,10 +1052,7 @@ extern "C" int ms_model_set_sampling(ms_model *m, float temperature, float penal
   m->samp_temp = temperature;
   m->samp_pen = penalty;
   m->samp_seed = seed;
-  if (m->gexec) {  // the captured step holds the former choice
-    (void)hipGraphExecDestroy(m->gexec);
-    m->gexec = nullptr;
-  }
+  drop_graphs(m);  // the captured step holds the former choice
   return MS_OK;
 }
 
@@ -1089,6 +1083,7 @@ static int forward_impl(ms_model *m, int first, int count, float *d_x, int B, in
   rc.first_layer = first;
   rc.n_layers = count;
   rc.plan_pos = h_base[0];
+  for (int b = 0; b < B; ++b) rc.pos_bound = std::max(rc.pos_bound, h_base[b] + T);
   if (int r = run_layers(m, rc, st)) return r;
   if (int r = enqueue_output(m, rc, st)) return r;
   MS_HIP_TRY(hipStreamSynchronize(st));
@@ -1109,7 +1104,8 @@ extern "C" int ms_forward(ms_model *m, float *d_x, int n_seqs, int T, const int 
 }
 
 // ---- decode --------------------------------------------------------------------
-static int enqueue_decode_step(ms_model *m, int B, hipStream_t st) {
+// pos_bound: every sequence's position in this step is below it.
+static int enqueue_decode_step(ms_model *m, int B, int pos_bound, hipStream_t st) {
   const int D = m->d.hidden;
   {
     ProfScope ps(PC_PREP, (double)D * B / 2, st);
@@ -1125,6 +1121,7 @@ static int enqueue_decode_step(ms_model *m, int B, hipStream_t st) {
   rc.first_layer = 0;
   rc.n_layers = (int)m->L.size();
   rc.hidden = m->tap_hidden;
+  rc.pos_bound = pos_bound;
   if (int r = run_layers(m, rc, st)) return r;
   ArgmaxFin f{};
   f.tok_state = m->tok;
@@ -1132,6 +1129,48 @@ static int enqueue_decode_step(ms_model *m, int B, hipStream_t st) {
   f.ids_hist = m->ids_hist;
   f.step = m->step;
   return enqueue_lm(m, rc, 0, B, f, st);
+}
+
+// A captured step serves every step whose positions lie below its bound: the
+// end of the kBoundBucket-position bucket of the step's largest position.
+// Its attention launches the key chunks below the bound only and loads them
+// before the position arrives; a step's unattended loads stay under one
+// bucket of cache rows.
+constexpr int kBoundBucket = 64;
+constexpr size_t kMaxGraphs = 16;
+static int decode_bound(int max_pos) { return (max_pos / kBoundBucket + 1) * kBoundBucket; }
+
+static int decode_graph(ms_model *m, int B, int bound, hipStream_t st, hipGraphExec_t *out) {
+  if (m->g_nseq != B) {
+    drop_graphs(m);
+    m->g_nseq = B;
+  }
+  for (auto &g : m->graphs)
+    if (g.first == bound) {
+      *out = g.second;
+      return MS_OK;
+    }
+  // a new bound: capture one step while earlier launches run (capture records
+  // work, it runs none); an evicted graph may still be in flight, so the
+  // stream drains before it is destroyed
+  if (m->graphs.size() >= kMaxGraphs) {
+    MS_HIP_TRY(hipStreamSynchronize(st));
+    (void)hipGraphExecDestroy(m->graphs.front().second);
+    m->graphs.erase(m->graphs.begin());
+  }
+  hipGraph_t g;
+  MS_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  const int rc = enqueue_decode_step(m, B, bound, st);
+  const hipError_t e = hipStreamEndCapture(st, &g);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(MS_E_HIP, "decode graph capture failed");
+  hipGraphExec_t ge = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  MS_HIP_TRY(ei);
+  m->graphs.emplace_back(bound, ge);
+  *out = ge;
+  return MS_OK;
 }
 
 extern "C" int ms_decode_begin(ms_model *m, int n_seqs, const int32_t *h_tokens,
@@ -1165,31 +1204,21 @@ extern "C" int ms_decode_run(ms_model *m, int n_steps, int use_graph, int32_t *h
                    "8192 ids (prompt + generated); reset the model first");
   if (!m->d.resident) use_graph = 0;  // streaming runs eagerly (host-side slot logic)
   hipStream_t st = ctx().stream;
+  int p0 = 0;  // largest position of the first step
+  for (int b = 0; b < B; ++b) p0 = std::max(p0, m->h_pos[b]);
   int done = 0;
   while (done < n_steps) {
     const int chunk = std::min(n_steps - done, m->hist_cap);
     MS_HIP_TRY(hipMemsetAsync(m->step, 0, 4, st));
-    if (use_graph) {
-      if (!m->gexec || m->g_nseq != B) {
-        if (m->gexec) {
-          (void)hipGraphExecDestroy(m->gexec);
-          m->gexec = nullptr;
-        }
-        MS_HIP_TRY(hipStreamSynchronize(st));
-        hipGraph_t g;
-        MS_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        int rc = enqueue_decode_step(m, B, st);
-        hipError_t e = hipStreamEndCapture(st, &g);
-        if (rc) return rc;
-        if (e != hipSuccess) return fail(MS_E_HIP, "decode graph capture failed");
-        MS_HIP_TRY(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
-        (void)hipGraphDestroy(g);
-        m->g_nseq = B;
+    for (int s = 0; s < chunk; ++s) {
+      const int p = p0 + done + s;
+      if (use_graph) {
+        hipGraphExec_t g = nullptr;
+        if (int rc = decode_graph(m, B, decode_bound(p), st, &g)) return rc;
+        MS_HIP_TRY(hipGraphLaunch(g, st));
+      } else if (int rc = enqueue_decode_step(m, B, p + 1, st)) {
+        return rc;
       }
-      for (int s = 0; s < chunk; ++s) MS_HIP_TRY(hipGraphLaunch(m->gexec, st));
-    } else {
-      for (int s = 0; s < chunk; ++s)
-        if (int rc = enqueue_decode_step(m, B, st)) return rc;
     }
     if (h_ids_out)
       MS_HIP_TRY(hipMemcpyAsync(h_ids_out + (size_t)done * B, m->ids_hist,
@@ -1260,6 +1289,7 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
     rc.first_layer = 0;
     rc.n_layers = (int)m->L.size();
     rc.plan_pos = base;
+    rc.pos_bound = base + t;
     if (c0 + t >= n_tokens) rc.tap_last = m->tap_hidden;
     if ((rcode = run_layers(m, rc, st))) break;
     if (c0 + t >= n_tokens) {
@@ -1285,10 +1315,7 @@ extern "C" int ms_model_set_taps(ms_model *m, float *d_hidden, float *d_logits) 
   MS_CHECK_ARG(!d_logits || m->d.vocab > 0, "set_taps: logits need an LM head");
   m->tap_hidden = d_hidden;
   m->tap_logits = d_logits;
-  if (m->gexec) {  // the captured step holds the former targets
-    (void)hipGraphExecDestroy(m->gexec);
-    m->gexec = nullptr;
-  }
+  drop_graphs(m);  // the captured step holds the former targets
   return MS_OK;
 }
 

@@ -326,6 +326,32 @@ def test_e4b_small_graph_replays_match_eager(gpu, fast_oracle):
     b.close()
 
 
+def test_graph_position_bounds_match_eager(gpu):
+    """A captured decode step serves positions below its bound (64-position
+    buckets) and launches only the attention chunks below it; decoding across
+    several buckets in graph mode, in runs of uneven length, gives the same
+    ids as eager steps with exact bounds.  Balanced weights and a repetition
+    penalty keep the ids input-dependent, so a dropped or extra key shows."""
+    ms = gpu
+    arch = ms.arch_e4b(max_full_seq=256, n_layers=6, vocab=16384)
+    say("graph decode across position-bound buckets vs eager, batch 2")
+    ids = {}
+    for mode in ("graph", "eager"):
+        m = ms.Model(arch, max_seqs=2, max_rows=1, max_pos=256)
+        m.fill_synthetic(SEED, balanced=True)
+        m.set_sampling(0.0, 1.2)
+        g = mode == "graph"
+        runs = [m.decode([7, 11], [3, 50], 30, use_graph=g)]
+        for n in (41, 7, 60):  # the second sequence reaches position 187
+            runs.append(m.decode_continue(n, 2, use_graph=g))
+        ids[mode] = np.concatenate(runs)
+        m.close()
+    print(f"  distinct ids {len(set(ids['graph'][:, 0].tolist()))}, "
+          f"{len(set(ids['graph'][:, 1].tolist()))}")
+    assert len(set(ids["graph"][:, 1].tolist())) >= 5
+    assert np.array_equal(ids["graph"], ids["eager"])
+
+
 def test_streaming_equals_resident(gpu):
     ms = gpu
     arch = ms.arch_demo(max_len=64, n_layers=8)
