@@ -240,10 +240,12 @@ def pmc_summary(fetch_csv, write_csv, kernel, copy_bytes):
             raise SystemExit(f"no calibration copy in {path}")
         # the copy reads and writes copy_bytes
         factor = copy_bytes / 1024.0 / max(copy)
-        # decode launches (one activation row: the smallest grid of the kernel)
+        # decode launches (one activation row: the smallest grid of the kernel;
+        # decode attention's grid follows the position, so all of its launches)
         ks = [r for r in rows if kernel in r["Kernel_Name"]]
         g = min((int(r["Grid_Size"]) for r in ks), default=0)
-        vals = [float(r["Counter_Value"]) for r in ks if int(r["Grid_Size"]) == g]
+        vals = [float(r["Counter_Value"]) for r in ks
+                if int(r["Grid_Size"]) == g or "attn_decode" in kernel]
         if not vals:
             raise SystemExit(f"no {kernel} dispatches in {path}")
         res[counter] = {"factor": factor, "n": len(vals), "min_kib": min(vals),
@@ -379,7 +381,9 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="one device-to-device copy of this size (HBM counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="HBM traffic of the Gate|Up GEMV from two --pmc runs and exit")
+                    help="HBM traffic of a decode kernel from two --pmc runs and exit")
+    ap.add_argument("--pmc-kernel", default=GATEUP_KERNEL,
+                    help="kernel name (substring) for --pmc-summary")
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--c5-steps", type=int, default=256,
                     help="decode steps of the 14B streaming section (0: skip it)")
@@ -389,7 +393,7 @@ def main():
         print(rocpd_summary(args.rocpd_summary, args.steps))
         return
     if args.pmc_summary:
-        r = pmc_summary(args.pmc_summary[0], args.pmc_summary[1], GATEUP_KERNEL,
+        r = pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.pmc_kernel,
                         (args.copy_mib or 256) << 20)
         for c in ("FETCH_SIZE", "WRITE_SIZE"):
             v = r[c]
