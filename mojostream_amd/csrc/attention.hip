@@ -981,9 +981,6 @@ int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, float *fpa
 __device__ inline void st_agent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline float ld_agent(const float *p) {
-  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ inline float lane_of(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -1250,12 +1247,17 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
     st_agent(pml + (c * G + tid) * 2 + 1, sl[tid]);
   }
 
-  // ---- count this block done; the last one merges
+  // ---- count this block done; the last one merges.  The block's partial
+  // stores complete (device-scope stores, waited for), the barrier orders
+  // every thread's stores before thread 0's increment, and the increment is
+  // an agent-scope release + acquire: a block that sees the count reach
+  // n_active reads the other blocks' partials after their releases (the
+  // acquire invalidates stale cache lines; the loads are device-scope too).
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
   if (tid == 0) {
     unsigned *ctr = p.ctr + b * p.n_kv + h;
-    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     const int last = old + 1 == (unsigned)n_active;
     if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last;
