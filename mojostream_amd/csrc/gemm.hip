@@ -15,14 +15,15 @@
 // Tiling: a block computes kBM = 32 activation rows (128 limb rows, 8 MFMA A
 // tiles) by 4 kWB panels (8 panels, 128 columns).  Wave (wa, wb) owns A tiles
 // 4wa..4wa+3 and panels 4wb..4wb+3: 16 accumulators and 32 MFMAs per 128-row
-// step of K.  (A 16-panel tile measured the same on the prefill shapes.)  The
-// A operand of a step (128 limb rows x 128 bytes) is staged in LDS (a ring of
-// three steps), rows padded to 144 bytes so that the 16 rows one operand read
-// touches fall in different banks.  Each wave loads its panels' 1 KiB
-// super-tiles straight into registers.  Loads run two steps ahead of the
-// MFMAs, which a step's MFMA time alone does not cover.  In the D fragment of
-// an A tile, lane j + 16r holds the four limbs of activation row r, column j,
-// so the limbs combine inside the lane and no cross-wave reduction is needed.
+// step of K.  Both operands of a step (A 128 limb rows x 128 bytes, B one
+// 1 KiB super-tile of each panel) go from global memory straight into LDS
+// (global_load_lds: each wave instruction fills 1 KiB), in a ring of three
+// steps; loads run two steps ahead of the MFMAs, which a step's MFMA time
+// alone does not cover.  A limb rows are stored without padding, chunk c of
+// row r at chunk position c ^ ((r >> 1) & 7), so the 16 rows one fragment
+// read touches fall in 16 different bank groups.  In the D fragment of an A
+// tile, lane j + 16r holds the four limbs of activation row r, column j, so
+// the limbs combine inside the lane and no cross-wave reduction is needed.
 //
 // EPI_SWIGLU: the first half of the wave columns computes gate panels, the
 // second half the up panels of the same columns; the gate values pass through
@@ -37,10 +38,15 @@ namespace {
 constexpr int kBM = 32;                  // activation rows per block
 constexpr int kWB = 2;                   // wave columns: 4 panels each
 constexpr int kNT = 128 * kWB;           // threads (2 wave rows x kWB wave columns)
-constexpr int kApitch = 144;             // LDS bytes per staged limb row
-constexpr int kAstage = 4 * kBM * kApitch;  // one K step of A
-constexpr int kStages = 3;                  // A steps resident in LDS
-constexpr int kGemmLds = kStages * kAstage;
+constexpr int kAstage = 4 * kBM * 128;   // one K step of A: 128 limb rows x 128 bytes
+constexpr int kBstage = 8 * 1024;        // one super-tile of each of the 8 panels
+constexpr int kStage = kAstage + kBstage;
+constexpr int kStages = 3;               // K steps resident in LDS
+constexpr int kGemmLds = kStages * kStage;  // 72 KiB
+constexpr int kLoads = 6;                // direct loads per thread per K step
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
 
 template <int EPI>
 __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
@@ -76,55 +82,71 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   const int r0 = blockIdx.y * kBM;
   const int KG = K >> 7;
 
-  // this wave's four panels (scalar: block and wave uniform)
-  const uint8_t *wp[4];
+  // panel slot sl of the block's 8 -> weights, scale, first column, valid
+  // (block-uniform selects).  EPI_SWIGLU: slots 0-3 gate, 4-7 up panels of
+  // the same 4 column groups.
+  auto slot = [&](int sl, const uint8_t **w, float *sc, int *cl, bool *ok) {
+    if constexpr (EPI == EPI_SWIGLU) {
+      const int hf = sl >> 2, cp = blockIdx.x * 4 + (sl & 3);
+      *ok = cp < sn0;
+      *w = (hf == 0 ? sw0 : sw1) + (size_t)(*ok ? cp : 0) * K * 8;
+      *sc = hf == 0 ? ss0 : ss1;
+      *cl = cp * 16;
+    } else {
+      const int pi = blockIdx.x * 8 + sl;
+      const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
+      const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
+      *ok = pi < sn0 + sn1 + sn2;
+      const uint8_t *base = si == 0 ? sw0 : (si == 1 ? sw1 : sw2);
+      *w = *ok ? base + (size_t)loc * K * 8 : sw0;
+      *sc = si == 0 ? ss0 : (si == 1 ? ss1 : ss2);
+      *cl = (si == 0 ? sc0 : (si == 1 ? sc1 : sc2)) + loc * 16;
+    }
+  };
+  // the panels this wave computes: slots 4 wb .. 4 wb + 3
   float wsc[4];
   int col[4];
   bool pv[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if constexpr (EPI == EPI_SWIGLU) {
-      const int cp = blockIdx.x * (2 * kWB) + 4 * sub + j;
-      pv[j] = cp < sn0;
-      wp[j] = (half == 0 ? sw0 : sw1) + (size_t)(pv[j] ? cp : 0) * K * 8;
-      wsc[j] = half == 0 ? ss0 : ss1;
-      col[j] = cp * 16;
-    } else {
-      const int pi = blockIdx.x * (4 * kWB) + 4 * wb + j;
-      const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
-      const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
-      pv[j] = pi < sn0 + sn1 + sn2;
-      const uint8_t *base = si == 0 ? sw0 : (si == 1 ? sw1 : sw2);
-      wp[j] = pv[j] ? base + (size_t)loc * K * 8 : sw0;
-      wsc[j] = si == 0 ? ss0 : (si == 1 ? ss1 : ss2);
-      col[j] = (si == 0 ? sc0 : (si == 1 ? sc1 : sc2)) + loc * 16;
-    }
+    const uint8_t *w;
+    slot(4 * wb + j, &w, &wsc[j], &col[j], &pv[j]);
+  }
+  // the panels this wave loads: slots 2 wave, 2 wave + 1 (an invalid slot
+  // loads a valid panel, so every wave issues the same number of loads)
+  const uint8_t *lw[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float sc;
+    int cl;
+    bool ok;
+    slot(2 * wave + j, &lw[j], &sc, &cl, &ok);
   }
 
-  // A staging: 128 limb rows x 128 bytes = 1024 pieces of 16 bytes; thread t
-  // moves pieces t, t + kNT, ... (eight threads per row).
-  constexpr int NA = 1024 / kNT;
+  // A: this wave fills LDS blocks 4 wave + i (limb rows 8q .. 8q + 7) of a
+  // stage; lane l writes row 8q + l / 8 at chunk position l % 8, which holds
+  // chunk (l % 8) ^ ((row >> 1) & 7) of the row, so the 16 rows one fragment
+  // read touches fall in 16 different bank groups
   const int8_t *abase = limbs + (size_t)(4 * r0) * K;
-  auto a_load = [&](int G, u32x4 (&ar)[NA]) {
+  const int8_t *asrc[4];
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int e = tid + kNT * i, row = e >> 3, c = e & 7;
-      ar[i] = ldg<u32x4>(abase + (size_t)row * K + (size_t)G * 128 + c * 16);
-    }
-  };
-  auto a_store = [&](int buf, const u32x4 (&ar)[NA]) {
+  for (int i = 0; i < 4; ++i) {
+    const int row = 8 * (4 * wave + i) + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    asrc[i] = abase + (size_t)row * K + c * 16;
+  }
+  // K step G into stage stg: global memory straight into LDS
+  auto issue = [&](int G, int stg) {
+    uint8_t *sa = lds + stg * kStage;
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int e = tid + kNT * i, row = e >> 3, c = e & 7;
-      *reinterpret_cast<u32x4 *>(lds + buf * kAstage + row * kApitch + c * 16) = ar[i];
-    }
-  };
-  auto b_load = [&](int G, u32x4 (&br)[4]) {
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((gbl_void *)(asrc[i] + (size_t)G * 128),
+                                       (lds_void *)(sa + (4 * wave + i) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      br[j] = u32x4{0u, 0u, 0u, 0u};
-      if (pv[j]) br[j] = ldg<u32x4>(wp[j] + (size_t)G * 1024 + lane * 16);
-    }
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_void *)(lw[j] + (size_t)G * 1024 + lane * 16),
+                                       (lds_void *)(sa + kAstage + (2 * wave + j) * 1024), 16,
+                                       0, 0);
   };
 
   v4i acc[4][4];
@@ -134,20 +156,27 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
     for (int j = 0; j < 4; ++j) acc[a][j] = v4i{0, 0, 0, 0};
 
   const int li = lane & 15, lg = lane >> 4;
-  auto compute = [&](int buf, const u32x4 (&br)[4]) {
+  const int swz = (li >> 1) & 7;  // (row >> 1) & 7 for every row this lane reads
+  auto compute = [&](int stg) {
+    const uint8_t *sa = lds + stg * kStage;
+    u32x4 braw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      braw[j] = *reinterpret_cast<const u32x4 *>(sa + kAstage + (4 * wb + j) * 1024 + lane * 16);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       v4i bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t d0 = br[j][2 * h], d1 = br[j][2 * h + 1];
+        const uint32_t d0 = braw[j][2 * h], d1 = braw[j][2 * h + 1];
         bf[j] = v4i{(int)(d0 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu),
                     (int)(d1 & 0x0F0F0F0Fu), (int)((d1 >> 4) & 0x0F0F0F0Fu)};
       }
+      const int pos = (2 * lg + h) ^ swz;
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const v4i af = *reinterpret_cast<const v4i *>(
-            lds + buf * kAstage + (16 * (4 * wa + a) + li) * kApitch + 32 * lg + 16 * h);
+        const v4i af = *reinterpret_cast<const v4i *>(sa + (16 * (4 * wa + a) + li) * 128 +
+                                                      pos * 16);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[a][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[a][j], 0, 0, 0);
@@ -155,37 +184,34 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
     }
   };
 
-  // Software pipeline, two steps deep: the loads of step G + 2 go out while
-  // step G computes; step G + 1's A (loaded one step earlier) enters LDS at
-  // the end of step G.
-  u32x4 a1[NA], a2[NA], bc[4], b1[4], b2[4];
-  a_load(0, a1);
-  b_load(0, bc);
-  a_store(0, a1);
-  if (KG > 1) {
-    a_load(1, a1);
-    b_load(1, b1);
+  // the epilogue's row shifts and sums, loaded before the K loop (rows past
+  // M: shift 0, sum 0; their outputs are not stored)
+  int32_t rsh[4];
+  long long rz[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int row = r0 + 4 * (4 * wa + a) + (lane >> 4);
+    rsh[a] = row < M ? ldg<int32_t>(shift + row) : 0;
+    rz[a] = row < M ? 8 * ldg<long long>(xsum + row) : 0;
   }
-  __syncthreads();
-  int buf = 0;
+
+  // Ring of kStages K steps: step G + 2 is issued into the stage step G - 1
+  // used, once every wave has passed the barrier after computing it.  The
+  // barrier is a bare s_barrier: this wave's own loads of step G are waited
+  // for explicitly, and those of step G + 1 stay in flight (a __syncthreads
+  // would wait for them too).
+  issue(0, 0);
+  if (KG > 1) issue(1, 1);
   for (int G = 0; G < KG; ++G) {
-    const bool more2 = G + 2 < KG;
-    if (more2) {
-      a_load(G + 2, a2);
-      b_load(G + 2, b2);
-    }
-    compute(buf, bc);
-    const int nbuf = buf == kStages - 1 ? 0 : buf + 1;
-    if (G + 1 < KG) a_store(nbuf, a1);
-    __syncthreads();
-    buf = nbuf;
-#pragma unroll
-    for (int i = 0; i < NA; ++i) a1[i] = a2[i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      bc[j] = b1[j];
-      b1[j] = b2[j];
-    }
+    if (G + 1 < KG)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | kLoads);  // vmcnt(6)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);           // vmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (G + 2 < KG) issue(G + 2, (G + 2) % kStages);
+    compute(G % kStages);
   }
 
   // ---- epilogue: lane (column jc, row rr of each A tile)
@@ -193,9 +219,8 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   float v[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
-    const int row = r0 + 4 * (4 * wa + a) + rr;
-    const float sc = row < M ? ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.f;
-    const long long z = row < M ? 8 * ldg<long long>(xsum + row) : 0;
+    const float sc = ldexpf(1.0f, -rsh[a]);
+    const long long z = rz[a];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const v4i d = acc[a][j];
@@ -206,6 +231,7 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   }
   if constexpr (EPI == EPI_SWIGLU) {
     // gate values of wave (wa, sub) -> LDS -> up wave (wa, sub)
+    __syncthreads();  // every wave is done reading the operand stages
     float *xg = reinterpret_cast<float *>(lds);
     const int xo = (wa * (kWB / 2) + sub) * 16;
     if (half == 0) {
@@ -275,9 +301,6 @@ constexpr int kGLds = kGStages * kGStage;    // 144 KiB
 constexpr int kGNT = 512;                    // threads per block
 constexpr int kGLoads = 6;                   // direct loads per thread per K step
 constexpr int kGemmBigMinBlocks = 512;
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef const __attribute__((address_space(1))) void gbl_void;
 
 template <int EPI>
 __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
@@ -398,6 +421,16 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
     }
   };
 
+  // the epilogue's row shifts and sums, loaded before the K loop
+  double rsc[4];
+  long long rz[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int row = r0 + 16 * wr + 4 * a + (lane >> 4);
+    rsc[a] = row < M ? (double)ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.0;
+    rz[a] = row < M ? 8 * ldg<long long>(xsum + row) : 0;
+  }
+
   // Ring of kGStages K steps: step G + 2 is issued into the stage step G - 1
   // used, once every wave has passed the barrier after computing it.
   issue(0, 0);
@@ -422,14 +455,6 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
   for (int j = 0; j < 8; ++j) {
     const uint8_t *w;
     slot(8 * wc + j, &w, &wsc[j], &col[j], &pv[j]);
-  }
-  double rsc[4];
-  long long rz[4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int row = r0 + 16 * wr + 4 * a + rr;
-    rsc[a] = row < M ? (double)ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.0;
-    rz[a] = row < M ? 8 * ldg<long long>(xsum + row) : 0;
   }
   auto value = [&](int a, int j) {
     const v4i d = acc[a][j];
