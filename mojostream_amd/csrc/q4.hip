@@ -673,25 +673,20 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
 
   // output (slot p, row m, column j): sum the waves per limb row (exact int32:
   // |limb * (n - 8)| <= 1024 per term, K <= 16384), combine the limbs in
-  // int64, scale once.  Loops over the slot are unrolled so every per-slot
-  // value is a compile-time index.
+  // int64, scale once.  Each output is finished by the thread that sums it
+  // (no second pass through LDS).
+  auto value = [&](int p, int m, int j) {
+    const int c = m >> 2, r0 = 4 * (m & 3);
+    long long t = 0;
 #pragma unroll
-  for (int p = 0; p < P; ++p)
-    for (int o = threadIdx.x; o < M * 16; o += NT) {
-      const int m = o >> 4, j = o & 15;
-      const int c = m >> 2, r0 = 4 * (m & 3);
-      long long t = 0;
-#pragma unroll
-      for (int l = 0; l < 4; ++l) {
-        int d = 0;
-        for (int w = 0; w < W; ++w)
-          d += red[(((size_t)w * P + p) * C + c) * 256 + dfrag(r0 + l, j)];
-        t += (long long)d << (8 * l);
-      }
-      vals[p * M * 16 + o] = (float)((double)t * (double)ldexpf(1.0f, -row_s[m]) * (double)wsc[p]);
+    for (int l = 0; l < 4; ++l) {
+      int d = 0;
+      for (int w = 0; w < W; ++w)
+        d += red[(((size_t)w * P + p) * C + c) * 256 + dfrag(r0 + l, j)];
+      t += (long long)d << (8 * l);
     }
-  __syncthreads();
-
+    return (float)((double)t * (double)ldexpf(1.0f, -row_s[m]) * (double)wsc[p]);
+  };
   if constexpr (EPI == EPI_STORE || EPI == EPI_ACCUMULATE || EPI == EPI_RESID) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -699,7 +694,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
       for (int o = threadIdx.x; o < M * 16; o += NT) {
         const int m = o >> 4, j = o & 15;
         const size_t oi = (size_t)m * ldo + col[p] + j;
-        const float v = vals[p * M * 16 + o];
+        const float v = value(p, m, j);
         if constexpr (EPI == EPI_STORE) {
           out[oi] = v;
         } else if constexpr (EPI == EPI_ACCUMULATE) {
@@ -717,11 +712,15 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
     // (kernels.mojo:519-532) fused into the producer.
     for (int o = threadIdx.x; o < M * 16; o += NT) {
       const int m = o >> 4, j = o & 15;
-      const float gt = vals[o], up = vals[M * 16 + o];
+      const float gt = value(0, m, j), up = value(1, m, j);
       const float y = up * gt * (1.0f / (1.0f + expf(-gt)));
       sw_out[(size_t)m * ldo_sw + col[0] + j] = y;
     }
   } else if constexpr (EPI == EPI_ARGMAX) {
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      for (int o = threadIdx.x; o < M * 16; o += NT) vals[p * M * 16 + o] = value(p, o >> 4, o & 15);
+    __syncthreads();
     // logits (optional) and the block's first index of the maximum per row
     if (out) {
 #pragma unroll
