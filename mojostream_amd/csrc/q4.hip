@@ -253,14 +253,15 @@ __device__ inline void row_load(const RowSrc &r, int K, int m, RowRegs<NT, NG, G
 }
 
 // Sum of squares and maximum |value| over the block in one reduction pass.
-// sh: >= 2 * 16 floats.
+// sh: >= 2 * 16 floats.  fresh (block-uniform): sh has not been used yet in
+// this block, so no barrier is needed before writing it.
 template <int NT>
-__device__ inline void block_sum_max(float &ss, float &mx, float *sh) {
+__device__ inline void block_sum_max(float &ss, float &mx, float *sh, bool fresh = false) {
   constexpr int nw = NT / 64;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   ss = wave_sum(ss);
   mx = wave_max(mx);
-  __syncthreads();
+  if (!fresh) __syncthreads();
   if (lane == 0) {
     sh[w] = ss;
     sh[16 + w] = mx;
@@ -285,7 +286,8 @@ __device__ inline void block_sum_max(float &ss, float &mx, float *sh) {
 template <int NT, int NG, bool GAM, bool XS = false>
 __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
                                   RowRegs<NT, NG, GAM> &R, int8_t *dst, size_t ld_dst,
-                                  float *sh, int *s_out, double *xsum_out = nullptr) {
+                                  float *sh, int *s_out, double *xsum_out = nullptr,
+                                  bool sh_fresh = false) {
   const int nq = K >> 3;
   float y[NG][8];
   float ss = 0.f, mx = 0.f;
@@ -298,7 +300,7 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
       mx = fmaxf(mx, fabsf(y[gi][e]));
     }
   // one reduction for the norm and the maximum (max|y * inv| = max|y| * inv)
-  block_sum_max<NT>(ss, mx, sh);
+  block_sum_max<NT>(ss, mx, sh, sh_fresh);
   float inv = 1.f;
   if (r.norm) {
     inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(NT) void k_quant_rows(RowSrc r, int K, QuantRows q)
   row_load<NT, 2, GAM>(r, K, m, R);
   int s;
   double xs;
-  row_finish<NT, 2, GAM, true>(r, K, m, true, R, q.limbs, K, sh, &s, &xs);
+  row_finish<NT, 2, GAM, true>(r, K, m, true, R, q.limbs, K, sh, &s, &xs, true);
   if (threadIdx.x == 0) {
     q.shift[m] = s;
     q.xsum[m] = (int64_t)xs;
@@ -605,7 +607,8 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
     asm volatile("" ::"v"(R.v[0][0]), "v"(R.v[rows_ng(W) - 1][7]) : "memory");
     issue_part(0, 0, kEarly);
     int s;
-    row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s);
+    row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s, nullptr,
+                                      true);
     if (threadIdx.x == 0) row_s[0] = s;
     for (int m = 1; m < M; ++m) {
       row_load<NT, rows_ng(W), false>(rs, K, m, R);
