@@ -485,12 +485,13 @@ __host__ __device__ constexpr int rows_ng(int W) { return (void)W, 2; }
 
 // C: 16-row MFMA groups (4 limb rows per activation row: M <= 4C).
 // P: panels per block.  AS: GemvASource.  W: waves per block.  EPI: epilogue.
+// RP: activation rows whose loads the AS_ROWS prologue issues at once.
 //
 // Block pg = P panels of 16 columns over the whole K.  Wave w owns super-tiles
 // w, w+W, ...; each batch issues U of them (P panels each) before any is
 // consumed, and the first batch is issued before the prologue so that the
 // weight stream overlaps the activation quantization.
-template <int C, int P, int AS, int W, int EPI>
+template <int C, int P, int AS, int W, int EPI, int RP>
 __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ float sh[32];
@@ -602,17 +603,26 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
     // its share of the quantization: at most four loads per wave go out
     // before it, the rest after the prologue.
     constexpr int kEarly = (4 / P) < 1 ? 1 : ((4 / P) < U ? (4 / P) : U);
-    RowRegs<NT, rows_ng(W), false> R;
-    row_load<NT, rows_ng(W), false>(rs, K, 0, R);
-    asm volatile("" ::"v"(R.v[0][0]), "v"(R.v[rows_ng(W) - 1][7]) : "memory");
+    // The loads of the first RP rows go out together, before the weights, so
+    // that rows 1.. are in registers by the time the previous row is done.
+    RowRegs<NT, rows_ng(W), false> R[RP];
+#pragma unroll
+    for (int m = 0; m < RP; ++m)
+      if (m < M) row_load<NT, rows_ng(W), false>(rs, K, m, R[m]);
+    asm volatile("" ::"v"(R[0].v[0][0]), "v"(R[0].v[rows_ng(W) - 1][7]) : "memory");
     issue_part(0, 0, kEarly);
     int s;
-    row_finish<NT, rows_ng(W), false>(rs, K, 0, blockIdx.x == 0, R, limbs, ldl, sh, &s, nullptr,
-                                      true);
-    if (threadIdx.x == 0) row_s[0] = s;
-    for (int m = 1; m < M; ++m) {
-      row_load<NT, rows_ng(W), false>(rs, K, m, R);
-      row_finish<NT, rows_ng(W), false>(rs, K, m, blockIdx.x == 0, R, limbs, ldl, sh, &s);
+#pragma unroll
+    for (int m = 0; m < RP; ++m) {
+      if (m < M) {
+        row_finish<NT, rows_ng(W), false>(rs, K, m, blockIdx.x == 0, R[m], limbs, ldl, sh, &s,
+                                          nullptr, m == 0);
+        if (threadIdx.x == 0) row_s[m] = s;
+      }
+    }
+    for (int m = RP; m < M; ++m) {
+      row_load<NT, rows_ng(W), false>(rs, K, m, R[0]);
+      row_finish<NT, rows_ng(W), false>(rs, K, m, blockIdx.x == 0, R[0], limbs, ldl, sh, &s);
       if (threadIdx.x == 0) row_s[m] = s;
     }
     __syncthreads();
@@ -850,12 +860,14 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   const int C = a.M <= 4 ? 1 : 4;
   bool ok = false;
   // Supported (epilogue, panels per block, activation source, waves).
-#define MS_GEMV_L(CC, EP, PP, AS, WW) \
-  hipLaunchKernelGGL((k_gemv<CC, PP, AS, WW, EP>), dim3(blocks), dim3(64 * WW), shmem, st, a)
+#define MS_GEMV_L(CC, EP, PP, AS, WW, RR) \
+  hipLaunchKernelGGL((k_gemv<CC, PP, AS, WW, EP, RR>), dim3(blocks), dim3(64 * WW), shmem, st, a)
 #define MS_GEMV(EP, PP, AS, WW)                                                   \
   if (!ok && a.epi == EP && a.P == PP && a.asrc == AS && a.waves == WW) {        \
-    if (C == 1) MS_GEMV_L(1, EP, PP, AS, WW);                                     \
-    else MS_GEMV_L(4, EP, PP, AS, WW);                                            \
+    constexpr int RP = WW > 8 ? 1 : 4;                                            \
+    if (a.M == 1) MS_GEMV_L(1, EP, PP, AS, WW, 1);                                \
+    else if (C == 1) MS_GEMV_L(1, EP, PP, AS, WW, RP);                            \
+    else MS_GEMV_L(4, EP, PP, AS, WW, RP);                                        \
     ok = true;                                                                    \
   }
   MS_GEMV(EPI_STORE, 1, AS_ROWS, 8)
