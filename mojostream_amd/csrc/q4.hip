@@ -483,6 +483,128 @@ __host__ __device__ inline int gemv_ldl(int K) { return K + 16; }
 // 8-row groups per thread in the row prologue: K <= 8 * rows_ng(W) * 64 * W.
 __host__ __device__ constexpr int rows_ng(int W) { return (void)W, 2; }
 
+// Row prologue for two to four rows in a block of W = 4 or 8 waves: row r
+// belongs to waves r*G .. r*G + G - 1 (G = W / 4), so the rows are normalized
+// and quantized side by side instead of one after another.  The values are
+// dealt as in the one-row prologue of the same block (thread t = 64 vw + lane
+// of "virtual wave" vw holds groups t + 64 W gi): each real wave plays W / G
+// virtual waves, keeps a partial sum of squares per virtual wave, reduces each
+// with the same lane butterfly and adds them in virtual-wave order, so every
+// row's statistics, and therefore its limbs, are bit-identical to the one-row
+// prologue's.  Returns after the limb stores (no barrier after them).
+// kw: issue the first weight loads once the rows have arrived.
+template <int W, class KW>
+__device__ inline void rows_to_waves(const RowSrc &rs, int K, int M, int8_t *limbs, int ldl,
+                                     int32_t *row_s, float *sh, KW kw) {
+  constexpr int NT = 64 * W;
+  constexpr int G = W / 4;       // real waves per row
+  constexpr int VPR = W / G;     // virtual waves per real wave (4)
+  constexpr int NG = rows_ng(W);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int r = wave / G, j = wave % G;
+  const bool on = r < M;
+  const int nq = K >> 3;
+  float v[VPR][NG][8];
+#pragma unroll
+  for (int k = 0; k < VPR; ++k)
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      const int q = 64 * (j + G * k) + lane + NT * gi;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[k][gi][e] = 0.f;
+      if (on && q < nq) {
+        const float *p = rs.x + (size_t)r * rs.ld + 8 * q;
+        const float4 a = ldg<float4>(p), b = ldg<float4>(p + 4);
+        v[k][gi][0] = a.x; v[k][gi][1] = a.y; v[k][gi][2] = a.z; v[k][gi][3] = a.w;
+        v[k][gi][4] = b.x; v[k][gi][5] = b.y; v[k][gi][6] = b.z; v[k][gi][7] = b.w;
+      }
+    }
+  asm volatile("" ::"v"(v[0][0][0]), "v"(v[VPR - 1][NG - 1][7]) : "memory");
+  kw();
+  // statistics per virtual wave, in the one-row prologue's order
+  float ss[VPR], mx[VPR];
+#pragma unroll
+  for (int k = 0; k < VPR; ++k) {
+    ss[k] = 0.f;
+    mx[k] = 0.f;
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = v[k][gi][e] * rs.pre_scale;
+        ss[k] += y * y;
+        mx[k] = fmaxf(mx[k], fabsf(y));
+      }
+    ss[k] = wave_sum(ss[k]);
+    mx[k] = wave_max(mx[k]);
+  }
+  float SS = 0.f, MX = 0.f;
+  if constexpr (G == 1) {
+#pragma unroll
+    for (int k = 0; k < VPR; ++k) {
+      SS += ss[k];
+      MX = fmaxf(MX, mx[k]);
+    }
+  } else {
+    // the row's G waves meet in LDS: sh[(2 r) * W + vw] sums, [(2 r + 1) * W + vw] maxima
+    if (lane == 0) {
+#pragma unroll
+      for (int k = 0; k < VPR; ++k) {
+        sh[(2 * r) * W + j + G * k] = ss[k];
+        sh[(2 * r + 1) * W + j + G * k] = mx[k];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int vw = 0; vw < W; ++vw) {
+      SS += sh[(2 * r) * W + vw];
+      MX = fmaxf(MX, sh[(2 * r + 1) * W + vw]);
+    }
+  }
+  if (!on) return;
+  // row_emit's transform, quantization and stores for this thread's values
+  float inv = 1.f;
+  if (rs.norm) inv = 1.0f / sqrtf(SS / (float)K + 1e-6f);
+  const float amax = MX * inv * (1.0f + 1.0f / 4194304.0f);
+  const int s = row_shift(amax);
+  const float mul = ldexpf(1.0f, s);
+  const bool writer = blockIdx.x == 0;
+#pragma unroll
+  for (int k = 0; k < VPR; ++k)
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      const int q = 64 * (j + G * k) + lane + NT * gi;
+      if (q >= nq) continue;
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[e] = v[k][gi][e] * rs.pre_scale;
+        if (rs.norm) y[e] = y[e] * inv;
+      }
+      if (writer) {
+        const size_t o = (size_t)r * K + 8 * q;
+        if (rs.y_out) {
+          *reinterpret_cast<float4 *>(rs.y_out + o) = float4{y[0], y[1], y[2], y[3]};
+          *reinterpret_cast<float4 *>(rs.y_out + o + 4) = float4{y[4], y[5], y[6], y[7]};
+        }
+        if (rs.x_out) {
+          *reinterpret_cast<float4 *>(rs.x_out + o) =
+              float4{v[k][gi][0], v[k][gi][1], v[k][gi][2], v[k][gi][3]};
+          *reinterpret_cast<float4 *>(rs.x_out + o + 4) =
+              float4{v[k][gi][4], v[k][gi][5], v[k][gi][6], v[k][gi][7]};
+        }
+      }
+      uint32_t lo[4], hi[4];
+      quant8<false>(y, mul, lo, hi);
+      const int pos = limb_pos8(8 * q);
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        *reinterpret_cast<uint2 *>(limbs + (size_t)(4 * r + l) * ldl + pos) = uint2{lo[l], hi[l]};
+    }
+  if (j == 0 && lane == 0) row_s[r] = s;
+}
+
 // C: 16-row MFMA groups (4 limb rows per activation row: M <= 4C).
 // P: panels per block.  AS: GemvASource.  W: waves per block.  EPI: epilogue.
 // RP: activation rows whose loads the AS_ROWS prologue issues at once.
@@ -492,9 +614,9 @@ __host__ __device__ constexpr int rows_ng(int W) { return (void)W, 2; }
 // consumed, and the first batch is issued before the prologue so that the
 // weight stream overlaps the activation quantization.
 template <int C, int P, int AS, int W, int EPI, int RP>
-__global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ float sh[32];
+  __shared__ float sh[W > 8 ? 32 : (8 * W > 32 ? 8 * W : 32)];  // reduction scratch
   constexpr int NT = 64 * W;
   constexpr int U = gemv_batch<C, P, AS>();
   // wave-uniform in a scalar register: tile predicates below are then scalar
@@ -603,6 +725,10 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
     // its share of the quantization: at most four loads per wave go out
     // before it, the rest after the prologue.
     constexpr int kEarly = (4 / P) < 1 ? 1 : ((4 / P) < U ? (4 / P) : U);
+    if constexpr (RP == 4 && C == 1) {
+      // two to four rows: side by side, one wave group per row
+      rows_to_waves<W>(rs, K, M, limbs, ldl, row_s, sh, [&] { issue_part(0, 0, kEarly); });
+    } else {
     // The loads of the first RP rows go out together, before the weights, so
     // that rows 1.. are in registers by the time the previous row is done.
     RowRegs<NT, rows_ng(W), false> R[RP];
@@ -624,6 +750,7 @@ __global__ __launch_bounds__(64 * W) void k_gemv(GemvArgs a) {
       row_load<NT, rows_ng(W), false>(rs, K, m, R[0]);
       row_finish<NT, rows_ng(W), false>(rs, K, m, blockIdx.x == 0, R[0], limbs, ldl, sh, &s);
       if (threadIdx.x == 0) row_s[m] = s;
+    }
     }
     __syncthreads();
     if constexpr (kEarly < U) issue_part(0, kEarly, U);
