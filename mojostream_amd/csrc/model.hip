@@ -275,7 +275,9 @@ static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipS
   a.asrc = AS_QUANT;
   a.rows = RowSrc{};
   a.q = quant_rows_view(m->quant, a.M, a.K);
-  a.waves = 4;
+  // one to four rows of a long residual projection (Down at batch 2-4): 16
+  // waves, every super-tile of a wave in one batch
+  a.waves = (a.M <= 4 && a.P == 1 && a.epi == EPI_RESID && waves == 16) ? 16 : 4;
   if (int rc = launch_quant_rows(r, a.M, a.K, a.q, st)) return rc;
   return launch_gemv_rec(a, st);
 }

@@ -464,8 +464,11 @@ __device__ inline int dfrag(int i, int j) { return (j + 16 * (i >> 2)) * 4 + (i 
 // GEMV live in registers next to the weights, so it holds fewer.  Ten per
 // wave lets the decode shapes (E4B gate|up: 5 per panel at W = 4) finish
 // in one batch.
-template <int C, int P, int AS>
+template <int C, int P, int AS, int W>
 constexpr int gemv_batch() {
+  // one to four rows from global limbs in 16 waves (the Down projection at
+  // batch 2-4): five super-tiles per wave take K <= 10240 in one batch
+  if (AS == AS_QUANT && C == 1 && P == 1 && W == 16) return 5;
   constexpr int u = (AS == AS_QUANT ? 4 / C : 10 / C) / P;
   return u < 1 ? 1 : u;
 }
@@ -618,7 +621,7 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ float sh[W > 8 ? 32 : (8 * W > 32 ? 8 * W : 32)];  // reduction scratch
   constexpr int NT = 64 * W;
-  constexpr int U = gemv_batch<C, P, AS>();
+  constexpr int U = gemv_batch<C, P, AS, W>();
   // wave-uniform in a scalar register: tile predicates below are then scalar
   // branches, and loads behind them need no merge (and no wait) at the join
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -1006,6 +1009,12 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_GEMV(EPI_RESID, 1, AS_ROWS, 8)
   MS_GEMV(EPI_RESID, 1, AS_ROWS, 16)
   MS_GEMV(EPI_RESID, 1, AS_QUANT, 4)
+  if (!ok && a.epi == EPI_RESID && a.P == 1 && a.asrc == AS_QUANT && a.waves == 16) {
+    MS_CHECK_ARG(a.M <= 4, "GEMV: 16 waves over global limbs take at most 4 rows");
+    if (a.M == 1) MS_GEMV_L(1, EPI_RESID, 1, AS_QUANT, 16, 1);
+    else MS_GEMV_L(1, EPI_RESID, 1, AS_QUANT, 16, 4);
+    ok = true;
+  }
   MS_GEMV(EPI_SWIGLU, 2, AS_ROWS, 8)
   MS_GEMV(EPI_SWIGLU, 2, AS_ROWS, 4)
   MS_GEMV(EPI_SWIGLU, 2, AS_QUANT, 4)
