@@ -172,6 +172,31 @@ def test_e4b_small_batch4_vs_single(gpu, fast_oracle):
     m.close()
 
 
+def test_step_rows_bit_identical_to_single_rows(gpu):
+    """The rows of a decode step are independent: a row of a 2-4 row step,
+    whose GEMV prologues normalize and quantize the rows side by side (one wave
+    group per row), must equal the same row run alone, bit for bit, in every
+    layer's output.  The four sequences' caches are primed with the same 20-token
+    prompt, so a row's result depends only on its input and position."""
+    ms = gpu
+    arch = ms.arch_e4b(max_full_seq=256, n_layers=6, vocab=4096)
+    say("E4B 6 layers (1 full): rows of 2-4 row steps against single rows")
+    m = build(ms, arch, max_seqs=4, max_rows=4, max_pos=256)
+    D, P = arch.hidden, 20
+    prompt = prompt_ids(P, arch.vocab, 77)
+    for s in range(4):
+        m.prefill(prompt, 0, seq=s)
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((4, D)) * rng.uniform(0.1, 10, (4, 1))).astype(np.float32)
+    for B in (4, 3, 2):
+        out, hid = m.forward(x[:B], [P] * B, T=1, hidden=True)
+        for i in range(B):
+            o1, h1 = m.forward(x[i:i + 1], [P], T=1, hidden=True)
+            assert np.array_equal(h1[:, 0], hid[:, i]), (B, i)
+            assert np.array_equal(o1[0], out[i]), (B, i)
+    m.close()
+
+
 def oracle_sampled(om, oracle, prompt, n_steps, temperature, penalty, seed):
     """gemma4_e4b_infer.mojo:134-182 with the oracle: the prompt ids open the
     penalty history, every drawn id joins it, draw k of sequence 0 uses
