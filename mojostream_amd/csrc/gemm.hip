@@ -48,6 +48,18 @@ constexpr int kLoads = 6;                // direct loads per thread per K step
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void gbl_void;
 
+// Exact limb combine of one D fragment value, minus the zero-point term z:
+// each limb's int32 dot product is below 2^25 in magnitude (K <= 16384,
+// |limb| <= 128, nibble <= 15), so d0 + 2^8 d1 + 2^16 d2 + 2^24 d3 - z is an
+// integer below 2^51, formed exactly in double by FMAs: the same double the
+// 64-bit integer path produces, in fewer instructions.
+__device__ inline double limb_combine(const v4i d, double z) {
+  return __builtin_fma((double)d[3], 16777216.0,
+                       __builtin_fma((double)d[2], 65536.0,
+                                     __builtin_fma((double)d[1], 256.0, (double)d[0]))) -
+         z;
+}
+
 template <int EPI>
 __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -187,12 +199,12 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   // the epilogue's row shifts and sums, loaded before the K loop (rows past
   // M: shift 0, sum 0; their outputs are not stored)
   int32_t rsh[4];
-  long long rz[4];
+  double rz[4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const int row = r0 + 4 * (4 * wa + a) + (lane >> 4);
     rsh[a] = row < M ? ldg<int32_t>(shift + row) : 0;
-    rz[a] = row < M ? 8 * ldg<long long>(xsum + row) : 0;
+    rz[a] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
   }
 
   // Ring of kStages K steps: step G + 2 is issued into the stage step G - 1
@@ -220,14 +232,9 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const float sc = ldexpf(1.0f, -rsh[a]);
-    const long long z = rz[a];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const v4i d = acc[a][j];
-      const long long t = (long long)d[0] + ((long long)d[1] << 8) + ((long long)d[2] << 16) +
-                          ((long long)d[3] << 24) - z;
-      v[a][j] = (float)((double)t * (double)sc * (double)wsc[j]);
-    }
+    for (int j = 0; j < 4; ++j)
+      v[a][j] = (float)(limb_combine(acc[a][j], rz[a]) * (double)sc * (double)wsc[j]);
   }
   if constexpr (EPI == EPI_SWIGLU) {
     // gate values of wave (wa, sub) -> LDS -> up wave (wa, sub)
@@ -278,32 +285,35 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------
-// Big-tile variant for GEMMs with many blocks.  A block computes kGBM = 64
-// activation rows (256 limb rows) by kGPan = 16 panels (SwiGLU: 8 gate and
-// the 8 up panels of the same 128 columns).  Eight waves; wave (wr, wc) owns
-// limb rows 64wr..64wr+63 (4 A tiles) and panel slots 8wc..8wc+7: 32
-// accumulators.  Both operands of a K step (A 32 KiB, B 16 KiB) go from
-// global memory straight into LDS (global_load_lds_dwordx4: each wave
-// instruction fills 1 KiB, lane l the 16 bytes at l * 16), in a ring of three
-// steps, so the weights cross the L2 once per block rather than once per wave
-// row, and a K step does 64 MFMAs per wave against 16 KiB of LDS reads.  A limb rows
-// are stored without padding, the 16-byte chunk c of row r at chunk position
-// c ^ ((r >> 1) & 7): the 16 rows one A fragment read touches then fall in
-// 16 different bank groups.
+// Big-tile variant for GEMMs with many blocks.  A block computes kGBM = 32
+// activation rows (128 limb rows) by kGPan = 16 panel slots (SwiGLU: the gate
+// and the up panels of 8 column groups).  Four waves; wave (wr, wc) owns limb
+// rows 64wr..64wr+63 (4 A tiles) and 8 panel slots: 32 accumulators.  Both
+// operands of a K step (A 16 KiB, B 16 KiB) go from global memory straight
+// into LDS (global_load_lds_dwordx4: each wave instruction fills 1 KiB, lane l
+// the 16 bytes at l * 16), in a ring of two steps: 64 KiB, so two blocks share
+// a CU and one block's barriers, pipeline start and epilogue overlap the
+// other's MFMAs (with one 8-wave block per CU, the per-step barrier and the
+// epilogue left the MFMA units idle for a third of the time).  A limb rows are
+// stored without padding, the 16-byte chunk c of row r at chunk position
+// c ^ ((r >> 1) & 7): the 16 rows one A fragment read touches then fall in 16
+// different bank groups.
+//
+// EPI_SWIGLU: wave column wc holds the gate panels of column groups
+// 4wc..4wc+3 (slots j < 4) and the up panels of the same groups (j >= 4), so
+// each output's gate and up values meet in one lane.
 // ------------------------------------------------------------------------------
-constexpr int kGBM = 64;                     // activation rows per block
+constexpr int kGBM = 32;                     // activation rows per block
 constexpr int kGPan = 16;                    // panel slots per block
 constexpr int kGStageA = 4 * kGBM * 128;     // limb rows x 128 bytes
 constexpr int kGStageB = kGPan * 1024;       // one super-tile per panel
 constexpr int kGStage = kGStageA + kGStageB;
-constexpr int kGStages = 3;
-constexpr int kGLds = kGStages * kGStage;    // 144 KiB
-constexpr int kGNT = 512;                    // threads per block
-constexpr int kGLoads = 6;                   // direct loads per thread per K step
-constexpr int kGemmBigMinBlocks = 512;
+constexpr int kGStages = 2;
+constexpr int kGLds = kGStages * kGStage;    // 64 KiB
+constexpr int kGNT = 256;                    // threads per block
 
 template <int EPI>
-__global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
+__global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int M = launder(g.M), K = launder(g.K);
   const int8_t *limbs = launder(g.a.limbs);
@@ -329,7 +339,7 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int wr = wave & 3, wc = wave >> 2;
+  const int wr = wave & 1, wc = wave >> 1;
   const int r0 = blockIdx.y * kGBM;
   const int KG = K >> 7;
 
@@ -352,15 +362,20 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
       *col = (si == 0 ? sc0 : (si == 1 ? sc1 : sc2)) + loc * 16;
     }
   };
-  // this wave loads panel slots 2 wave, 2 wave + 1 (an invalid slot loads a
+  // the panel slot of this wave's accumulator column j
+  auto wslot = [&](int j) {
+    if constexpr (EPI == EPI_SWIGLU) return j < 4 ? 4 * wc + j : 8 + 4 * wc + (j - 4);
+    else return 8 * wc + j;
+  };
+  // this wave loads panel slots 4 wave .. 4 wave + 3 (an invalid slot loads a
   // valid panel: every wave issues the same number of loads per step)
-  const uint8_t *lw[2];
+  const uint8_t *lw[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < 4; ++j) {
     float sc;
     int col;
     bool ok;
-    slot(2 * wave + j, &lw[j], &sc, &col, &ok);
+    slot(4 * wave + j, &lw[j], &sc, &col, &ok);
   }
   // A: this wave fills LDS blocks 4 wave + i (limb rows 8q .. 8q + 7); lane l
   // writes row 8q + l / 8 at chunk position l % 8, which holds chunk
@@ -380,9 +395,9 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
       __builtin_amdgcn_global_load_lds((gbl_void *)(asrc[i] + (size_t)G * 128),
                                        (lds_void *)(sa + (4 * wave + i) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_global_load_lds((gbl_void *)(lw[j] + (size_t)G * 1024 + lane * 16),
-                                       (lds_void *)(sa + kGStageA + (2 * wave + j) * 1024), 16,
+                                       (lds_void *)(sa + kGStageA + (4 * wave + j) * 1024), 16,
                                        0, 0);
   };
 
@@ -396,10 +411,10 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
   const int swz = (li >> 1) & 7;  // (row >> 1) & 7 for every row this lane reads
   auto compute = [&](int stg) {
     const uint8_t *sa = lds + stg * kGStage;
-    const uint8_t *sb = sa + kGStageA + (8 * wc) * 1024 + lane * 16;
+    const uint8_t *sb = sa + kGStageA + lane * 16;
     u32x4 braw[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) braw[j] = *reinterpret_cast<const u32x4 *>(sb + j * 1024);
+    for (int j = 0; j < 8; ++j) braw[j] = *reinterpret_cast<const u32x4 *>(sb + wslot(j) * 1024);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       v4i bf[8];
@@ -421,69 +436,49 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
     }
   };
 
-  // the epilogue's row shifts and sums, loaded before the K loop
-  double rsc[4];
-  long long rz[4];
+  // Ring of two K steps: step G + 1 is issued into the stage step G - 1 used,
+  // once every wave has passed the barrier after computing it.  The barrier
+  // is a bare s_barrier after this wave's own loads of step G have landed.
+  issue(0, 0);
+  for (int G = 0; G < KG; ++G) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (G + 1 < KG) issue(G + 1, (G + 1) & 1);
+    compute(G & 1);
+  }
+
+  // ---- epilogue: lane (column jc, row rr of each A tile)
+  const int jc = lane & 15, rr = lane >> 4;
+  double rsc[4], rz[4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const int row = r0 + 16 * wr + 4 * a + (lane >> 4);
     rsc[a] = row < M ? (double)ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.0;
-    rz[a] = row < M ? 8 * ldg<long long>(xsum + row) : 0;
+    rz[a] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
   }
-
-  // Ring of kGStages K steps: step G + 2 is issued into the stage step G - 1
-  // used, once every wave has passed the barrier after computing it.
-  issue(0, 0);
-  if (KG > 1) issue(1, 1);
-  for (int G = 0; G < KG; ++G) {
-    // this wave's loads of step G are in LDS (step G + 1's may be in flight)
-    if (G + 1 < KG)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | kGLoads);  // vmcnt(6)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);            // vmcnt(0)
-    __syncthreads();
-    if (G + 2 < KG) issue(G + 2, (G + 2) % kGStages);
-    compute(G % kGStages);
-  }
-
-  // ---- epilogue: lane (column jc, row rr of each A tile), one tile at a time
-  const int jc = lane & 15, rr = lane >> 4;
   float wsc[8];
   int col[8];
   bool pv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint8_t *w;
-    slot(8 * wc + j, &w, &wsc[j], &col[j], &pv[j]);
+    slot(wslot(j), &w, &wsc[j], &col[j], &pv[j]);
   }
   auto value = [&](int a, int j) {
-    const v4i d = acc[a][j];
-    const long long t = (long long)d[0] + ((long long)d[1] << 8) + ((long long)d[2] << 16) +
-                        ((long long)d[3] << 24) - rz[a];
-    return (float)((double)t * rsc[a] * (double)wsc[j]);
+    return (float)(limb_combine(acc[a][j], rz[a]) * rsc[a] * (double)wsc[j]);
   };
   if constexpr (EPI == EPI_SWIGLU) {
-    // gate values of wave (wr, 0) -> LDS -> up wave (wr, 1)
-    __syncthreads();  // every wave is done reading the operand stages
-    float *xg = reinterpret_cast<float *>(lds) + wr * 32 * 64;
-    if (wc == 0) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 4; ++a) {
+      const int row = r0 + 16 * wr + 4 * a + rr;
+      if (row >= M) continue;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xg[(a * 8 + j) * 64 + lane] = value(a, j);
-    }
-    __syncthreads();
-    if (wc == 1) {
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int row = r0 + 16 * wr + 4 * a + rr;
-        if (row >= M) continue;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (!pv[j]) continue;
-          const float gt = xg[(a * 8 + j) * 64 + lane], up = value(a, j);
-          sw_out[(size_t)row * ldo_sw + col[j] + jc] = up * gt * (1.0f / (1.0f + expf(-gt)));
-        }
+      for (int j = 0; j < 4; ++j) {
+        if (!pv[j]) continue;
+        const float gt = value(a, j), up = value(a, j + 4);
+        sw_out[(size_t)row * ldo_sw + col[j] + jc] = up * gt * (1.0f / (1.0f + expf(-gt)));
       }
     }
   } else {
@@ -515,6 +510,31 @@ __global__ __launch_bounds__(kGNT) void k_gemm_big(GemmArgs g) {
 // Rows of the quantized operand a GEMM reads: the big tile's row block.
 int gemm_row_pad(int M) { return (M + kGBM - 1) / kGBM * kGBM; }
 
+namespace {
+
+// The kernel for a GEMM, from a model of its time in big-tile K steps: a
+// launch of B blocks runs ceil(B / slots) rounds (two blocks per CU), and the
+// 32-row, 8-panel kernel's K step costs about 0.8 of a big one.  (A split of
+// K over several blocks, their exact partials meeting through a counter, was
+// slower: the release/acquire increments disturbed the other blocks' L2
+// traffic, and with relaxed increments the partials' round trip still cost
+// more than the shorter rounds saved.)
+constexpr double kSmallStepCost = 0.8;
+
+bool gemm_use_big(const GemmArgs &g, int np) {
+  const bool swiglu = g.epi == EPI_SWIGLU;
+  const long slots = 2L * (ctx().n_cu > 0 ? ctx().n_cu : 256);
+  auto rounds = [&](long blocks) { return (double)((blocks + slots - 1) / slots); };
+  const long big = (long)(swiglu ? (np / 2 + 7) / 8 : (np + kGPan - 1) / kGPan) *
+                   (gemm_row_pad(g.M) / kGBM);
+  const long small = (long)(swiglu ? (np / 2 + 2 * kWB - 1) / (2 * kWB)
+                                   : (np + 4 * kWB - 1) / (4 * kWB)) *
+                     ((g.M + kBM - 1) / kBM);
+  return rounds(big) <= rounds(small) * kSmallStepCost;
+}
+
+}  // namespace
+
 int launch_gemm(const GemmArgs &g, hipStream_t st) {
   MS_CHECK_ARG(g.M >= 1 && g.K >= 128 && g.K % 128 == 0 && g.K <= kQuantMaxK,
                "GEMM: K must be a multiple of 128 in [128, 16384]");
@@ -535,11 +555,9 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
   int np = 0;
   for (int i = 0; i < g.nseg; ++i) np += g.seg[i].n_cols / 16;
   const bool swiglu = g.epi == EPI_SWIGLU;
-  // the big tile when it makes at least two rounds of the CUs
-  const int gxb = swiglu ? (np / 2 + 7) / 8 : (np + kGPan - 1) / kGPan;
-  const int gyb = gemm_row_pad(g.M) / kGBM;
-  if ((long)gxb * gyb >= kGemmBigMinBlocks) {
-    const dim3 grid(gxb, gyb);
+  if (gemm_use_big(g, np)) {
+    const int gxb = swiglu ? (np / 2 + 7) / 8 : (np + kGPan - 1) / kGPan;
+    const dim3 grid(gxb, gemm_row_pad(g.M) / kGBM);
 #define MS_GB(E) hipLaunchKernelGGL(k_gemm_big<E>, grid, dim3(kGNT), kGLds, st, g)
     switch (g.epi) {
       case EPI_STORE: MS_GB(EPI_STORE); break;
