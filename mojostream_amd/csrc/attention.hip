@@ -1251,8 +1251,10 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
   // stores complete (device-scope stores, waited for), the barrier orders
   // every thread's stores before thread 0's increment, and the increment is
   // an agent-scope release + acquire: a block that sees the count reach
-  // n_active reads the other blocks' partials after their releases (the
-  // acquire invalidates stale cache lines; the loads are device-scope too).
+  // n_active reads the other blocks' partials after their releases: the
+  // acquire invalidates this CU's stale cache lines, and the barrier after it
+  // orders every thread's loads after the acquire, so ordinary loads see the
+  // partials (device-scope loads were no faster).
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
   if (tid == 0) {
@@ -1267,7 +1269,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
 
   // The merge.  Each thread owns UPT float4 units (head t, dims 4d4..) and
   // issues the loads of its o partials for the first CB chunks before the
-  // (max, sum) pairs are read (device-coherent buffer loads), so both arrive
+  // (max, sum) pairs are read (buffer loads), so both arrive
   // in one memory round trip.  Wave w turns the pairs of heads w, w+4, .. into
   // chunk weights e^(m_c - M) / sum_c e^(m_c - M) l_c (lanes over chunks),
   // shared through LDS; then o = sum_c w_c o_c.  Chunks past the first CB (long
@@ -1287,7 +1289,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
 #pragma unroll
       for (int k = 0; k < UPT; ++k)
         ov[j][k] = cc < n_active ? __builtin_amdgcn_raw_buffer_load_b128(
-                                       rs_o, ((cc * G + t0) * HD + 4 * (d40 + k)) * 4, 0, kSc1)
+                                       rs_o, ((cc * G + t0) * HD + 4 * (d40 + k)) * 4, 0, 0)
                                  : af32x4{0.f, 0.f, 0.f, 0.f};
     }
   };
@@ -1305,7 +1307,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
       lc[i] = 0.f;
       if (cc < n_active) {
         const float2 v = __builtin_bit_cast(
-            float2, __builtin_amdgcn_raw_buffer_load_b64(rs_ml, (cc * G + g) * 8, 0, kSc1));
+            float2, __builtin_amdgcn_raw_buffer_load_b64(rs_ml, (cc * G + g) * 8, 0, 0));
         mc[i] = v.x;
         lc[i] = v.y;
       }
