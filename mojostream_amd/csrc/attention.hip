@@ -672,23 +672,34 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
     key_range(p, base + row, &rlo[e], &rhi[e]);
   }
 
+  // K: a wave's lanes take consecutive dims of one key (whole rows, one
+  // float4 LDS store each).  V: lanes take the 16 keys of four dim quads, so
+  // the transposed stores of a wave fall in different banks (with a wave over
+  // the dims of one key, lane l's V^T rows start 4 l * VP floats apart and
+  // every store instruction hit a few banks many times over).
   af32x4 kreg[NF], vreg[NF];
   auto tile_load = [&](int k0) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      const int idx = tid + NT * f, key = idx / (HD / 4), d4 = idx % (HD / 4);
-      const int k = k0 + key;
+      const int idx = tid + NT * f;
+      const int key = idx / (HD / 4), d4 = idx % (HD / 4);
+      const int vkey = idx % 16, vd4 = idx / 16;
+      const int k = k0 + key, vk = k0 + vkey;
       kreg[f] = af32x4{0.f, 0.f, 0.f, 0.f};
       vreg[f] = af32x4{0.f, 0.f, 0.f, 0.f};
       if (k <= khi) {
         if (k < base) {
-          const size_t o = (size_t)cache_slot(p, k) * p.kv_dim + h * HD + 4 * d4;
-          kreg[f] = aldg<af32x4>(p.kc + o);
-          vreg[f] = aldg<af32x4>(p.vc + o);
+          kreg[f] = aldg<af32x4>(p.kc + (size_t)cache_slot(p, k) * p.kv_dim + h * HD + 4 * d4);
         } else {
-          const int rr = k - base;
-          kreg[f] = aldg<af32x4>(kr + (size_t)rr * p.kv_dim + h * HD + 4 * d4);
-          vreg[f] = aldg<af32x4>(p.qkv + (size_t)rr * p.ld + p.q_dim + p.kv_dim + h * HD + 4 * d4);
+          kreg[f] = aldg<af32x4>(kr + (size_t)(k - base) * p.kv_dim + h * HD + 4 * d4);
+        }
+      }
+      if (vk <= khi) {
+        if (vk < base) {
+          vreg[f] = aldg<af32x4>(p.vc + (size_t)cache_slot(p, vk) * p.kv_dim + h * HD + 4 * vd4);
+        } else {
+          vreg[f] = aldg<af32x4>(p.qkv + (size_t)(vk - base) * p.ld + p.q_dim + p.kv_dim +
+                                 h * HD + 4 * vd4);
         }
       }
     }
@@ -696,10 +707,12 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
   auto tile_store = [&]() {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      const int idx = tid + NT * f, key = idx / (HD / 4), d4 = idx % (HD / 4);
+      const int idx = tid + NT * f;
+      const int key = idx / (HD / 4), d4 = idx % (HD / 4);
+      const int vkey = idx % 16, vd4 = idx / 16;
       *reinterpret_cast<af32x4 *>(Ks + key * KP + 4 * d4) = kreg[f];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) VT[(4 * d4 + c) * VP + key] = vreg[f][c];
+      for (int c = 0; c < 4; ++c) VT[(4 * vd4 + c) * VP + vkey] = vreg[f][c];
     }
   };
 
