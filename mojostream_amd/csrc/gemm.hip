@@ -303,17 +303,27 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 // 4wc..4wc+3 (slots j < 4) and the up panels of the same groups (j >= 4), so
 // each output's gate and up values meet in one lane.
 // ------------------------------------------------------------------------------
+//
+// PS = 16 panel slots per block, or 10 (wave tile 4 A tiles x 5 panels) for
+// launches whose 16-slot tiles leave a last round of blocks mostly empty: O
+// and Down at 2048 rows (N = 160 panels) make 1024 ten-slot tiles, two full
+// rounds, against 640 sixteen-slot ones.
+// ------------------------------------------------------------------------------
 constexpr int kGBM = 32;                     // activation rows per block
-constexpr int kGPan = 16;                    // panel slots per block
+constexpr int kGPan = 16;                    // panel slots per block (wide tile)
+constexpr int kGPanNarrow = 10;              // panel slots per block (narrow tile)
 constexpr int kGStageA = 4 * kGBM * 128;     // limb rows x 128 bytes
-constexpr int kGStageB = kGPan * 1024;       // one super-tile per panel
-constexpr int kGStage = kGStageA + kGStageB;
 constexpr int kGStages = 2;
-constexpr int kGLds = kGStages * kGStage;    // 64 KiB
 constexpr int kGNT = 256;                    // threads per block
+// one super-tile per panel slot after the A step; two stages
+constexpr int gemm_big_stage(int ps) { return kGStageA + ps * 1024; }
+constexpr int gemm_big_lds(int ps) { return kGStages * gemm_big_stage(ps); }
 
-template <int EPI>
+template <int EPI, int PS>
 __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
+  static_assert(PS == kGPan || (PS == kGPanNarrow && EPI != EPI_SWIGLU), "panel slots");
+  constexpr int PW = PS / 2;                 // panel slots per wave
+  constexpr int kGStage = gemm_big_stage(PS);
   extern __shared__ __align__(16) uint8_t lds[];
   const int M = launder(g.M), K = launder(g.K);
   const int8_t *limbs = launder(g.a.limbs);
@@ -352,7 +362,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
       *sc = half == 0 ? ss0 : ss1;
       *col = cp * 16;
     } else {
-      const int pi = blockIdx.x * kGPan + sl;
+      const int pi = blockIdx.x * PS + sl;
       const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
       const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
       *ok = pi < sn0 + sn1 + sn2;
@@ -365,17 +375,18 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
   // the panel slot of this wave's accumulator column j
   auto wslot = [&](int j) {
     if constexpr (EPI == EPI_SWIGLU) return j < 4 ? 4 * wc + j : 8 + 4 * wc + (j - 4);
-    else return 8 * wc + j;
+    else return PW * wc + j;
   };
-  // this wave loads panel slots 4 wave .. 4 wave + 3 (an invalid slot loads a
-  // valid panel: every wave issues the same number of loads per step)
-  const uint8_t *lw[4];
+  // this wave loads panel slots wave, wave + 4, .. (an invalid slot loads a
+  // valid panel)
+  constexpr int kBL = (PS + 3) / 4;  // B loads per wave per step (the most)
+  const uint8_t *lw[kBL];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kBL; ++j) {
     float sc;
     int col;
     bool ok;
-    slot(4 * wave + j, &lw[j], &sc, &col, &ok);
+    slot(wave + 4 * j < PS ? wave + 4 * j : wave, &lw[j], &sc, &col, &ok);
   }
   // A: this wave fills LDS blocks 4 wave + i (limb rows 8q .. 8q + 7); lane l
   // writes row 8q + l / 8 at chunk position l % 8, which holds chunk
@@ -395,31 +406,32 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
       __builtin_amdgcn_global_load_lds((gbl_void *)(asrc[i] + (size_t)G * 128),
                                        (lds_void *)(sa + (4 * wave + i) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds((gbl_void *)(lw[j] + (size_t)G * 1024 + lane * 16),
-                                       (lds_void *)(sa + kGStageA + (4 * wave + j) * 1024), 16,
-                                       0, 0);
+    for (int j = 0; j < kBL; ++j)
+      if (wave + 4 * j < PS)
+        __builtin_amdgcn_global_load_lds((gbl_void *)(lw[j] + (size_t)G * 1024 + lane * 16),
+                                         (lds_void *)(sa + kGStageA + (wave + 4 * j) * 1024), 16,
+                                         0, 0);
   };
 
-  v4i acc[4][8];
+  v4i acc[4][PW];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[a][j] = v4i{0, 0, 0, 0};
+    for (int j = 0; j < PW; ++j) acc[a][j] = v4i{0, 0, 0, 0};
 
   const int li = lane & 15, lg = lane >> 4;
   const int swz = (li >> 1) & 7;  // (row >> 1) & 7 for every row this lane reads
   auto compute = [&](int stg) {
     const uint8_t *sa = lds + stg * kGStage;
     const uint8_t *sb = sa + kGStageA + lane * 16;
-    u32x4 braw[8];
+    u32x4 braw[PW];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) braw[j] = *reinterpret_cast<const u32x4 *>(sb + wslot(j) * 1024);
+    for (int j = 0; j < PW; ++j) braw[j] = *reinterpret_cast<const u32x4 *>(sb + wslot(j) * 1024);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      v4i bf[8];
+      v4i bf[PW];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < PW; ++j) {
         const uint32_t d0 = braw[j][2 * h], d1 = braw[j][2 * h + 1];
         bf[j] = v4i{(int)(d0 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu),
                     (int)(d1 & 0x0F0F0F0Fu), (int)((d1 >> 4) & 0x0F0F0F0Fu)};
@@ -430,7 +442,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
         const v4i af = *reinterpret_cast<const v4i *>(sa + (64 * wr + 16 * a + li) * 128 +
                                                       pos * 16);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < PW; ++j)
           acc[a][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[a][j], 0, 0, 0);
       }
     }
@@ -458,11 +470,11 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
     rsc[a] = row < M ? (double)ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.0;
     rz[a] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
   }
-  float wsc[8];
-  int col[8];
-  bool pv[8];
+  float wsc[PW];
+  int col[PW];
+  bool pv[PW];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < PW; ++j) {
     const uint8_t *w;
     slot(wslot(j), &w, &wsc[j], &col[j], &pv[j]);
   }
@@ -487,7 +499,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
       const int row = r0 + 16 * wr + 4 * a + rr;
       if (row >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < PW; ++j) {
         if (!pv[j]) continue;
         const size_t oi = (size_t)row * ldo + col[j] + jc;
         const float x = value(a, j);
@@ -512,25 +524,55 @@ int gemm_row_pad(int M) { return (M + kGBM - 1) / kGBM * kGBM; }
 
 namespace {
 
-// The kernel for a GEMM, from a model of its time in big-tile K steps: a
-// launch of B blocks runs ceil(B / slots) rounds (two blocks per CU), and the
-// 32-row, 8-panel kernel's K step costs about 0.8 of a big one.  (A split of
-// K over several blocks, their exact partials meeting through a counter, was
-// slower: the release/acquire increments disturbed the other blocks' L2
-// traffic, and with relaxed increments the partials' round trip still cost
-// more than the shorter rounds saved.)
+// The kernel for a GEMM, from a model of its time in wide-tile K steps: a
+// launch of B blocks runs ceil(B / slots) rounds (two blocks per CU); a K step
+// of the 10-slot tile costs 0.85 of a 16-slot one (5/8 of the MFMAs, but more
+// LDS reads and barriers per MFMA), and the 32-row, 8-panel kernel's 0.8: the
+// factors that reproduce the measured choices (at 2048 rows O and Down run
+// 146 us with 16 slots, 126 us with 10; at 512 rows the 32-row kernel's 49 us
+// beat the 10-slot tile's 52).  (A split of K over several blocks, their
+// exact partials meeting through a counter or in a second launch, was
+// slower: see the notes on the measured variants.)
+constexpr double kNarrowStepCost = 0.85;
 constexpr double kSmallStepCost = 0.8;
 
-bool gemm_use_big(const GemmArgs &g, int np) {
+// 0: the 32-row kernel; else the big tile's panel slots (16 or 10)
+int gemm_pick(const GemmArgs &g, int np) {
   const bool swiglu = g.epi == EPI_SWIGLU;
   const long slots = 2L * (ctx().n_cu > 0 ? ctx().n_cu : 256);
   auto rounds = [&](long blocks) { return (double)((blocks + slots - 1) / slots); };
-  const long big = (long)(swiglu ? (np / 2 + 7) / 8 : (np + kGPan - 1) / kGPan) *
-                   (gemm_row_pad(g.M) / kGBM);
+  const long rows = gemm_row_pad(g.M) / kGBM;
+  const long wide = (long)(swiglu ? (np / 2 + 7) / 8 : (np + kGPan - 1) / kGPan) * rows;
+  const long narrow = (long)((np + kGPanNarrow - 1) / kGPanNarrow) * rows;
   const long small = (long)(swiglu ? (np / 2 + 2 * kWB - 1) / (2 * kWB)
                                    : (np + 4 * kWB - 1) / (4 * kWB)) *
                      ((g.M + kBM - 1) / kBM);
-  return rounds(big) <= rounds(small) * kSmallStepCost;
+  int pick = kGPan;
+  double cost = rounds(wide);
+  if (!swiglu && rounds(narrow) * kNarrowStepCost < cost) {
+    pick = kGPanNarrow;
+    cost = rounds(narrow) * kNarrowStepCost;
+  }
+  if (rounds(small) * kSmallStepCost < cost) pick = 0;
+  return pick;
+}
+
+template <int PS>
+void launch_big(const GemmArgs &g, int np, hipStream_t st) {
+  const int gxb = g.epi == EPI_SWIGLU ? (np / 2 + 7) / 8 : (np + PS - 1) / PS;
+  const dim3 grid(gxb, gemm_row_pad(g.M) / kGBM);
+  const size_t lds = gemm_big_lds(PS);
+  switch (g.epi) {
+    case EPI_STORE: hipLaunchKernelGGL((k_gemm_big<EPI_STORE, PS>), grid, dim3(kGNT), lds, st, g); break;
+    case EPI_ACCUMULATE:
+      hipLaunchKernelGGL((k_gemm_big<EPI_ACCUMULATE, PS>), grid, dim3(kGNT), lds, st, g);
+      break;
+    case EPI_RESID: hipLaunchKernelGGL((k_gemm_big<EPI_RESID, PS>), grid, dim3(kGNT), lds, st, g); break;
+    default:
+      if constexpr (PS == kGPan)
+        hipLaunchKernelGGL((k_gemm_big<EPI_SWIGLU, PS>), grid, dim3(kGNT), lds, st, g);
+      break;
+  }
 }
 
 }  // namespace
@@ -555,17 +597,11 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
   int np = 0;
   for (int i = 0; i < g.nseg; ++i) np += g.seg[i].n_cols / 16;
   const bool swiglu = g.epi == EPI_SWIGLU;
-  if (gemm_use_big(g, np)) {
-    const int gxb = swiglu ? (np / 2 + 7) / 8 : (np + kGPan - 1) / kGPan;
-    const dim3 grid(gxb, gemm_row_pad(g.M) / kGBM);
-#define MS_GB(E) hipLaunchKernelGGL(k_gemm_big<E>, grid, dim3(kGNT), kGLds, st, g)
-    switch (g.epi) {
-      case EPI_STORE: MS_GB(EPI_STORE); break;
-      case EPI_ACCUMULATE: MS_GB(EPI_ACCUMULATE); break;
-      case EPI_RESID: MS_GB(EPI_RESID); break;
-      default: MS_GB(EPI_SWIGLU); break;
-    }
-#undef MS_GB
+  const int pick = gemm_pick(g, np);
+  if (pick == kGPan) {
+    launch_big<kGPan>(g, np, st);
+  } else if (pick == kGPanNarrow) {
+    launch_big<kGPanNarrow>(g, np, st);
   } else {
     const dim3 blk(kNT);
     const int gy = (g.M + kBM - 1) / kBM;
