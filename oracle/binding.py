@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, never by the product package.  The oracle is the
-checker; nothing here is on the measured or shipped path.
+reference the tests compare against; nothing here is on the measured or shipped path.
 """
 from __future__ import annotations
 

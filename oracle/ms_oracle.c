@@ -1,7 +1,7 @@
 /*
  * ms_oracle.c -- CPU restatement of MojoStream's Gemma-4 layer loop.
  *
- * TEST INFRASTRUCTURE ONLY (parity checker + timed CPU baseline); see
+ * TEST INFRASTRUCTURE ONLY (parity reference + timed CPU baseline); see
  * ms_oracle.h for the pinning of each function.  Built by oracle/Makefile with
  * -ffp-contract=off so every a*b+c in the reference text is a rounded multiply
  * followed by a rounded add, independent of the host's FMA support.
@@ -242,7 +242,7 @@ void or_kv_write(const or_layer *L, const float *knew, const float *vnew,
 }
 
 /* ---- a10/a11: attention ----
- * Rows are independent given the cache and the fresh K/V, so the checker may
+ * Rows are independent given the cache and the fresh K/V, so the oracle may
  * split them over threads (or_set_threads); each row's arithmetic is the same
  * for any split. */
 typedef struct {

@@ -1,7 +1,7 @@
 /*
  * ms_oracle.h -- CPU restatement of MojoStream's Gemma-4 per-token layer loop.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity reference for the HIP
  * path and the timed CPU baseline in bench.py.  It is never linked into,
  * loaded by or called from the product library (libms_gpu.so); only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
@@ -96,7 +96,7 @@ void or_dequant_q4(const uint8_t *wq, int K, int N, float scale, float *out);
 void or_matmul_q4(float *C, const float *A, const uint8_t *wq, int M, int K,
                   int N, float scale);
 
-/* Checker-only column split of or_matmul_q4 over n threads (default 1, the
+/* Test-only column split of or_matmul_q4 over n threads (default 1, the
  * reference's decode threading).  Bit-identical results for any n. */
 void or_set_threads(int n);
 

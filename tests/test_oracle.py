@@ -397,7 +397,7 @@ def test_q4_quantize_tiny_block_rule(oracle):
     assert s == np.float32(1e-8)
 
 
-# ---- whole-model token step and the checker's threading ------------------------------
+# ---- whole-model token step and the oracle's threading ------------------------------
 def _small_model(o, n_layers=3, D=128, F=256, V=512, seed=5):
     """A 3-layer model mixing a circular window (6 slots), a linear cache with
     partial RoPE and GQA 2:1, and its tied Q4 head."""
@@ -454,8 +454,8 @@ def test_decode_token_vs_f64_model(oracle):
         tok = tid
 
 
-def test_threaded_checker_is_bit_identical(oracle):
-    """The checker's thread split (columns of a matmul, rows of attention)
+def test_threaded_oracle_is_bit_identical(oracle):
+    """The oracle's thread split (columns of a matmul, rows of attention)
     keeps every element's summation order."""
     # one loaded library: the thread count is switched between the two runs
     try:
