@@ -122,7 +122,7 @@ int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
  * rows live in a 4 MiB static device array of the library (one per GPU,
  * held until the process ends, its address taken at ms_init); a call whose
  * rows need more (M <= 16: K <= 16384 always fits; M > 16: about
- * 4 * round_up(M, 64) * K bytes) fails with MS_E_INVALID.  Same kernels and
+ * 4 * round_up(M, 32) * K bytes) fails with MS_E_INVALID.  Same kernels and
  * same results as ms_q4_matmul.  Every call on a GPU shares that array, so
  * calls that overlap on one GPU (from several host threads) race; calls on
  * the library's stream are ordered and do not. */
