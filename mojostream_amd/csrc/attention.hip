@@ -673,35 +673,42 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
   }
 
   // K: a wave's lanes take consecutive dims of one key (whole rows, one
-  // float4 LDS store each).  V: lanes take the 16 keys of four dim quads, so
-  // the transposed stores of a wave fall in different banks (with a wave over
-  // the dims of one key, lane l's V^T rows start 4 l * VP floats apart and
-  // every store instruction hit a few banks many times over).
+  // float4 LDS store each).  V (VK, head dim 256 and below): lanes take the
+  // 16 keys of four dim quads, so the transposed stores of a wave fall in
+  // different banks; with a wave over the dims of one key, lane l's V^T rows
+  // start 4 l * VP floats apart and each store instruction hits a few banks
+  // many times over.  At head dim 512 the V addresses of the key-fastest
+  // deal would spill registers, so V is dealt like K there.
+  constexpr bool VK = HD <= 256;
+  // (NT is a multiple of 16: with VK, a thread's V key is the same for every f)
+  const int vkey = tid % 16;
   af32x4 kreg[NF], vreg[NF];
   auto tile_load = [&](int k0) {
+    const int vk = k0 + vkey;
+    const float *vrow = nullptr;
+    if (VK && vk <= khi)
+      vrow = vk < base ? p.vc + (size_t)cache_slot(p, vk) * p.kv_dim + h * HD
+                       : p.qkv + (size_t)(vk - base) * p.ld + p.q_dim + p.kv_dim + h * HD;
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
       const int idx = tid + NT * f;
       const int key = idx / (HD / 4), d4 = idx % (HD / 4);
-      const int vkey = idx % 16, vd4 = idx / 16;
-      const int k = k0 + key, vk = k0 + vkey;
+      const int k = k0 + key;
       kreg[f] = af32x4{0.f, 0.f, 0.f, 0.f};
       vreg[f] = af32x4{0.f, 0.f, 0.f, 0.f};
       if (k <= khi) {
         if (k < base) {
-          kreg[f] = aldg<af32x4>(p.kc + (size_t)cache_slot(p, k) * p.kv_dim + h * HD + 4 * d4);
+          const size_t o = (size_t)cache_slot(p, k) * p.kv_dim + h * HD + 4 * d4;
+          kreg[f] = aldg<af32x4>(p.kc + o);
+          if (!VK) vreg[f] = aldg<af32x4>(p.vc + o);
         } else {
-          kreg[f] = aldg<af32x4>(kr + (size_t)(k - base) * p.kv_dim + h * HD + 4 * d4);
+          const int rr = k - base;
+          kreg[f] = aldg<af32x4>(kr + (size_t)rr * p.kv_dim + h * HD + 4 * d4);
+          if (!VK)
+            vreg[f] = aldg<af32x4>(p.qkv + (size_t)rr * p.ld + p.q_dim + p.kv_dim + h * HD + 4 * d4);
         }
       }
-      if (vk <= khi) {
-        if (vk < base) {
-          vreg[f] = aldg<af32x4>(p.vc + (size_t)cache_slot(p, vk) * p.kv_dim + h * HD + 4 * vd4);
-        } else {
-          vreg[f] = aldg<af32x4>(p.qkv + (size_t)(vk - base) * p.ld + p.q_dim + p.kv_dim +
-                                 h * HD + 4 * vd4);
-        }
-      }
+      if (VK && vrow) vreg[f] = aldg<af32x4>(vrow + 4 * (idx / 16));
     }
   };
   auto tile_store = [&]() {
@@ -709,10 +716,10 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
     for (int f = 0; f < NF; ++f) {
       const int idx = tid + NT * f;
       const int key = idx / (HD / 4), d4 = idx % (HD / 4);
-      const int vkey = idx % 16, vd4 = idx / 16;
+      const int vr = VK ? vkey : key, vd4 = VK ? idx / 16 : d4;
       *reinterpret_cast<af32x4 *>(Ks + key * KP + 4 * d4) = kreg[f];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) VT[(4 * vd4 + c) * VP + vkey] = vreg[f][c];
+      for (int c = 0; c < 4; ++c) VT[(4 * vd4 + c) * VP + vr] = vreg[f][c];
     }
   };
 
