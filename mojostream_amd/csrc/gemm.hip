@@ -302,7 +302,6 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 // EPI_SWIGLU: wave column wc holds the gate panels of column groups
 // 4wc..4wc+3 (slots j < 4) and the up panels of the same groups (j >= 4), so
 // each output's gate and up values meet in one lane.
-// ------------------------------------------------------------------------------
 //
 // PS = 16 panel slots per block, or 10 (wave tile 4 A tiles x 5 panels) for
 // launches whose 16-slot tiles leave a last round of blocks mostly empty: O
