@@ -83,7 +83,9 @@ def test_q4_matmul_vs_f64(gpu, oracle, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(48, 2560, 512), (70, 1024, 160), (256, 4096, 128),
-                                   (600, 1024, 16432)])
+                                   (600, 1024, 16432),
+                                   # 160 panels at 2048 rows: the 10-slot big tile
+                                   (2048, 1024, 2560)])
 def test_q4_gemm_rows_equal_gemv_rows(gpu, M, K, N):
     """The GEMM (M > 16) and the GEMV (row chunks of <= 16) use the same exact
     integer operands and the same scaling, so every row must agree bit for bit."""
