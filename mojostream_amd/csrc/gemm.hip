@@ -8,11 +8,13 @@
 // most of this kernel's VALU work), and the zero point comes back per row:
 // sum_k X_k (n_k - 8) = sum_k X_k n_k - 8 * xsum, with xsum = sum_k X_k from
 // the quantization.  Each limb row's dot product is exact in int32; the four
-// limbs of an output combine in int64, minus 8 * xsum, and are scaled by 2^-s
-// and the tensor scale with the GEMV's expression, so a row gets the same
-// value from this kernel as from the GEMV.
+// limbs of an output combine exactly (limb_combine: an integer below 2^51,
+// formed in double), minus 8 * xsum, and are scaled by 2^-s and the tensor
+// scale with the GEMV's expression, so a row gets the same value from these
+// kernels as from the GEMV.  launch_gemm picks the 32-row kernel (k_gemm) or
+// the big tile (k_gemm_big, described further down) per launch.
 //
-// Tiling: a block computes kBM = 32 activation rows (128 limb rows, 8 MFMA A
+// k_gemm tiling: a block computes kBM = 32 activation rows (128 limb rows, 8 MFMA A
 // tiles) by 4 kWB panels (8 panels, 128 columns).  Wave (wa, wb) owns A tiles
 // 4wa..4wa+3 and panels 4wb..4wb+3: 16 accumulators and 32 MFMAs per 128-row
 // step of K.  Both operands of a step (A 128 limb rows x 128 bytes, B one
