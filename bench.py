@@ -366,6 +366,72 @@ def bench_c5(ms, seed, steps, prompt_len):
             "prefill_ms": round(ttft, 1)}
 
 
+def bench_sparse_pin(ms, seed, steps=32, prompt_len=32):
+    """E4B-scale streaming with SparsePinEngine's pinning (sparse_pin.mojo:
+    49-330; the gemma4_e4b_infer.mojo:160-186 loop): a 42-layer E4B-shape
+    .mojostream file and its LM head file, loaded twice as streaming models,
+    once with the 24 layers of build_pinned_mask() kept in HBM and once with
+    none; each runs a seeded prompt and `steps` greedy steps, one call per
+    step.  Per token: copy time (io), the time compute waited for a copy,
+    bytes streamed, and the hit rate (pinned layer passes / all), the figures
+    the reference publishes for its SSD run (README.md:424-431)."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from mojostream_amd import streaming as st
+    d = tempfile.mkdtemp(prefix="e4b_")
+    path, lm = os.path.join(d, "e4b.mojostream"), os.path.join(d, "lm_head.bin")
+    t0 = time.perf_counter()
+    st.write_synthetic_e4b(path, 42, seed=seed)
+    st.write_synthetic_lm_head(lm, 2560, 262144, seed=seed)
+    log(f"sparse-pin: E4B file written in {time.perf_counter() - t0:.1f}s")
+    prompt = [int(v % 262144) for v in ms.host_random_u8(4 * prompt_len, 9, 81).view(np.uint32)]
+    out = {"workload": "E4B-shape .mojostream file (42 layers, 1.97 GB Q4) streamed from pinned "
+                       "host memory through 2 HBM slots; tied Q4 head resident",
+           "prompt_tokens": prompt_len, "decode_steps": steps,
+           "reference_ssd_run": {"ms_per_token": 1843, "io_mb_per_token": 826,
+                                 "hit_rate": 0.571}}
+    try:
+        for name, mask in (("pinned_24", st.build_pinned_mask()), ("streamed_all", None)):
+            max_pos = prompt_len + steps + 8
+            t0 = time.perf_counter()
+            m = st.load_model(path, lm_head_path=lm, vocab=262144, max_rows=16, max_pos=max_pos,
+                              max_len=max_pos, resident=False, pinned=mask)
+            load_s = time.perf_counter() - t0
+            tok = m.prefill(prompt, 0)
+            io = wait = total = nbytes = 0.0
+            hits = passes = 0
+            t0 = time.perf_counter()
+            for k in range(steps):
+                o = (m.decode([tok], [prompt_len], 1) if k == 0 else m.decode_continue(1, 1))
+                tok = int(o[0, 0])
+                s = m.stream_stats()
+                io += s["io_ms"]
+                wait += s["wait_ms"]
+                total += s["total_ms"]
+                nbytes += s["bytes"]
+                hits += s["layers_pinned"]
+                passes += s["layers_pinned"] + s["layers_streamed"]
+            dt = time.perf_counter() - t0
+            m.close()
+            r = {"ms_per_token": round(dt * 1e3 / steps, 2),
+                 "tokens_per_s": round(steps / dt, 2),
+                 "io_ms_per_token": round(io / steps, 2),
+                 "wait_ms_per_token": round(wait / steps, 2),
+                 "compute_ms_per_token": round((total - wait) / steps, 2),
+                 "streamed_mb_per_token": round(nbytes / steps / 1e6, 1),
+                 "stream_gbps": round(nbytes / (io * 1e-3) / 1e9, 1) if io > 0 else None,
+                 "hit_rate": round(hits / passes, 3),
+                 "load_s": round(load_s, 2)}
+            log(f"sparse-pin {name}: {r['ms_per_token']} ms/token, io {r['io_ms_per_token']} ms, "
+                f"wait {r['wait_ms_per_token']} ms, {r['streamed_mb_per_token']} MB/token, "
+                f"hit rate {r['hit_rate']}")
+            out[name] = r
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -380,9 +446,10 @@ def main():
                     help="demo decode harness section (config 1)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time the decode with eager launches")
-    ap.add_argument("--only", choices=["all", "decode", "ttft", "c5"], default="all",
+    ap.add_argument("--only", choices=["all", "decode", "ttft", "c5", "sparse-pin"],
+                    default="all",
                     help="decode: batch-1 decode only; ttft: prefill (TTFT) only; c5: the 14B "
-                         "streaming section only")
+                         "streaming section only; sparse-pin: the E4B pinning section only")
     ap.add_argument("--prof-tokens", type=int, default=16)
     ap.add_argument("--rocpd-summary", metavar="DB", help="summarize a rocprofv3 database and exit")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -395,6 +462,8 @@ def main():
     ap.add_argument("--c5-steps", type=int, default=256,
                     help="decode steps of the 14B streaming section (0: skip it)")
     ap.add_argument("--c5-prompt", type=int, default=3840)
+    ap.add_argument("--sparse-pin-steps", type=int, default=32,
+                    help="decode steps of the E4B sparse-pinning streaming section (0: skip it)")
     args = ap.parse_args()
     if args.rocpd_summary:
         print(rocpd_summary(args.rocpd_summary, args.steps))
@@ -422,6 +491,11 @@ def main():
     if args.only == "c5":
         print(json.dumps({"c5_streaming_14b": bench_c5(ms, args.seed, args.c5_steps,
                                                          args.c5_prompt), "device": name}))
+        return
+    if args.only == "sparse-pin":
+        print(json.dumps({"e4b_sparse_pin": bench_sparse_pin(ms, args.seed,
+                                                             args.sparse_pin_steps),
+                          "device": name}))
         return
     if args.only == "ttft":
         ttft = measure_ttft(ms, sorted({args.ttft_prompt, 2048}), args.seed)
@@ -535,6 +609,8 @@ def main():
             out["c1_harness"] = bench_c1(ms)
         if args.c5_steps > 0:
             out["c5_streaming_14b"] = bench_c5(ms, args.seed, args.c5_steps, args.c5_prompt)
+        if args.sparse_pin_steps > 0:
+            out["e4b_sparse_pin"] = bench_sparse_pin(ms, args.seed, args.sparse_pin_steps)
     else:
         m.close()
 

@@ -117,8 +117,9 @@ int ms_dequant_q4_packed(float *d_out, const uint8_t *d_packed, int K, int N,
 int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
                  int K, int N, float scale, int accumulate);
 /* ms_q4_matmul without any allocation.  No counterpart in the reference: it is
- * for callers that cannot allocate device memory (code under HIP graph
- * capture, serving loops, harnesses that forbid hipMalloc).  The quantized
+ * for callers that cannot allocate device memory (serving loops, harnesses
+ * that forbid hipMalloc).  Its kernels run on the library's own stream, so a
+ * graph the caller captures on another stream does not record them.  The quantized
  * rows live in a 4 MiB static device array of the library (one per GPU,
  * held until the process ends, its address taken at ms_init); a call whose
  * rows need more (M <= 16: K <= 16384 always fits; M > 16: about
@@ -457,14 +458,55 @@ int ms_lm_head_file_write_synthetic(const char *path, int hidden, int vocab,
 
 /* ---- streaming statistics ------------------------------------------------ */
 typedef struct {
-  double io_ms;        /* host->HBM copy time of the last ms_forward/decode call */
-  double compute_ms;   /* kernel time */
+  double io_ms;        /* host->HBM copy time of the last ms_forward / ms_prefill /
+                          ms_decode_run call (summed over its layer passes) */
+  double compute_ms;   /* wall time minus wait */
   double wait_ms;      /* time compute waited for a copy (measured with events) */
   double total_ms;
+  double bytes;        /* bytes copied host->HBM */
+  int layers_streamed; /* layer passes whose weights came through an HBM slot */
+  int layers_pinned;   /* layer passes of pinned (resident) layers: the hits of
+                          SparsePinEngine's pass statistics, sparse_pin.mojo:136-330 */
 } ms_stream_stats;
 /* I/O vs compute of the last call (run_streaming_bench stream_runner.mojo:503-546
- * reports the same split analytically). */
+ * reports the same split analytically).  Zero for a resident model. */
 int ms_model_stream_stats(ms_model *m, ms_stream_stats *out);
+
+/* ---- ModelRunner: double-buffered layer files ----------------------------- */
+/* ModelRunner (loader.mojo:47-144).  n_layers square N x N Q4 matrices, one
+ * per file <base_path>/layer_<i>.bin ([f32 scale][N * N/2 row-major bytes],
+ * the "row-major" layer files of create_fake_model.py:126-140), two HBM slots.
+ * N % 128 == 0. */
+typedef struct ms_runner ms_runner;
+typedef struct {
+  double load_ms;     /* LayerStats.load_ns: loading the next layer (host file read
+                         and repack + host->HBM copy); 0 for the last layer */
+  double compute_ms;  /* LayerStats.compute_ns: C += A . deq(W) of this layer */
+  double wait_ms;     /* LayerStats.wait_ns: measured idle time of the compute
+                         stream before the next layer (the reference models it as
+                         max(0, load_next - compute)) */
+} ms_layer_stats;
+/* ModelRunner.__init__ (loader.mojo:59-76): two slots of N * N/2 bytes. */
+int ms_runner_create(const char *base_path, int n_layers, int N, ms_runner **out);
+int ms_runner_destroy(ms_runner *r);
+/* load_into_slot (loader.mojo:82-94): layer idx into slot 0 or 1, synchronous;
+ * *load_ms the wall time.  A missing or short file is MS_E_IO (the reference
+ * raises). */
+int ms_runner_load_into_slot(ms_runner *r, int slot, int idx, double *load_ms);
+/* ModelRunner.active (loader.mojo:52): the slot compute_active reads. */
+int ms_runner_set_active(ms_runner *r, int slot);
+int ms_runner_active(const ms_runner *r, int *slot);
+/* compute_active (loader.mojo:97-106): C [M][N] += A [M][N] . deq(W_active);
+ * *compute_ms the device time (events on the library stream). */
+int ms_runner_compute_active(ms_runner *r, float *d_C, const float *d_A, int M,
+                             double *compute_ms);
+/* run_pipeline (loader.mojo:115-144): layer 0 loaded cold into slot 0; then
+ * per layer i: C += A . deq(W_i) on the active slot, C zeroed, the slots
+ * flipped, while layer i+1 loads into the other slot on the copy stream (a
+ * real overlap; the reference times the two in sequence).  stats[n_layers].
+ * d_taps (or null): [n_layers][M][N], C of each layer before the zeroing. */
+int ms_runner_run_pipeline(ms_runner *r, float *d_C, const float *d_A, int M,
+                           ms_layer_stats *stats, float *d_taps);
 
 /* ---- profiling ------------------------------------------------------------ */
 /* When enabled, ms_decode_run (eager mode) records HIP events around every

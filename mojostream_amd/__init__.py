@@ -52,7 +52,8 @@ class ModelDesc(C.Structure):
 
 class StreamStats(C.Structure):
     _fields_ = [("io_ms", C.c_double), ("compute_ms", C.c_double),
-                ("wait_ms", C.c_double), ("total_ms", C.c_double)]
+                ("wait_ms", C.c_double), ("total_ms", C.c_double), ("bytes", C.c_double),
+                ("layers_streamed", C.c_int), ("layers_pinned", C.c_int)]
 
 
 class FileMeta(C.Structure):
@@ -157,6 +158,12 @@ _SIGS = {
     "ms_token_map_load": [C.c_char_p, _P], "ms_token_map_free": [_P],
     "ms_token_map_size": [_P, _P], "ms_token_map_decode": [_P, _I, _P, _I, _P],
     "ms_model_set_lm_head_f32": [_P, _P, _I, _P],
+    "ms_runner_create": [C.c_char_p, _I, _I, C.POINTER(C.c_void_p)],
+    "ms_runner_destroy": [_P],
+    "ms_runner_load_into_slot": [_P, _I, _I, C.POINTER(C.c_double)],
+    "ms_runner_set_active": [_P, _I], "ms_runner_active": [_P, _IP],
+    "ms_runner_compute_active": [_P, _P, _P, _I, C.POINTER(C.c_double)],
+    "ms_runner_run_pipeline": [_P, _P, _P, _I, _P, _P],
     "ms_prof_enable": [_I],
     "ms_prof_sweep": [_P, _I, _I, C.POINTER(C.c_double), C.POINTER(C.c_double),
                       C.POINTER(C.c_long)],
@@ -636,7 +643,8 @@ class Model:
         s = StreamStats()
         check(_lib.ms_model_stream_stats(self.h, C.byref(s)))
         return dict(io_ms=s.io_ms, compute_ms=s.compute_ms, wait_ms=s.wait_ms,
-                    total_ms=s.total_ms)
+                    total_ms=s.total_ms, bytes=s.bytes, layers_streamed=s.layers_streamed,
+                    layers_pinned=s.layers_pinned)
 
 
 def prof_enable(on: bool) -> None:

@@ -46,6 +46,24 @@ inline size_t attn_part_floats(int B, int n_kv, int n_chunks, int T, int G, int 
   return (size_t)B * n_kv * ((size_t)n_chunks * T * G * (hd + 2) + 4);
 }
 
+// Decode at one row per sequence with the merge left to the consumer: one
+// block per (32-key chunk, sequence x kv head) writes the chunk's unnormalized
+// o = sum_k e^(s_k - m) v_k and (m, l = sum_k e^(s_k - m)) per query head, and
+// the block holding the current slot appends the row's k and v to the cache.
+// The O projection merges the chunks (AttnSrc in q4.h).  Per sequence, at
+// a.part: o [kDecPartMaxChunks][n_heads][hd], then (m, l)
+// [kDecPartMaxChunks][n_heads][2].  Needs G <= 4 and at most kDecPartMaxChunks
+// launched chunks (dec_part_ok).
+constexpr int kDecPartChunk = 32;
+constexpr int kDecPartMaxChunks = 64;
+inline size_t dec_part_floats(int B, int n_heads, int hd) {
+  return (size_t)B * kDecPartMaxChunks * n_heads * (hd + 2);
+}
+// Chunks a partials launch covers (the host's position bound, else the cache).
+int dec_part_chunks(const AttnArgs &a);
+bool dec_part_ok(const AttnArgs &a);
+int launch_attention_partials(const AttnArgs &a, hipStream_t st);
+
 // T == 1 (decode): one launch; the chunk blocks append the row to the cache and
 // the last block of each (sequence, kv head) merges the chunks (needs a.ctr).
 // T > 1: scores + chunk softmax + P.V partials, then the merge of the chunks

@@ -1294,11 +1294,14 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
   // chunk weights e^(m_c - M) / sum_c e^(m_c - M) l_c (lanes over chunks),
   // shared through LDS; then o = sum_c w_c o_c.  Chunks past the first CB (long
   // linear caches) follow in further batches.
+  // NUG unit groups of 256 * UPT units: more than one only at head dim 512
+  // with more than 16 query heads per kv head (the first group's loads go out
+  // before the weights, later groups' after them).
   constexpr int UPT = dec_units_per_thread(HD, TGM);
   constexpr int CB = dec_merge_batch(UPT);
-  const int u0 = tid * UPT;
-  const int t0 = u0 / H4, d40 = u0 % H4;
-  const bool owner = u0 < nu;
+  constexpr int NUG = (TGM * HD / 4 + 256 * UPT - 1) / (256 * UPT);
+  int u0 = tid * UPT;
+  int t0 = u0 / H4, d40 = u0 % H4;
   af32x4 ov[CB][UPT];
   auto load_o = [&](int c0) {
 #pragma unroll
@@ -1313,7 +1316,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
                                  : af32x4{0.f, 0.f, 0.f, 0.f};
     }
   };
-  if (owner) load_o(0);
+  if (u0 < nu) load_o(0);
   const __amdgpu_buffer_rsrc_t rs_ml =
       __builtin_amdgcn_make_buffer_rsrc(pml, 0, p.n_chunks * G * 2 * 4, 0x00020000);
   const int wave = tid >> 6, lane = tid & 63;
@@ -1350,27 +1353,290 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
     }
   }
   __syncthreads();
-  if (!owner) return;
-  float4 oacc[UPT];
 #pragma unroll
-  for (int k = 0; k < UPT; ++k) oacc[k] = float4{0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0; c0 < n_active; c0 += CB) {
-    if (c0 > 0) load_o(c0);
+  for (int ug = 0; ug < NUG; ++ug) {
+    if (ug > 0) {
+      u0 = (tid + 256 * ug) * UPT;
+      t0 = u0 / H4;
+      d40 = u0 % H4;
+    }
+    if (u0 >= nu) return;
+    float4 oacc[UPT];
 #pragma unroll
-    for (int j = 0; j < CB; ++j) {
-      const float w = c0 + j < n_active ? wsh[(c0 + j) * G + t0] : 0.f;
+    for (int k = 0; k < UPT; ++k) oacc[k] = float4{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < n_active; c0 += CB) {
+      if (c0 > 0 || ug > 0) load_o(c0);
 #pragma unroll
-      for (int k = 0; k < UPT; ++k) {
-        oacc[k].x += w * ov[j][k].x;
-        oacc[k].y += w * ov[j][k].y;
-        oacc[k].z += w * ov[j][k].z;
-        oacc[k].w += w * ov[j][k].w;
+      for (int j = 0; j < CB; ++j) {
+        const float w = c0 + j < n_active ? wsh[(c0 + j) * G + t0] : 0.f;
+#pragma unroll
+        for (int k = 0; k < UPT; ++k) {
+          oacc[k].x += w * ov[j][k].x;
+          oacc[k].y += w * ov[j][k].y;
+          oacc[k].z += w * ov[j][k].z;
+          oacc[k].w += w * ov[j][k].w;
+        }
       }
+    }
+#pragma unroll
+    for (int k = 0; k < UPT; ++k)
+      if (u0 + k < nu) *reinterpret_cast<float4 *>(orow + 4 * (u0 + k)) = oacc[k];
+  }
+}
+
+// ------------------------------------------------------------------------------
+// k_attn_part: the decode attention of one row per sequence without the merge.
+// Block (c, b x h): cache slots 32c..32c+31 of sequence b, kv head h, for its
+// G <= 4 query heads.  Like k_attn_decode, the chunk's cached rows, q and the
+// fresh k, v are loaded before the position arrives (the host launches only
+// the chunks below its bound on the position), rows past the attended ones
+// are zeroed, and the slot of the current position takes the fresh row (and
+// appends it to the cache).  Then scores (dot over the head dim, 8 lanes per
+// key), the chunk's softmax numerators (max and sum over its keys) and
+// o = sum_k e^(s_k - m) v_k, stored with (m, l) per query head.  The consumer
+// (the O projection) merges the chunks, so no block waits for another.
+// ------------------------------------------------------------------------------
+// sum / max over the 8 lanes of each half-row (quad permutes, then the
+// half-row mirror)
+__device__ inline float row8_sum(float v) {
+  v += adpp<0xB1>(v);
+  v += adpp<0x4E>(v);
+  return v + adpp<0x141>(v);
+}
+
+template <int HD, int CH>
+__global__ __launch_bounds__(256) void k_attn_part(AttnArgs args) {
+  extern __shared__ __align__(16) float lds[];
+  static_assert(CH == 16 || CH == 32, "16 or 32 keys per chunk");
+  constexpr int LPK = 256 / CH;          // lanes per key in the scores
+  constexpr int TGM = 4;
+  constexpr int F4 = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
+  constexpr int NV = HD / (4 * LPK);     // float4 per thread per key (scores)
+  constexpr int DPT = (HD + 255) / 256;  // head dims per thread (fresh row)
+  constexpr int H4 = HD / 4;
+  constexpr int UPT = (TGM * H4 + 255) / 256;  // P.V float4 units per thread
+  // key rows in LDS at a pitch of HD + 32 floats: the 16 lanes of one LDS
+  // read pass (two keys, eight dim groups each) fall in distinct banks
+  constexpr int KP = HD + 32;
+  const AttnP p = load_params(args);
+  const int tid = threadIdx.x;
+  const int c = blockIdx.x;
+  const int b = (int)blockIdx.y / p.n_kv, h = (int)blockIdx.y % p.n_kv;
+  const int G = p.G;
+  const int L = p.cache_len;
+  const int nq = G * HD;
+
+  float *sk = lds;              // [CH][KP] keys of the chunk
+  float *sv = sk + CH * KP;     // [CH][HD] values
+  float *sq = sv + CH * HD;     // [TGM][HD] rotated queries
+  float *ss = sq + TGM * HD;    // [TGM][CH] scores -> numerators
+  float *sm = ss + TGM * CH;    // [TGM]
+  float *sl = sm + TGM;         // [TGM]
+  const size_t cbase = (size_t)b * p.cache_seq_stride;
+  const float *qrow = p.qkv + (size_t)b * p.ld;
+
+  // ---- loads that do not depend on the position
+  const int base = aldg<int32_t>(p.pos + b);
+  float4 kr[F4], vr[F4];
+#pragma unroll
+  for (int j = 0; j < F4; ++j) {
+    kr[j] = float4{0.f, 0.f, 0.f, 0.f};
+    vr[j] = float4{0.f, 0.f, 0.f, 0.f};
+    const int f = tid + 256 * j;
+    const int slot = c * CH + f / H4, d4 = f % H4;
+    if (slot < L) {
+      const size_t off = cbase + (size_t)slot * p.kv_dim + h * HD + 4 * d4;
+      kr[j] = aldg<float4>(p.kc + off);
+      vr[j] = aldg<float4>(p.vc + off);
+    }
+  }
+  constexpr int QPT = TGM * HD / 256;  // q elements per thread
+  float qx[QPT], qy[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int e = tid + 256 * u;
+    qx[u] = qy[u] = 0.f;
+    if (e < nq) {
+      const int g = e / HD, d = e % HD;
+      const float *qh = qrow + (h * G + g) * HD;
+      qx[u] = aldg<float>(qh + d);
+      qy[u] = aldg<float>(qh + rope_partner(p, d));
+    }
+  }
+  float kx[DPT], ky[DPT], vx[DPT];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = tid + 256 * j;
+    kx[j] = ky[j] = vx[j] = 0.f;
+    if (d < HD) {
+      const float *kh = qrow + p.q_dim + h * HD;
+      kx[j] = aldg<float>(kh + d);
+      ky[j] = aldg<float>(kh + rope_partner(p, d));
+      vx[j] = aldg<float>(qrow + p.q_dim + p.kv_dim + h * HD + d);
+    }
+  }
+
+  // ---- the position: attended slots [0, nslots), the slot of this row
+  int lo, hi;
+  key_range(p, base, &lo, &hi);
+  const int nslots = p.circular ? min(L, base + 1) : min(hi + 1, L);
+  const int n_active = min((nslots + CH - 1) / CH, p.grid_chunks);
+  if (c >= n_active) return;
+  const int fslot = p.circular ? base % L : base;
+  const bool fresh_here = fslot < nslots && fslot / CH == c;
+  float qc[QPT], qs[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int e = tid + 256 * u;
+    qc[u] = 1.f;
+    qs[u] = 0.f;
+    if (e < nq) rope_cs(p, e % HD, base, qc[u], qs[u]);
+  }
+  float kc_[DPT], ks_[DPT];
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    const int d = tid + 256 * j;
+    kc_[j] = 1.f;
+    ks_[j] = 0.f;
+    if (fresh_here && d < HD) rope_cs(p, d, base, kc_[j], ks_[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < F4; ++j) {
+    const int f = tid + 256 * j;
+    const int slot = c * CH + f / H4;
+    if (slot >= nslots) {
+      kr[j] = float4{0.f, 0.f, 0.f, 0.f};
+      vr[j] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (!(fresh_here && slot == fslot)) {
+      const int kl = f / H4;  // key of the chunk
+      *reinterpret_cast<float4 *>(sk + kl * KP + 4 * (f % H4)) = kr[j];
+      reinterpret_cast<float4 *>(sv)[f] = vr[j];
     }
   }
 #pragma unroll
-  for (int k = 0; k < UPT; ++k)
-    if (u0 + k < nu) *reinterpret_cast<float4 *>(orow + 4 * (u0 + k)) = oacc[k];
+  for (int u = 0; u < QPT; ++u) {
+    const int e = tid + 256 * u;
+    sq[e] = e < nq ? rope_mix(p, e % HD, qx[u], qy[u], qc[u], qs[u]) : 0.f;
+  }
+  if (fresh_here) {
+    // write_kv_sliding / write_kv_full (gemma4_e4b.mojo:211-249)
+    const int kf = fslot - c * CH;
+    const size_t off = cbase + (size_t)fslot * p.kv_dim + h * HD;
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) {
+      const int d = tid + 256 * j;
+      if (d < HD) {
+        const float kv = rope_mix(p, d, kx[j], ky[j], kc_[j], ks_[j]);
+        sk[kf * KP + d] = kv;
+        sv[kf * HD + d] = vx[j];
+        if (p.write_cache) {
+          p.kc[off + d] = kv;
+          p.vc[off + d] = vx[j];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- scores: thread (key kk, dim group dg of LPK lanes), sums by DPP
+  const int kk = tid / LPK, dg = tid % LPK;
+  float acc[TGM];
+#pragma unroll
+  for (int t = 0; t < TGM; ++t) acc[t] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int d = dg * 4 + 4 * LPK * i;
+    const float4 kv = *reinterpret_cast<const float4 *>(sk + kk * KP + d);
+#pragma unroll
+    for (int t = 0; t < TGM; ++t) {
+      const float4 qq = *reinterpret_cast<const float4 *>(sq + t * HD + d);
+      acc[t] += qq.x * kv.x + qq.y * kv.y + qq.z * kv.z + qq.w * kv.w;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TGM; ++t) acc[t] = LPK == 8 ? row8_sum(acc[t]) : row16_sum(acc[t]);
+  if (dg == 0) {
+    const bool ok = c * CH + kk < nslots;
+#pragma unroll
+    for (int t = 0; t < TGM; ++t)
+      if (t < G) ss[t * CH + kk] = ok ? acc[t] * p.scale : -INFINITY;
+  }
+  __syncthreads();
+  // numerators of the chunk: query head t on CH lanes, lane = key; max and
+  // sum over the chunk's keys (a row of 16 by DPP, two rows by one exchange)
+  if (tid < CH * TGM) {
+    const int t = tid / CH, k = tid % CH;
+    const float sc = t < G ? ss[t * CH + k] : -INFINITY;
+    float m = row16_max(sc);
+    if (CH == 32) m = fmaxf(m, __shfl_xor(m, 16, 64));
+    const float pr = (sc == -INFINITY) ? 0.f : expf(sc - m);
+    float l = row16_sum(pr);
+    if (CH == 32) l += __shfl_xor(l, 16, 64);
+    if (t < G) {
+      ss[t * CH + k] = pr;
+      if (k == 0) {
+        sm[t] = m;
+        sl[t] = l;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- P.V on float4 units (head t, dims 4u..4u+3), stored per query head
+  const int nhq = p.n_heads;
+  float *po = p.part + (size_t)b * kDecPartMaxChunks * nhq * (HD + 2);
+  float *pml = po + (size_t)kDecPartMaxChunks * nhq * HD;
+  const float4 *sv4 = reinterpret_cast<const float4 *>(sv);
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) {
+    const int u = tid + 256 * j;
+    if (u >= G * H4) break;
+    const int t = u / H4, d4 = u % H4;
+    float4 o = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int k = 0; k < CH; ++k) {
+      const float pk = ss[t * CH + k];
+      const float4 v = sv4[k * H4 + d4];
+      o.x += pk * v.x;
+      o.y += pk * v.y;
+      o.z += pk * v.z;
+      o.w += pk * v.w;
+    }
+    *reinterpret_cast<float4 *>(po + ((size_t)c * nhq + h * G + t) * HD + 4 * d4) = o;
+  }
+  if (tid < G)
+    *reinterpret_cast<float2 *>(pml + ((size_t)c * nhq + h * G + tid) * 2) =
+        float2{sm[tid], sl[tid]};
+}
+
+int dec_part_chunks(const AttnArgs &a) {
+  const int reach = a.pos_bound > 0 ? std::min(a.pos_bound, a.cache_len) : a.cache_len;
+  return std::max(1, (reach + kDecPartChunk - 1) / kDecPartChunk);
+}
+
+bool dec_part_ok(const AttnArgs &a) {
+  const int G = a.n_kv > 0 ? a.n_heads / a.n_kv : 0;
+  return a.T == 1 && G >= 1 && G <= 4 && a.n_heads % a.n_kv == 0 &&
+         (a.hd == 128 || a.hd == 256 || a.hd == 512) && a.rot % 2 == 0 && a.rot <= a.hd &&
+         a.ld >= a.q_dim + 2 * a.kv_dim && dec_part_chunks(a) <= kDecPartMaxChunks;
+}
+
+int launch_attention_partials(const AttnArgs &a, hipStream_t st) {
+  MS_CHECK_ARG(dec_part_ok(a), "attention partials: unsupported shape");
+  MS_CHECK_ARG(a.qkv && a.part && a.pos && a.kc && a.vc, "attention partials: missing buffers");
+  AttnArgs a2 = a;
+  a2.grid_chunks = dec_part_chunks(a);
+  const dim3 grid(a2.grid_chunks, a.B * a.n_kv);
+  constexpr int CH = kDecPartChunk;
+  const size_t shmem = (size_t)(CH * (2 * a.hd + 32) + 4 * a.hd + 4 * CH + 8) * 4;
+  switch (a.hd) {
+    case 128: hipLaunchKernelGGL((k_attn_part<128, CH>), grid, dim3(256), shmem, st, a2); break;
+    case 256: hipLaunchKernelGGL((k_attn_part<256, CH>), grid, dim3(256), shmem, st, a2); break;
+    default: hipLaunchKernelGGL((k_attn_part<512, CH>), grid, dim3(256), shmem, st, a2); break;
+  }
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
 }
 
 static size_t attn_decode_lds(const AttnArgs &a, int tgm) {

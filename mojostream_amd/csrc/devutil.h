@@ -37,6 +37,10 @@ __device__ inline T launder(T v) {
   return v;
 }
 
+// Low nibbles of the four bytes of d as bytes 0..15 (the zero point is added
+// separately, with a constant -8 operand).
+__device__ inline int nib_u8(uint32_t d) { return (int)(d & 0x0F0F0F0Fu); }
+
 // Low nibbles of the four bytes of d as signed bytes n - 8 (the Q4 zero point
 // folded into the operand): n + 0x78 stays inside its byte for n <= 15, and
 // flipping bit 7 turns it into the two's complement of n - 8.

@@ -79,6 +79,7 @@ struct Prof {
   AttnArgs last_attn[2] = {};
   int last_attn_layer[2] = {};
   bool have_attn[2] = {};
+  bool attn_part[2] = {};  // that launch left its chunks to the O projection
   int layer = -1;
 };
 static Prof g_prof;
@@ -234,6 +235,11 @@ struct RunCfg {
   int pos_bound;            // every row's position is below it (decode attention
                             // launches only the key chunks below it)
   float *tap_last;          // optional [n_layers][D]: each layer's last output row
+  // one row of one sequence (a batch-1 decode step), where the layer's shapes
+  // allow it: the attention leaves its key chunks unmerged and the O
+  // projection merges them (k_attn_part + AS_ATTN); Q|K|V, Gate|Up and Down
+  // quantize their input row per wave (AS_WAVES)
+  bool one_row;
 };
 
 // Launch a projection of rows r: quantized in the kernel's prologue with
@@ -247,6 +253,11 @@ static int launch_gemv_rec(const GemvArgs &a, hipStream_t st) {
   }
   return launch_gemv(a, st);
 }
+
+// One row of one sequence with the row quantized per wave (AS_WAVES) when the
+// shapes fit (K = waves * 640), else launch_proj.
+static int launch_proj_row(ms_model *m, const RunCfg &rc, GemvArgs a, const RowSrc &r,
+                           int waves, int waves_row, hipStream_t st);
 
 static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipStream_t st) {
   constexpr size_t kLdsLimit = 150 * 1024;
@@ -280,6 +291,17 @@ static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipS
   a.waves = (a.M <= 4 && a.P == 1 && a.epi == EPI_RESID && waves == 16) ? 16 : 4;
   if (int rc = launch_quant_rows(r, a.M, a.K, a.q, st)) return rc;
   return launch_gemv_rec(a, st);
+}
+
+static int launch_proj_row(ms_model *m, const RunCfg &rc, GemvArgs a, const RowSrc &r,
+                           int waves, int waves_row, hipStream_t st) {
+  if (rc.one_row && a.M == 1 && a.K == waves_row * kWaveTiles * kSuperK) {
+    a.asrc = AS_WAVES;
+    a.rows = r;
+    a.waves = waves_row;
+    return launch_gemv_rec(a, st);
+  }
+  return launch_proj(m, a, r, waves, st);
 }
 
 // Rows entering layer l: the previous layer's output or the call's input rows.
@@ -316,9 +338,10 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.out = m->qkv;
     a.ldo = ld;
     ProfScope ps(PC_QKV, (double)D * ld / 2, st);
-    if (int rc2 = launch_proj(m, a, r, 8, st)) return rc2;
+    if (int rc2 = launch_proj_row(m, rc, a, r, 8, 4, st)) return rc2;
   }
   // 2. attention (chunks + merge/cache append)
+  bool merged_in_o = false;
   {
     AttnArgs a{};
     a.B = rc.B;
@@ -351,7 +374,19 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.pos_bound = rc.pos_bound;
     // KV bytes read at the current position are counted by bench.py
     ProfScope ps(PC_ATTN, 0.0, st);
-    if (rc.B == 1 && rc.T > kGemvMaxM && m->fq && prefill_flash_ok(a)) {
+    if (rc.one_row && rc.B == 1 && rc.T == 1 && d.n_heads == 8 &&
+        d.q_dim == 8 * d.head_dim && dec_part_ok(a)) {
+      // chunk partials only; the O projection below merges them
+      if (g_prof.on) {
+        const int k = d.cache_kind == MS_CACHE_CIRCULAR ? 1 : 0;
+        g_prof.last_attn[k] = a;
+        g_prof.last_attn_layer[k] = l;
+        g_prof.have_attn[k] = true;
+        g_prof.attn_part[k] = true;
+      }
+      if (int rc2 = launch_attention_partials(a, st)) return rc2;
+      merged_in_o = true;
+    } else if (rc.B == 1 && rc.T > kGemvMaxM && m->fq && prefill_flash_ok(a)) {
       // prefill rows: flash attention on fp32 MFMA
       if (int rc2 = launch_attention_prefill(a, m->fq, m->fk, m->fpart, m->fpart_floats, st))
         return rc2;
@@ -361,6 +396,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
         g_prof.last_attn[k] = a;
         g_prof.last_attn_layer[k] = l;
         g_prof.have_attn[k] = true;
+        g_prof.attn_part[k] = false;
       }
       if (int rc2 = launch_attention(a, st)) return rc2;
     } else {
@@ -393,7 +429,25 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.ldo = D;
     a.resid = m->xn;
     ProfScope ps(PC_O, (double)d.q_dim * D / 2, st);
-    if (int rc2 = launch_proj(m, a, r, 8, st)) return rc2;
+    if (merged_in_o) {
+      // the attention chunks merged per head in the O projection's prologue
+      a.asrc = AS_ATTN;
+      a.waves = 8;
+      a.at.part = m->attn_part;
+      a.at.pos = m->pos + rc.seq0;
+      a.at.hd = d.head_dim;
+      a.at.n_heads = d.n_heads;
+      a.at.circular = d.cache_kind == MS_CACHE_CIRCULAR;
+      a.at.cache_len = d.cache_len;
+      a.at.clamp = d.clamp_reads;
+      AttnArgs pa{};
+      pa.cache_len = d.cache_len;
+      pa.pos_bound = rc.pos_bound;
+      a.at.chunks = dec_part_chunks(pa);
+      if (int rc2 = launch_gemv_rec(a, st)) return rc2;
+    } else if (int rc2 = launch_proj(m, a, r, 8, st)) {
+      return rc2;
+    }
   }
   // 4. x2n = rmsnorm(x2) in the prologue, Gate|Up, SwiGLU epilogue
   {
@@ -414,7 +468,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.sw_out = m->aF;
     a.ldo_sw = F;
     ProfScope ps(PC_GATEUP, (double)D * F, st);
-    if (int rc2 = launch_proj(m, a, r, 4, st)) return rc2;
+    if (int rc2 = launch_proj_row(m, rc, a, r, 4, 4, st)) return rc2;
   }
   // 5. x_out = x2n + ffn . Wd (residual epilogue): the layer output
   {
@@ -434,7 +488,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.resid = m->x2n;
     if (rc.hidden) a.out2 = rc.hidden + (size_t)(l - rc.first_layer) * M * D;
     ProfScope ps(PC_DOWN, (double)F * D / 2, st);
-    if (int rc2 = launch_proj(m, a, r, 16, st)) return rc2;
+    if (int rc2 = launch_proj_row(m, rc, a, r, 16, 16, st)) return rc2;
   }
   return MS_OK;
 }
@@ -579,8 +633,8 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
   const bool streaming = !m->d.resident;
   const int l0 = rc.first_layer, l1 = rc.first_layer + rc.n_layers;
   if (streaming) {
-    // per-call timing: [copy start, copy end] per layer and compute waits
-    m->stats = ms_stream_stats{};
+    // timing of this pass ([copy start, copy end] per layer and compute
+    // waits), added to the statistics of the API call (reset at its start)
     auto t0 = std::chrono::steady_clock::now();
     std::vector<hipEvent_t> ev;
     auto mk = [&]() {
@@ -600,9 +654,12 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
         // streamed layer while this one computes
         if (int r = enqueue_layer(m, l, rc, st)) return r;
         if (int r = tap_last_row(m, rc, l, st)) return r;
+        m->stats.layers_pinned += 1;
         continue;
       }
       const int s = n_streamed++ & 1;
+      for (int i = 0; i < 7; ++i) m->stats.bytes += (double)m->L[l].bytes[i];
+      m->stats.layers_streamed += 1;
       hipEvent_t a = mk(), b = mk();
       if (int r = stream_prefetch(m, l, s, a, b)) return r;
       cp0.push_back(a);
@@ -632,10 +689,10 @@ static int run_layers(ms_model *m, const RunCfg &rc, hipStream_t st) {
     const double total =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
             .count();
-    m->stats.io_ms = io;
-    m->stats.wait_ms = wait;
-    m->stats.total_ms = total;
-    m->stats.compute_ms = total - wait;
+    m->stats.io_ms += io;
+    m->stats.wait_ms += wait;
+    m->stats.total_ms += total;
+    m->stats.compute_ms += total - wait;
     return MS_OK;
   }
   for (int l = l0; l < l1; ++l) {
@@ -741,6 +798,8 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
     const int G = ld.n_heads / ld.n_kv_heads;
     max_part = std::max(max_part, attn_part_floats(d.max_seqs, ld.n_kv_heads, Ly.n_chunks,
                                                    attn_rows, G, ld.head_dim));
+    // a batch-1 decode step's chunk partials, merged in the O projection
+    max_part = std::max(max_part, dec_part_floats(1, ld.n_heads, ld.head_dim));
     m->qkv_max = std::max(m->qkv_max, ncols_qkv);
     m->q_max = std::max(m->q_max, ld.q_dim);
     m->quant_k = std::max(m->quant_k, std::max(std::max(d.hidden, d.ffn), ld.q_dim));
@@ -782,6 +841,7 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
       (rc = dmalloc(m, (void **)&m->ids_hist, (size_t)m->hist_cap * d.max_seqs * 4)))
     return cleanup(rc);
   if (hipMemset(m->pos, 0, 64 * 4) != hipSuccess || hipMemset(m->step, 0, 64 * 4) != hipSuccess ||
+      hipMemset(m->attn_part, 0, max_part * 4) != hipSuccess ||
       hipMemset(m->tok, 0, 64 * 4) != hipSuccess ||
       hipMemset(m->attn_ctr, 0, (size_t)d.max_seqs * m->nkv_max * 4) != hipSuccess)
     return cleanup(fail(MS_E_HIP, "model: memset failed"));
@@ -1076,6 +1136,7 @@ static int forward_impl(ms_model *m, int first, int count, float *d_x, int B, in
   if (int rc = check_positions(m, h_base, B, T, 0)) return rc;
   hipStream_t st = ctx().stream;
   if (int rc = upload_pos(m, h_base, B, st)) return rc;
+  m->stats = ms_stream_stats{};
   RunCfg rc{};
   rc.B = B;
   rc.T = T;
@@ -1124,6 +1185,7 @@ static int enqueue_decode_step(ms_model *m, int B, int pos_bound, hipStream_t st
   rc.n_layers = (int)m->L.size();
   rc.hidden = m->tap_hidden;
   rc.pos_bound = pos_bound;
+  rc.one_row = B == 1;
   if (int r = run_layers(m, rc, st)) return r;
   ArgmaxFin f{};
   f.tok_state = m->tok;
@@ -1205,6 +1267,7 @@ extern "C" int ms_decode_run(ms_model *m, int n_steps, int use_graph, int32_t *h
                    "decode_run: the repetition-penalty history of a sequence would exceed "
                    "8192 ids (prompt + generated); reset the model first");
   if (!m->d.resident) use_graph = 0;  // streaming runs eagerly (host-side slot logic)
+  m->stats = ms_stream_stats{};
   hipStream_t st = ctx().stream;
   int p0 = 0;  // largest position of the first step
   for (int b = 0; b < B; ++b) p0 = std::max(p0, m->h_pos[b]);
@@ -1245,6 +1308,13 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
   if (int rc = check_ready(m, true)) return rc;
   for (int i = 0; i < n_tokens; ++i)
     MS_CHECK_ARG(h_tokens[i] >= 0 && h_tokens[i] < m->d.vocab, "prefill: token id out of range");
+  // the prompt ids open the sequence's penalty history
+  // (gemma4_e4b_infer.mojo:134-139,157-161); the history holds at most
+  // kSampleMaxHistory ids (prompt, the first draw, then one per step)
+  if (m->sampling)
+    MS_CHECK_ARG(n_tokens + 1 <= kSampleMaxHistory,
+                 "prefill: with sampling on, the prompt and the first draw must fit the "
+                 "8192-id repetition-penalty history");
   hipStream_t st = ctx().stream;
   const int D = m->d.hidden;
   // rows per chunk: the prefill workspace (projections as GEMMs)
@@ -1253,18 +1323,13 @@ extern "C" int ms_prefill(ms_model *m, int seq, const int32_t *h_tokens, int n_t
   MS_HIP_TRY(hipMallocAsync((void **)&dtok, (size_t)n_tokens * 4, st));
   MS_HIP_TRY(hipMemcpyAsync(dtok, h_tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice, st));
   if (m->sampling) {
-    // the prompt ids open the sequence's penalty history
-    // (gemma4_e4b_infer.mojo:134-139,157-161); the history holds at most
-    // kSampleMaxHistory ids (prompt, the first draw, then one per step)
-    MS_CHECK_ARG(n_tokens + 1 <= kSampleMaxHistory,
-                 "prefill: with sampling on, the prompt and the first draw must fit the "
-                 "8192-id repetition-penalty history");
     const int nh = n_tokens;
     MS_HIP_TRY(hipMemcpyAsync(m->shist + (size_t)seq * kSampleMaxHistory, dtok, (size_t)nh * 4,
                               hipMemcpyDeviceToDevice, st));
     MS_HIP_TRY(hipMemcpyAsync(m->shist_n + seq, &nh, 4, hipMemcpyHostToDevice, st));
     MS_HIP_TRY(hipStreamSynchronize(st));  // nh is a local
   }
+  m->stats = ms_stream_stats{};
   int rcode = MS_OK;
   std::vector<int32_t> sub;
   for (int c0 = 0; c0 < n_tokens && rcode == MS_OK; c0 += T) {
@@ -1422,7 +1487,9 @@ static int attn_sweep(ms_model *m, int passes, double *avg_us, double *bytes_per
       a.cache_len = Ly.d.cache_len;
       a.clamp = Ly.d.clamp_reads;
       a.write_cache = 0;
-      if ((rc = launch_attention(a, st))) break;
+      if ((rc = g_prof.attn_part[k] ? launch_attention_partials(a, st)
+                                     : launch_attention(a, st)))
+        break;
       for (int b = 0; b < a.B; ++b) {
         const int keys = std::min(pos[b] + 1, Ly.d.cache_len);
         bytes += 2.0 * keys * Ly.d.kv_dim * 4;

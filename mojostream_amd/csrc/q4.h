@@ -29,6 +29,24 @@ enum GemvEpilogue {
 enum GemvASource {
   AS_ROWS = 0,   // prologue: every block quantizes the fp32 rows into LDS
   AS_QUANT = 1,  // limbs prepared in global memory by launch_quant_rows
+  AS_ATTN = 2,   // one row: the attention chunks of k_attn_part, merged per
+                 // query head by the wave that owns the head's K range
+  AS_WAVES = 3,  // one row: each wave quantizes its own contiguous K slice
+                 // with its own shift (no block-wide prologue); the row's
+                 // RMSNorm factor is applied in the epilogue
+};
+
+// AS_ATTN: the chunk partials of one decode row (layout in attention.h:
+// o [kDecPartMaxChunks][n_heads][hd], then (m, l)).  Wave w of the block owns
+// head w, K = n_heads * hd with hd / 128 super-tiles per wave; it merges the
+// head's chunks, quantizes the head with its own shift and multiplies its
+// super-tiles, and the epilogue scales each wave's sums by its shift.
+struct AttnSrc {
+  const float *part;
+  const int32_t *pos;   // position of the row
+  int hd, n_heads;
+  int circular, cache_len, clamp;
+  int chunks;           // chunks the attention launch covered
 };
 
 // fp32 rows and the transform applied before quantization:
@@ -57,8 +75,9 @@ struct GemvArgs {
   int epi;        // GemvEpilogue
   int asrc;       // GemvASource
   int K, M;
-  RowSrc rows;    // AS_ROWS
+  RowSrc rows;    // AS_ROWS, AS_WAVES (no gamma, no x_out)
   QuantRows q;    // AS_QUANT
+  AttnSrc at;     // AS_ATTN
   GemvSeg seg[3];
   int nseg;
   int P;          // panels per block (EPI_SWIGLU: 2, gate and up)
@@ -105,6 +124,8 @@ struct GemmArgs {
 };
 
 constexpr int kGemvMaxM = 16;
+// AS_WAVES: super-tiles per wave (640 values: K = 2560 on 4 waves, 10240 on 16)
+constexpr int kWaveTiles = 5;
 constexpr int kQuantMaxK = 16384;  // longest row a 1024-thread block quantizes
 
 int launch_gemv(const GemvArgs &a, hipStream_t st);

@@ -10,6 +10,7 @@
 // output.  For M <= 4 the 4M limb rows share one MFMA, so one MFMA covers
 // 1024 weights.  Prefill rows (M > 16) go through the GEMM in gemm.hip, which
 // uses the same operands and therefore gives the same values.
+#include "attention.h"
 #include "devutil.h"
 #include "q4.h"
 
@@ -611,9 +612,207 @@ __device__ inline void rows_to_waves(const RowSrc &rs, int K, int M, int8_t *lim
   if (j == 0 && lane == 0) row_s[r] = s;
 }
 
+// AS_ATTN instantiations carry the head dim and the load batch in the RP
+// template slot: RP = (hd / 128) * 100 + NJ.
+__host__ __device__ constexpr int attn_hd(int rp) { return rp / 100 * 128; }
+__host__ __device__ constexpr int attn_nj(int rp) { return rp % 100; }
+
+// AS_ATTN prologue of wave `wave` (head h = wave) in a block of W waves:
+// merge the head's attention chunks (k_attn_part), quantize the merged head
+// with its own shift and store its four limb rows into the block's limb rows
+// (the head's K range only; the wave reads nothing else, so no block barrier).
+//
+// Loads.  Each lane loads 8 dims of a chunk's o partial per load pair, so one
+// pair of 16-byte loads covers CPI = 512 / HD chunks (HD / 8 lanes each); NJ
+// pairs cover a batch of NJ * CPI chunks.  Every lane of every load reads
+// data (a wave load instruction costs the CU's address unit the same time
+// whatever lanes read), and loads of chunks past the launched ones read past
+// the buffer range: zeros, no memory access.  The position, the (m, l) pairs
+// (lane = chunk), the o partials and then the wave's weights (kw) are issued
+// in that order and without branches, so the compiler can count them and the
+// merge waits for the partials only.
+//
+// Merge (k_attn_decode's): w_c = e^(m_c - M) / sum_c e^(m_c - M) l_c and
+// o = sum_c w_c o_c, each lane summing its chunks in order, then the CPI lane
+// groups added.  Chunks past the position take no part (a select, so a stale
+// partial never enters the sum).
+template <int W, int HD, int NJ, class KW>
+__device__ inline void attn_merge_quant(const AttnSrc &at_, int8_t *limbs, int ldl,
+                                        int32_t *row_s, int wave, int lane, KW kw) {
+  constexpr int LPC = HD / 8;    // lanes per chunk
+  constexpr int CPI = 64 / LPC;  // chunks per load pair
+  constexpr int CPB = NJ * CPI;  // chunks per batch
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const float *po = launder(at_.part);
+  const int32_t *ppos = launder(at_.pos);
+  const int nhq = launder(at_.n_heads);
+  const int circular = launder(at_.circular), L = launder(at_.cache_len);
+  const int clamp = launder(at_.clamp), nch = launder(at_.chunks);
+  const float *pml = po + (size_t)kDecPartMaxChunks * nhq * HD;
+  const int h = wave;
+  const int q8 = lane % LPC, csub = lane / LPC;
+  const int base = ldg<int32_t>(ppos);
+  const __amdgpu_buffer_rsrc_t rs_ml = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(pml), 0, nch * nhq * 2 * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(po), 0, nch * nhq * HD * 4, 0x00020000);
+  const f32x2 ml = __builtin_bit_cast(
+      f32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_ml, (lane * nhq + h) * 8, 0, 0));
+  const uint32_t qoff = (uint32_t)(h * HD + 8 * q8) * 4u;
+  f32x4 ov[NJ][2];
+  auto load_o = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t off = (uint32_t)((c0 + j * CPI + csub) * nhq * HD) * 4u + qoff;
+      ov[j][0] = __builtin_amdgcn_raw_buffer_load_b128(rs_o, off, 0, 0);
+      ov[j][1] = __builtin_amdgcn_raw_buffer_load_b128(rs_o, off + 16, 0, 0);
+    }
+  };
+  // the scheduler would otherwise hold the partials back until the (m, l)
+  // pairs arrive, one more memory round trip
+  __builtin_amdgcn_sched_barrier(0);
+  load_o(0);
+  __builtin_amdgcn_sched_barrier(0);
+  kw();
+  __builtin_amdgcn_sched_barrier(0);
+  // attended slots and chunks (as k_attn_part computes them)
+  int hi = base;
+  if (!circular && clamp && hi > L - 1) hi = L - 1;
+  const int nslots = circular ? min(L, base + 1) : min(hi + 1, L);
+  const int n_active = min((nslots + kDecPartChunk - 1) / kDecPartChunk, nch);
+  const float mc = lane < n_active ? ml.x : -INFINITY;
+  const float M = wave_max(mc);
+  const float e = lane < n_active ? expf(mc - M) : 0.f;
+  const float inv = 1.0f / wave_sum((lane < n_active ? ml.y : 0.f) * e);
+  const float wl = e * inv;
+  float o[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = 0.f;
+  for (int c0 = 0; c0 < n_active; c0 += CPB) {
+    if (c0 > 0) load_o(c0);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = c0 + j * CPI + csub;
+      const float w = __shfl(wl, c & 63, 64);
+      const bool on = c < n_active;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        o[k] = on ? o[k] + w * ov[j][0][k] : o[k];
+        o[4 + k] = on ? o[4 + k] + w * ov[j][1][k] : o[4 + k];
+      }
+    }
+  }
+  // the lane groups holding the same dims (lanes q8 + LPC s)
+#pragma unroll
+  for (int x = LPC; x < 64; x <<= 1)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] += __shfl_xor(o[k], x, 64);
+  float mx = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(o[k]));
+  const int s = row_shift(wave_max(mx));
+  if (lane < LPC) {
+    uint32_t lo[4], hi4[4];
+    quant8<false>(o, ldexpf(1.0f, s), lo, hi4);
+    const int pos8 = limb_pos8(h * HD + 8 * lane);
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+      *reinterpret_cast<uint2 *>(limbs + (size_t)l * ldl + pos8) = uint2{lo[l], hi4[l]};
+  }
+  if (lane == 0) row_s[h] = s;
+  // this wave's limb stores before its own operand reads
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// AS_WAVES prologue of wave `wave`: the wave's slice of the row, K values
+// [128 TPW wave, 128 TPW (wave + 1)), as 8-value groups (lane l: groups l and
+// l + 64).  y = x * pre_scale; the wave's own maximum |y| sets its shift, its
+// sum of y^2 goes to ssw[wave] for the epilogue's RMSNorm factor.  The limbs
+// go to the block's limb rows in the wave's K range only, which the wave alone
+// reads, so no block barrier.  The row's loads are waited for before the
+// first weights go out (kw): they would otherwise queue behind the weights.
+// yv keeps y for the epilogue (the normalized row, block 0).
+template <int TPW, class KW>
+__device__ inline void wave_rows_quant(const RowSrc &rs, int K, int8_t *limbs, int ldl,
+                                       int32_t *row_s, float *ssw, float (&yv)[2][8], int wave,
+                                       int lane, KW kw) {
+  constexpr int NG8 = TPW * 16;
+  const int k0 = wave * TPW * 128;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int gq = lane + 64 * r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv[r][e] = 0.f;
+    if (gq < NG8) {
+      const float *p = rs.x + k0 + 8 * gq;
+      const float4 a = ldg<float4>(p), b = ldg<float4>(p + 4);
+      yv[r][0] = a.x; yv[r][1] = a.y; yv[r][2] = a.z; yv[r][3] = a.w;
+      yv[r][4] = b.x; yv[r][5] = b.y; yv[r][6] = b.z; yv[r][7] = b.w;
+    }
+  }
+  asm volatile("" ::"v"(yv[0][0]), "v"(yv[1][7]) : "memory");
+  kw();
+  float mx = 0.f, ss = 0.f;
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = yv[r][e] * rs.pre_scale;
+      yv[r][e] = y;
+      ss += y * y;
+      mx = fmaxf(mx, fabsf(y));
+    }
+  mx = wave_max(mx);
+  ss = wave_sum(ss);
+  const int s = row_shift(mx);
+  const float mul = ldexpf(1.0f, s);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int gq = lane + 64 * r;
+    if (gq < NG8) {
+      uint32_t lo[4], hi[4];
+      quant8<false>(yv[r], mul, lo, hi);
+      const int pos = limb_pos8(k0 + 8 * gq);
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        *reinterpret_cast<uint2 *>(limbs + (size_t)l * ldl + pos) = uint2{lo[l], hi[l]};
+    }
+  }
+  if (lane == 0) {
+    row_s[wave] = s;
+    ssw[wave] = ss;
+  }
+  (void)K;
+  // this wave's limb stores before its own operand reads
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// DPP move of a double (its two words), inside rows of 16 lanes.
+template <int CTRL>
+__device__ inline double dpp_d(double x) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+// Sum over aligned groups of W consecutive lanes (W = 4, 8 or 16; every lane
+// of the group gets it): quad permutes, then the half-row and row mirrors.
+template <int W>
+__device__ inline double lanes_sum_d(double v) {
+  static_assert(W == 4 || W == 8 || W == 16, "groups of 4, 8 or 16 lanes");
+  v += dpp_d<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_d<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v += dpp_d<0x141>(v);   // row_half_mirror
+  if constexpr (W == 16) v += dpp_d<0x140>(v);  // row_mirror
+  return v;
+}
+
 // C: 16-row MFMA groups (4 limb rows per activation row: M <= 4C).
 // P: panels per block.  AS: GemvASource.  W: waves per block.  EPI: epilogue.
-// RP: activation rows whose loads the AS_ROWS prologue issues at once.
+// RP: activation rows whose loads the AS_ROWS prologue issues at once
+// (AS_ATTN: attention chunks per load batch).
 //
 // Block pg = P panels of 16 columns over the whole K.  Wave w owns super-tiles
 // w, w+W, ...; each batch issues U of them (P panels each) before any is
@@ -624,7 +823,12 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ float sh[W > 8 ? 32 : (8 * W > 32 ? 8 * W : 32)];  // reduction scratch
   constexpr int NT = 64 * W;
-  constexpr int U = gemv_batch<C, P, AS, W>();
+  // AS_ATTN: the head's super-tiles, one batch
+  // (AS_WAVES: the wave's RP super-tiles, one batch)
+  constexpr int U = AS == AS_ATTN    ? attn_hd(RP) / 128
+                    : AS == AS_WAVES ? RP
+                                     : gemv_batch<C, P, AS, W>();
+  constexpr bool WAVE_K = AS == AS_ATTN || AS == AS_WAVES;  // contiguous K per wave
   // wave-uniform in a scalar register: tile predicates below are then scalar
   // branches, and loads behind them need no merge (and no wait) at the join
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -652,21 +856,24 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   int32_t *arg_idx = (EPI == EPI_ARGMAX) ? launder(a.arg_idx) : nullptr;
   RowSrc rs{};
   QuantRows qr{};
-  if (AS == AS_ROWS) {
+  if (AS == AS_ROWS || AS == AS_WAVES) {
     rs.x = launder(a.rows.x);
     rs.ld = launder(a.rows.ld);
     rs.pre_scale = launder(a.rows.pre_scale);
     rs.norm = launder(a.rows.norm);
     rs.y_out = launder(a.rows.y_out);
     rs.x_out = launder(a.rows.x_out);
-  } else {
+  } else if (AS == AS_QUANT) {
     qr.limbs = launder(a.q.limbs);
     qr.shift = launder(a.q.shift);
   }
 
   const int KG = K / kSuperK;
   const int pg = blockIdx.x;
-  const int nb = ((KG + W - 1) / W + U - 1) / U;  // batches (block-uniform)
+  // AS_ATTN: wave w owns the super-tiles of head w, contiguous; otherwise
+  // super-tiles are dealt to the waves round-robin
+  const int tpw = WAVE_K ? U : 0;  // = K / (128 W), checked by the launcher
+  const int nb = WAVE_K ? 1 : ((KG + W - 1) / W + U - 1) / U;  // batches
 
   const uint8_t *wl[P];
   float wsc[P];
@@ -677,6 +884,13 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
     gemv_slot<EPI>(sw0, sw1, sw2, ss0, ss1, ss2, sn0, sn1, sn2, sc0, sc1, sc2, K, P, pg, p,
                    &wl[p], &wsc[p], &col[p], &wv[p]);
 
+  // WAVE_K, residual epilogue: the thread that finishes output (p, j) loads
+  // its residual value now (a memory round trip off the epilogue's path)
+  float resid_pre = 0.f;
+  if constexpr (WAVE_K && EPI == EPI_RESID) {
+    const int t = threadIdx.x, w = t % W, p = (t / W) % P, j = t / (W * P);
+    if (t < 16 * P * W && w == 0 && wv[p]) resid_pre = ldg<float>(resid + col[p] + j);
+  }
   int32_t *red = reinterpret_cast<int32_t *>(lds);
   float *vals = reinterpret_cast<float *>(lds + gemv_lds_red(W, P, C));
   int32_t *row_s = reinterpret_cast<int32_t *>(lds + gemv_lds_red(W, P, C) + (size_t)P * M * 64);
@@ -691,17 +905,33 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
 
   uint4 q[U][P];
   v4i af[AS == AS_QUANT ? U : 1][C][2];
+  float yv[2][8];  // AS_WAVES: the wave's y values (for the normalized row)
   // Loads of super-tiles u0..u1-1 of batch bt; tiles past the end of K are
   // not loaded (their slots stay zero and are never consumed).
+  auto tile = [&](int bt, int u) {
+    return WAVE_K ? wave * tpw + u : wave + (bt * U + u) * W;
+  };
+  auto tile_on = [&](int bt, int u) {
+    return WAVE_K ? u < tpw : wave + (bt * U + u) * W < KG;
+  };
   auto issue_part = [&](int bt, int u0, int u1) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (u < u0 || u >= u1) continue;
-      const int Gu = wave + (bt * U + u) * W;
+      const int Gu = tile(bt, u);
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         q[u][p] = uint4{0u, 0u, 0u, 0u};
-        if (Gu < KG) {
+        if constexpr (AS == AS_ATTN) {
+          // the wave's own super-tiles as one range (no branch: tiles past
+          // it read zeros without a memory access), streaming hint (nt)
+          const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+              const_cast<uint8_t *>(wl[p]) + (size_t)wave * tpw * 1024, 0, tpw * 1024,
+              0x00020000);
+          const u32x4 v = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, u * 1024 + lane * 16, 0, 2));
+          q[u][p] = uint4{v.x, v.y, v.z, v.w};
+        } else if (tile_on(bt, u)) {
           const u32x4 v = ldg_nt<u32x4>(wl[p] + (size_t)Gu * 1024 + lane * 16);
           q[u][p] = uint4{v.x, v.y, v.z, v.w};
         }
@@ -760,25 +990,40 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
     }
     __syncthreads();
     if constexpr (kEarly < U) issue_part(0, kEarly, U);
+  } else if constexpr (AS == AS_ATTN) {
+    attn_merge_quant<W, attn_hd(RP), attn_nj(RP)>(a.at, limbs, ldl, row_s, wave, lane,
+                                                   [&] { issue(0); });
+  } else if constexpr (AS == AS_WAVES) {
+    constexpr int kEarlyW = (4 / P) < 1 ? 1 : ((4 / P) < U ? (4 / P) : U);
+    wave_rows_quant<RP>(rs, K, limbs, ldl, row_s, sh, yv, wave, lane,
+                        [&] { issue_part(0, 0, kEarlyW); });
+    if constexpr (kEarlyW < U) issue_part(0, kEarlyW, U);
   } else {
     if ((int)threadIdx.x < M) row_s[threadIdx.x] = ldg<int32_t>(qr.shift + threadIdx.x);
     issue(0);
   }
 
-  v4i acc[P][C];
+  // Weights enter the MFMA as unsigned nibbles n (one mask per four bytes);
+  // accz collects sum_k limb(k) * (-8) with a constant operand, added to every
+  // panel's sums after the K loop (exact: each term stays in int32).
+  const v4i kMinus8 = v4i{(int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u,
+                          (int)0xF8F8F8F8u};
+  v4i acc[P][C], accz[C];
 #pragma unroll
   for (int p = 0; p < P; ++p)
 #pragma unroll
     for (int c = 0; c < C; ++c) acc[p][c] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < C; ++c) accz[c] = v4i{0, 0, 0, 0};
 
   for (int bt = 0; bt < nb; ++bt) {
     if (bt > 0) issue(bt);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int Gu = wave + (bt * U + u) * W;
-      if (Gu < KG) {
+      const int Gu = tile(bt, u);
+      if (tile_on(bt, u)) {
         v4i al[C][2];
-        if constexpr (AS == AS_ROWS) {
+        if constexpr (AS == AS_ROWS || WAVE_K) {
 #pragma unroll
           for (int c = 0; c < C; ++c) {
             al[c][0] = v4i{0, 0, 0, 0};
@@ -796,7 +1041,7 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const uint32_t d0 = dw[2 * h], d1 = dw[2 * h + 1];
-            const v4i b = v4i{nib_s8(d0), nib_s8(d0 >> 4), nib_s8(d1), nib_s8(d1 >> 4)};
+            const v4i b = v4i{nib_u8(d0), nib_u8(d0 >> 4), nib_u8(d1), nib_u8(d1 >> 4)};
 #pragma unroll
             for (int c = 0; c < C; ++c) {
               const v4i av = (AS == AS_QUANT) ? af[u][c][h] : al[c][h];
@@ -804,9 +1049,22 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
             }
           }
         }
+        // the zero point: sum_k limb(k) * (-8), once for all panels
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int c = 0; c < C; ++c) {
+            const v4i av = (AS == AS_QUANT) ? af[u][c][h] : al[c][h];
+            accz[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, kMinus8, accz[c], 0, 0, 0);
+          }
       }
     }
   }
+  // acc = sum_k limb(k) * n_k + sum_k limb(k) * (-8) = sum_k limb(k) * (n_k - 8)
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[p][c] += accz[c];
 
 #pragma unroll
   for (int p = 0; p < P; ++p)
@@ -821,6 +1079,74 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   // |limb * (n - 8)| <= 1024 per term, K <= 16384), combine the limbs in
   // int64, scale once.  Each output is finished by the thread that sums it
   // (no second pass through LDS).
+  if constexpr (WAVE_K) {
+    // One row, one shift per wave: thread t takes column j, panel slot p and
+    // wave w (t = (j P + p) W + w), combines that wave's limb sums exactly and
+    // scales them by the wave's shift; the W lanes of (j, p) are then added.
+    static_assert(16 * P * W <= NT, "one thread per (column, panel, wave)");
+    static_assert(EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_SWIGLU,
+                  "per-wave shifts: store, residual or SwiGLU epilogue");
+    const int t = threadIdx.x;
+    const int w = t % W, p = (t / W) % P, j = t / (W * P);
+    const bool on = t < 16 * P * W;
+    double v = 0.0;
+    if (on) {
+      long long tw = 0;
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        tw += (long long)red[((size_t)w * P + p) * C * 256 + dfrag(l, j)] << (8 * l);
+      v = (double)tw * (double)ldexpf(1.0f, -row_s[w]);
+    }
+    v = lanes_sum_d<W>(v);
+    // RMSNorm of the row (rmsnorm_inplace kernels.mojo:474-489) as a factor on
+    // the products: y . W = inv (x . W)
+    float inv = 1.0f;
+    if (AS == AS_WAVES && rs.norm) {
+      float ssum = 0.f;
+#pragma unroll
+      for (int u = 0; u < W; ++u) ssum += sh[u];
+      inv = 1.0f / sqrtf(ssum / (float)K + 1e-6f);
+    }
+    if constexpr (EPI == EPI_SWIGLU) {
+      // gate (p = 0) and up (p = 1) of column j sit W lanes apart
+      const double vu = __shfl_down(v, W, 64);
+      if (on && w == 0 && p == 0) {
+        const float gt = (float)(v * (double)inv * (double)wsc[0]);
+        const float up = (float)(vu * (double)inv * (double)wsc[1]);
+        sw_out[col[0] + j] = up * gt * (1.0f / (1.0f + expf(-gt)));
+      }
+    } else {
+      if (on && w == 0 && wv[p]) {
+        const float val = (float)(v * (double)inv * (double)wsc[p]);
+        const size_t oi = (size_t)col[p] + j;
+        if constexpr (EPI == EPI_STORE) {
+          out[oi] = val;
+        } else {
+          // x = x + proj (gemma4_e4b.mojo:522,538)
+          const float x = resid_pre + val;
+          out[oi] = x;
+          if (out2) out2[oi] = x;
+        }
+      }
+    }
+    if constexpr (AS == AS_WAVES) {
+      // the normalized row, y * inv (block 0): the next projections' residual
+      if (blockIdx.x == 0 && rs.y_out) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int gq = lane + 64 * r;
+          if (gq < RP * 16) {
+            float *o = rs.y_out + wave * RP * 128 + 8 * gq;
+            *reinterpret_cast<float4 *>(o) = float4{yv[r][0] * inv, yv[r][1] * inv,
+                                                    yv[r][2] * inv, yv[r][3] * inv};
+            *reinterpret_cast<float4 *>(o + 4) = float4{yv[r][4] * inv, yv[r][5] * inv,
+                                                        yv[r][6] * inv, yv[r][7] * inv};
+          }
+        }
+      }
+    }
+    return;
+  }
   auto value = [&](int p, int m, int j) {
     const int c = m >> 2, r0 = 4 * (m & 3);
     long long t = 0;
@@ -954,14 +1280,17 @@ int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st) {
 size_t gemv_lds_need(const GemvArgs &a) {
   const int C = a.M <= 4 ? 1 : 4;
   size_t b = gemv_lds_fixed(a.waves, a.P, C, a.M);
-  if (a.asrc == AS_ROWS) b += (size_t)4 * a.M * gemv_ldl(a.K);
+  if (a.asrc == AS_ROWS || a.asrc == AS_ATTN || a.asrc == AS_WAVES)
+    b += (size_t)4 * a.M * gemv_ldl(a.K);
   return b;
 }
 
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_CHECK_ARG(a.M >= 1 && a.M <= kGemvMaxM, "GEMV: 1 <= M <= 16");
   MS_CHECK_ARG(a.K >= kSuperK && a.K % kSuperK == 0, "GEMV: K % 128 != 0");
-  MS_CHECK_ARG(a.asrc == AS_ROWS || a.asrc == AS_QUANT, "GEMV: bad activation source");
+  MS_CHECK_ARG(a.asrc == AS_ROWS || a.asrc == AS_QUANT || a.asrc == AS_ATTN ||
+                   a.asrc == AS_WAVES,
+               "GEMV: bad activation source");
   MS_CHECK_ARG(a.nseg >= 1 && a.nseg <= 3, "GEMV: 1 to 3 segments");
   MS_CHECK_ARG(a.epi != EPI_RESID || (a.resid && a.out), "GEMV: residual epilogue needs rows");
   MS_CHECK_ARG(a.epi != EPI_SWIGLU || (a.P == 2 && a.nseg == 2 && a.sw_out),
@@ -973,6 +1302,22 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     MS_CHECK_ARG(a.rows.x && a.rows.ld >= a.K && !a.rows.gamma,
                  "GEMV: row prologue needs rows (no gamma)");
     MS_CHECK_ARG(a.K <= 8 * rows_ng(a.waves) * 64 * a.waves, "GEMV: row prologue: row too long");
+  } else if (a.asrc == AS_WAVES) {
+    MS_CHECK_ARG(a.M == 1 && a.rows.x && !a.rows.gamma && !a.rows.x_out &&
+                     a.K == a.waves * kWaveTiles * kSuperK &&
+                     ((a.epi == EPI_STORE && a.P == 1 && a.waves == 4) ||
+                      (a.epi == EPI_SWIGLU && a.P == 2 && a.waves == 4) ||
+                      (a.epi == EPI_RESID && a.P == 1 && a.waves == 16)),
+                 "GEMV: per-wave rows: one row, K = waves * 640, store (4 waves), "
+                 "SwiGLU (4 waves) or residual (16 waves)");
+  } else if (a.asrc == AS_ATTN) {
+    MS_CHECK_ARG(a.M == 1 && a.P == 1 && a.waves == 8 && a.epi == EPI_RESID,
+                 "GEMV: attention source: one row, one panel per block, 8 waves, residual");
+    MS_CHECK_ARG(a.at.part && a.at.pos && a.at.n_heads == a.waves &&
+                     (a.at.hd == 128 || a.at.hd == 256 || a.at.hd == 512) &&
+                     a.K == a.at.n_heads * a.at.hd && a.at.chunks >= 1 &&
+                     a.at.chunks <= kDecPartMaxChunks && a.at.cache_len > 0,
+                 "GEMV: attention source: one head of 128/256/512 per wave, K = heads * hd");
   } else {
     MS_CHECK_ARG(a.q.limbs && a.q.shift, "GEMV: quantized rows missing");
   }
@@ -1012,6 +1357,24 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_GEMV(EPI_RESID, 1, AS_ROWS, 8)
   MS_GEMV(EPI_RESID, 1, AS_ROWS, 16)
   MS_GEMV(EPI_RESID, 1, AS_QUANT, 4)
+  if (!ok && a.asrc == AS_WAVES) {
+    if (a.epi == EPI_STORE) MS_GEMV_L(1, EPI_STORE, 1, AS_WAVES, 4, kWaveTiles);
+    else if (a.epi == EPI_SWIGLU) MS_GEMV_L(1, EPI_SWIGLU, 2, AS_WAVES, 4, kWaveTiles);
+    else MS_GEMV_L(1, EPI_RESID, 1, AS_WAVES, 16, kWaveTiles);
+    ok = true;
+  }
+  if (!ok && a.asrc == AS_ATTN) {
+    // the row-prologue template slot carries the head dim and the load pairs
+    // per batch (a pair covers 512 / hd chunks)
+    const int pairs = (a.at.chunks * a.at.hd + 511) / 512;
+    if (a.at.hd == 128) MS_GEMV_L(1, EPI_RESID, 1, AS_ATTN, 8, 104);
+    else if (a.at.hd == 256 && pairs <= 4) MS_GEMV_L(1, EPI_RESID, 1, AS_ATTN, 8, 204);
+    else if (a.at.hd == 256) MS_GEMV_L(1, EPI_RESID, 1, AS_ATTN, 8, 208);
+    else if (pairs <= 4) MS_GEMV_L(1, EPI_RESID, 1, AS_ATTN, 8, 404);
+    else if (pairs <= 8) MS_GEMV_L(1, EPI_RESID, 1, AS_ATTN, 8, 408);
+    else MS_GEMV_L(1, EPI_RESID, 1, AS_ATTN, 8, 416);
+    ok = true;
+  }
   if (!ok && a.epi == EPI_RESID && a.P == 1 && a.asrc == AS_QUANT && a.waves == 16) {
     MS_CHECK_ARG(a.M <= 4, "GEMV: 16 waves over global limbs take at most 4 rows");
     if (a.M == 1) MS_GEMV_L(1, EPI_RESID, 1, AS_QUANT, 16, 1);

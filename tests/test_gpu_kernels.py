@@ -202,6 +202,9 @@ ATTN_CASES = [
     ("decode-demo-last", 1024, 256, 128, 8, 2, 0, 512, 0, 1, 511),
     ("decode-g4-hd64", 1024, 256, 64, 16, 4, 0, 256, 0, 1, 200),
     ("decode-g20", 2560, 128, 128, 20, 1, 1, 512, 0, 1, 900),
+    # head dim 512 with 20 query heads per kv head: more merge units (2560
+    # float4) than one pass of the block's threads covers
+    ("decode-hd512-g20", 10240, 512, 512, 20, 1, 0, 512, 0, 1, 300),
     # many rows of one sequence: the flash-attention prefill path
     ("prefill-sliding", 2048, 512, 256, 8, 2, 1, 512, 0, 200, 0),
     ("prefill-sliding-wrap", 2048, 512, 256, 8, 2, 1, 512, 0, 333, 650),

@@ -43,23 +43,37 @@ def prompt_ids(n, vocab, stream):
 
 
 # ---- demo model (config: D=1024, 40 layers, 8q/2kv, hd 128, F 4096) -----------------
-def test_demo_harness_steps_per_layer(gpu, fast_oracle):
+def test_demo_harness_100_steps(gpu, fast_oracle):
+    """The harness workload itself (run_harness, harness.mojo:236-269): the
+    40-layer demo model, fresh N(0,1) rows [4][1024] every step at bases 0, 4,
+    .., 396, 100 steps, against the threaded oracle: the output rows of every
+    step, and every layer's rows at sampled steps including the last (per-layer
+    bar of validate_layer.mojo:138-154)."""
     ms = gpu
     arch = ms.arch_demo(max_len=512)
-    say("demo 40 layers, batch-4 rows, harness steps base 0,4,8")
+    say("demo 40 layers, batch-4 rows, the harness's 100 steps (bases 0..396)")
     m = build(ms, arch, max_seqs=1, max_rows=4, max_pos=512)
     om = synthetic_oracle_model(fast_oracle, arch, SEED, with_lm=False)
-    worst = 0.0
-    for step in range(3):
+    sampled = {0, 1, 2, 50, 98, 99}
+    worst_out = worst_layer = 0.0
+    for step in range(100):
         base = 4 * step
         x = ms.host_normal(4 * 1024, 1000 + step, 1).reshape(4, 1024)
-        g_out, g_hid = m.forward(x, [base], T=4, hidden=True)
-        o_out, o_hid = om.forward(x, base, hidden=True)
-        errs = [rel_rmse(g_hid[l], o_hid[l]) for l in range(arch.n_layers)]
-        worst = max(worst, max(errs))
-        print(f"  step {step}: max per-layer rel RMSE {max(errs):.2e} (layer {int(np.argmax(errs))})")
-        assert np.array_equal(g_out, g_hid[-1])
-    assert worst < 1e-4
+        if step in sampled:
+            g_out, g_hid = m.forward(x, [base], T=4, hidden=True)
+            o_out, o_hid = om.forward(x, base, hidden=True)
+            errs = [rel_rmse(g_hid[l], o_hid[l]) for l in range(arch.n_layers)]
+            worst_layer = max(worst_layer, max(errs))
+            print(f"  step {step} (base {base}): max per-layer rel RMSE {max(errs):.2e} "
+                  f"(layer {int(np.argmax(errs))})")
+            assert np.array_equal(g_out, g_hid[-1])
+        else:
+            g_out = m.forward(x, [base], T=4)
+            o_out = om.forward(x, base)
+        worst_out = max(worst_out, rel_rmse(g_out, o_out))
+    print(f"  100 steps: output rows rel RMSE max {worst_out:.2e}, sampled layers max "
+          f"{worst_layer:.2e}")
+    assert worst_out < 1e-4 and worst_layer < 1e-4
     m.close()
 
 
@@ -409,4 +423,88 @@ def test_model_guards(gpu):
         m.forward(x, [14], T=4)
     with pytest.raises(ms.MSError, match="scale"):
         m.set_matrix(0, 0, np.zeros((1024, 512), np.uint8), 0.0)
+    m.close()
+
+
+def test_sampling_history_limit(gpu):
+    """The repetition-penalty history holds 8192 ids per sequence (prompt, the
+    first draw, one per step): a prompt of 8191 ids fills it exactly, 8192 is
+    refused; a decode_run that would cross the limit is refused before it runs,
+    one that ends exactly at it runs, and the model's host mirror of the count
+    follows (reset empties it)."""
+    ms = gpu
+    arch = ms.arch_e4b(max_full_seq=64, n_layers=1, vocab=4096)
+    say("sampling history limit: 1 sliding layer, vocab 4096, prompts of 8191/8192 ids")
+    m = ms.Model(arch, max_seqs=1, max_rows=16, max_pos=8400)
+    m.fill_synthetic(SEED)
+    m.set_sampling(0.7, 1.2, 3)
+    ids = prompt_ids(8192, arch.vocab, 60)
+    with pytest.raises(ms.MSError, match="8192"):
+        m.prefill(ids, 0)
+    first = m.prefill(ids[:8191], 0)                     # 8191 + the first draw
+    with pytest.raises(ms.MSError, match="8192"):
+        m.decode([first], [8191], 1)
+    m.reset()
+    first = m.prefill(ids[:8000], 0)                     # 8001 ids
+    with pytest.raises(ms.MSError, match="8192"):
+        m.decode([first], [8000], 192)                   # would reach 8193
+    out = m.decode([first], [8000], 191)                 # ends at 8192 exactly
+    assert out.shape == (191, 1) and np.all((out >= 0) & (out < arch.vocab))
+    with pytest.raises(ms.MSError, match="8192"):
+        m.decode_continue(1, 1)
+    m.reset()                                            # history emptied
+    first = m.prefill(ids[:100], 0)
+    assert m.decode([first], [100], 4).shape == (4, 1)
+    m.close()
+
+
+def test_sampled_draw_seeds_per_sequence(gpu, fast_oracle):
+    """Two sequences with the same prompt, sampled: every draw of the model
+    equals ms_sample on that step's logits with the seed sample_seed(seed, b, k)
+    (k counts the drawing LM head calls), and sequence 1's draws are no copy of
+    sequence 0's shifted by one draw (the lag a seed of seed + b + k would
+    give).  The tied head of a random model puts a token's own id far ahead
+    (at temperature 1 every draw is that id), so the draws run at temperature
+    50, where the distribution is broad and the draws tell the seeds apart."""
+    import ctypes as C
+    ms = gpu
+    arch = ms.arch_e4b(max_full_seq=256, n_layers=2, vocab=16384)
+    say("sampled draw seeds per sequence: T=50, two sequences, identical prompts")
+    m = ms.Model(arch, max_seqs=2, max_rows=8, max_pos=256)
+    m.fill_synthetic(SEED, balanced=True)
+    TEMP = 50.0
+    m.set_sampling(TEMP, 1.0, 77)
+    V = arch.vocab
+    tl = ms.DeviceBuffer(2 * V * 4)
+    m.set_taps(None, tl)
+    prompt = np.asarray(prompt_ids(6, V, 70), np.int32)
+    firsts, pre_logits = [], []
+    for b in range(2):
+        f = C.c_int32()
+        ms.check(ms.lib().ms_prefill(m.h, b, prompt.ctypes.data, len(prompt), 0, C.byref(f)))
+        firsts.append(int(f.value))
+        pre_logits.append(tl.download(np.float32, (V,)))
+    assert np.array_equal(pre_logits[0], pre_logits[1])   # identical rows
+    dummy = ms.DeviceBuffer(64)
+
+    def draw(row, seed):
+        d = ms.DeviceBuffer.from_array(np.ascontiguousarray(row))
+        return ms.sample(d, V, TEMP, dummy, 0, 1.0, seed)
+
+    for b in range(2):
+        assert draw(pre_logits[b], ms.sample_seed(77, b, b)) == firsts[b]
+    steps = 24
+    ids = np.empty((steps, 2), np.int32)
+    for k in range(steps):
+        out = m.decode(firsts, [len(prompt)] * 2, 1) if k == 0 else m.decode_continue(1, 2)
+        ids[k] = out[0]
+        lg = tl.download(np.float32, (2, V))
+        for b in range(2):
+            assert draw(lg[b], ms.sample_seed(77, b, k + 2)) == ids[k, b], (k, b)
+    seq0 = [firsts[0]] + ids[:, 0].tolist()
+    seq1 = [firsts[1]] + ids[:, 1].tolist()
+    print(f"  seq 0 {seq0[:10]}...\n  seq 1 {seq1[:10]}...")
+    assert len(set(seq0)) > steps // 2 and len(set(seq1)) > steps // 2
+    assert seq0 != seq1
+    assert sum(a == b for a, b in zip(seq1[:-1], seq0[1:])) < steps // 2
     m.close()
