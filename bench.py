@@ -172,8 +172,10 @@ def bench_c1(ms, seed=42, steps=100):
     """Demo decode harness (config 1, bench.mojo -> run_harness harness.mojo:185-328):
     a seeded synthetic demo file (D=1024, 40 layers, 8q/2kv heads, hd 128,
     FFN 4096), 4 rows of one sequence per step, 100 steps, the sequence growing
-    by 4 a step; a step is the input rows uploaded plus the 40 layers
-    (ms_forward).  P50 / P95 and tokens/s as the reference's JSON reports them."""
+    by 4 a step; a step is the 40 layers (ms_forward) on rows uploaded before
+    the clock starts, as the reference fills x before its timed loop
+    (harness.mojo:256-262); repeated steps replay a HIP graph.  P50 / P95 and
+    tokens/s as the reference's JSON reports them."""
     import contextlib
     import tempfile
     from mojostream_amd import drivers, streaming as st

@@ -344,6 +344,12 @@ int ms_model_set_bos(ms_model *m, const float *h_bos);
  * sequence; prefill: the last prompt row).  Each call overwrites the taps.
  * NULL switches a tap off. */
 int ms_model_set_taps(ms_model *m, float *d_hidden, float *d_logits);
+/* Launch mode of ms_forward (no reference counterpart; results are the same
+ * either way).  on = 1 (the default): a whole-model call of a resident model
+ * with at most 16 rows that repeats the previous call's buffers, rows and
+ * position bucket is captured as a HIP graph and replayed from then on (the
+ * harness loop, harness.mojo:256-269); on = 0: every call launches eagerly. */
+int ms_model_set_forward_graphs(ms_model *m, int on);
 /* Rows of positions pos0..pos0+n-1 of a layer's KV cache for one sequence
  * (K after RoPE, V), into d_k / d_v [n][kv_dim] (either may be NULL).  A
  * circular cache holds position p in slot p % window (write_kv_sliding

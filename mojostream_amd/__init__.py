@@ -131,6 +131,7 @@ _SIGS = {
     "ms_model_set_sampling": [_P, _F, _F, _U64],
     "ms_model_set_pinned": [_P, _P],
     "ms_model_set_taps": [_P, _P, _P],
+    "ms_model_set_forward_graphs": [_P, _I],
     "ms_model_read_kv": [_P, _I, _I, _I, _I, _P, _P],
     "ms_file_open": [C.c_char_p, C.POINTER(C.c_void_p)], "ms_file_close": [_P],
     "ms_file_get_meta": [_P, C.POINTER(FileMeta)],
@@ -565,6 +566,10 @@ class Model:
 
     def reset(self) -> None:
         check(_lib.ms_model_reset(self.h))
+
+    def set_forward_graphs(self, on: bool) -> None:
+        """ms_forward's HIP graph replay of repeated calls (on by default)."""
+        check(_lib.ms_model_set_forward_graphs(self.h, 1 if on else 0))
 
     def set_sampling(self, temperature: float, penalty: float = 1.0, seed: int = 0) -> None:
         """temperature_sampling (lm_head.mojo:198-254) in prefill and decode

@@ -148,10 +148,12 @@ def run_harness(path: str, steps: int = BENCH_STEPS, batch: int = BENCH_BATCH,
     pos = batch
     dx = DeviceBuffer(batch * D * 4)   # the step's input rows, uploaded per step
     for s in range(steps):
+        # fresh rows before the clock starts, as the reference fills x before
+        # its timed layer loop (harness.mojo:256-262)
         x = host_normal(batch * D, seed, 1 + s).reshape(batch, D)
+        dx.upload(x)
         base = (C.c_int * 1)(pos)
         t0 = time.perf_counter_ns()
-        dx.upload(x)
         check(lib().ms_forward(model.h, dx.ptr, 1, batch, base, None))
         lat.append(time.perf_counter_ns() - t0)
         pos += batch

@@ -508,3 +508,34 @@ def test_sampled_draw_seeds_per_sequence(gpu, fast_oracle):
     assert seq0 != seq1
     assert sum(a == b for a, b in zip(seq1[:-1], seq0[1:])) < steps // 2
     m.close()
+
+
+def test_forward_graph_replays_equal_eager(gpu):
+    """ms_forward replays a captured HIP graph once a call repeats the previous
+    one's buffers, rows and position bucket (the harness loop).  The replays
+    must equal eager launches bit for bit: four rows a step (the harness), and
+    one row a step, both across a 64-position bucket edge (the attention's
+    key-chunk bound is part of the graph)."""
+    import ctypes as C
+    ms = gpu
+    arch = ms.arch_demo(max_len=512, n_layers=6)
+    say("forward graph replays vs eager: demo 6 layers, T=4 and T=1 steps")
+    a = build(ms, arch, max_seqs=1, max_rows=4, max_pos=512)
+    b = build(ms, arch, max_seqs=1, max_rows=4, max_pos=512)
+    b.set_forward_graphs(False)
+    for T, positions in ((4, list(range(40, 100, 4))), (1, list(range(100, 108)) + [120, 127, 128, 129])):
+        da, db = ms.DeviceBuffer(T * 1024 * 4), ms.DeviceBuffer(T * 1024 * 4)
+        ha, hb = ms.DeviceBuffer(6 * T * 1024 * 4), ms.DeviceBuffer(6 * T * 1024 * 4)
+        for s, p in enumerate(positions):
+            x = ms.host_normal(T * 1024, 900 + s, T).reshape(T, 1024)
+            base = (C.c_int * 1)(p)
+            da.upload(x)
+            db.upload(x)
+            ms.check(ms.lib().ms_forward(a.h, da.ptr, 1, T, base, ha.ptr))
+            ms.check(ms.lib().ms_forward(b.h, db.ptr, 1, T, base, hb.ptr))
+            assert np.array_equal(da.download(np.float32, (T, 1024)),
+                                  db.download(np.float32, (T, 1024))), (T, p)
+            assert np.array_equal(ha.download(np.float32, (6, T, 1024)),
+                                  hb.download(np.float32, (6, T, 1024))), (T, p)
+    a.close()
+    b.close()
