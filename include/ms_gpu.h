@@ -112,7 +112,9 @@ int ms_dequant_q4_packed(float *d_out, const uint8_t *d_packed, int K, int N,
  * matmul_q4_bpack :122-193 on a Q4Matrix).  A fp32 [M][K], W panel layout,
  * C fp32 [M][N].  accumulate=1 keeps the reference's C += semantics,
  * accumulate=0 overwrites.  Rows are processed in chunks of 16 (each row
- * quantized to a 31-bit fixed-point value, exact integer dot products);
+ * quantized to a 31-bit fixed-point value, exact integer dot products); up to
+ * four rows with K = 1024, 2048 or 4096 (or 2560 without accumulate) in one
+ * launch with a fixed-point shift per row and slice of 128 to 640 values of K;
  * K <= 16384. */
 int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
                  int K, int N, float scale, int accumulate);

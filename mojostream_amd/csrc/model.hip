@@ -272,8 +272,9 @@ static int launch_gemv_rec(const GemvArgs &a, hipStream_t st) {
 static int launch_proj_row(ms_model *m, const RunCfg &rc, GemvArgs a, const RowSrc &r,
                            int waves, int waves_row, hipStream_t st);
 
+constexpr size_t kLdsLimit = 150 * 1024;  // LDS of a GEMV launch with its limb rows
+
 static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipStream_t st) {
-  constexpr size_t kLdsLimit = 150 * 1024;
   if (a.M > kGemvMaxM) {
     // prefill rows: quantize every row once, then the MFMA GEMM
     GemmArgs g{};
@@ -306,13 +307,18 @@ static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipS
   return launch_gemv_rec(a, st);
 }
 
+// A batch-1 decode row through the per-wave prologue (AS_WAVES, waves_row
+// waves) when the matrix's shape has an instantiation and the row's limbs fit
+// the LDS; otherwise launch_proj.  (At two to four rows the per-row prologue
+// of launch_proj is faster.)
 static int launch_proj_row(ms_model *m, const RunCfg &rc, GemvArgs a, const RowSrc &r,
                            int waves, int waves_row, hipStream_t st) {
-  if (rc.one_row && a.M == 1 && a.K == waves_row * kWaveTiles * kSuperK) {
-    a.asrc = AS_WAVES;
-    a.rows = r;
-    a.waves = waves_row;
-    return launch_gemv_rec(a, st);
+  if (rc.one_row && a.M == 1 && !r.gamma && !r.x_out) {
+    GemvArgs w = a;
+    w.asrc = AS_WAVES;
+    w.rows = r;
+    w.waves = waves_row;
+    if (wave_shape_ok(w) && gemv_lds_need(w) <= kLdsLimit) return launch_gemv_rec(w, st);
   }
   return launch_proj(m, a, r, waves, st);
 }
@@ -458,7 +464,7 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
       pa.pos_bound = rc.pos_bound;
       a.at.chunks = dec_part_chunks(pa);
       if (int rc2 = launch_gemv_rec(a, st)) return rc2;
-    } else if (int rc2 = launch_proj(m, a, r, 8, st)) {
+    } else if (int rc2 = launch_proj_row(m, rc, a, r, 8, 8, st)) {
       return rc2;
     }
   }

@@ -31,9 +31,10 @@ enum GemvASource {
   AS_QUANT = 1,  // limbs prepared in global memory by launch_quant_rows
   AS_ATTN = 2,   // one row: the attention chunks of k_attn_part, merged per
                  // query head by the wave that owns the head's K range
-  AS_WAVES = 3,  // one row: each wave quantizes its own contiguous K slice
-                 // with its own shift (no block-wide prologue); the row's
-                 // RMSNorm factor is applied in the epilogue
+  AS_WAVES = 3,  // one to four rows: each wave quantizes its own contiguous
+                 // K slice of every row with its own shift per row (no
+                 // block-wide prologue); a row's RMSNorm factor is applied in
+                 // the epilogue
 };
 
 // AS_ATTN: the chunk partials of one decode row (layout in attention.h:
@@ -124,11 +125,17 @@ struct GemmArgs {
 };
 
 constexpr int kGemvMaxM = 16;
-// AS_WAVES: super-tiles per wave (640 values: K = 2560 on 4 waves, 10240 on 16)
-constexpr int kWaveTiles = 5;
+// AS_WAVES: at most this many rows, and K = waves * tpw * 128 (tpw super-tiles
+// per wave; E4B: 5 on 4 waves for K = 2560 and on 16 for 10240; the demo
+// model: 2 for K = 1024 on 4 waves and 4096 on 16)
+constexpr int kWaveRowsMax = 4;
 constexpr int kQuantMaxK = 16384;  // longest row a 1024-thread block quantizes
 
 int launch_gemv(const GemvArgs &a, hipStream_t st);
+// (epilogue, panels, waves, K) of a GemvArgs that an AS_WAVES launch takes:
+// store with 4 waves (tpw 2, 5) or 8 (tpw 1, 2, 4), accumulate with 8, SwiGLU
+// with 4 (tpw 2, 5), residual with 16 (tpw 2, 5) or 8 (tpw 1, 2, 4)
+bool wave_shape_ok(const GemvArgs &a);
 // LDS bytes a GEMV launch needs.
 size_t gemv_lds_need(const GemvArgs &a);
 // Quantize M rows of length K (one block per row) into q.

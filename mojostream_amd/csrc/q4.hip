@@ -478,12 +478,15 @@ constexpr int gemv_batch() {
 }
 
 // LDS layout: int partial sums [W][P][C][256], output values [P][M][16],
-// per-row shift, then (AS_ROWS) limb rows [4M][K + 16] (16-byte aligned).
+// shifts, then (AS_ROWS, AS_ATTN, AS_WAVES) limb rows [4M][K + 16] (16-byte
+// aligned).
 __host__ __device__ inline size_t gemv_lds_red(int W, int P, int C) {
   return (size_t)W * P * C * 256 * 4;
 }
+// shifts: one per row, or per (row, wave) with AS_WAVES (4 rows x 16 waves)
+constexpr int kRowShiftSlots = 64;
 __host__ __device__ inline size_t gemv_lds_fixed(int W, int P, int C, int M) {
-  return gemv_lds_red(W, P, C) + (size_t)P * M * 16 * 4 + (size_t)kGemvMaxM * 4;
+  return gemv_lds_red(W, P, C) + (size_t)P * M * 16 * 4 + (size_t)kRowShiftSlots * 4;
 }
 __host__ __device__ inline int gemv_ldl(int K) { return K + 16; }
 
@@ -725,65 +728,85 @@ __device__ inline void attn_merge_quant(const AttnSrc &at_, int8_t *limbs, int l
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-// AS_WAVES prologue of wave `wave`: the wave's slice of the row, K values
-// [128 TPW wave, 128 TPW (wave + 1)), as 8-value groups (lane l: groups l and
-// l + 64).  y = x * pre_scale; the wave's own maximum |y| sets its shift, its
-// sum of y^2 goes to ssw[wave] for the epilogue's RMSNorm factor.  The limbs
-// go to the block's limb rows in the wave's K range only, which the wave alone
-// reads, so no block barrier.  The row's loads are waited for before the
-// first weights go out (kw): they would otherwise queue behind the weights.
-// yv keeps y for the epilogue (the normalized row, block 0).
-template <int TPW, class KW>
-__device__ inline void wave_rows_quant(const RowSrc &rs, int K, int8_t *limbs, int ldl,
-                                       int32_t *row_s, float *ssw, float (&yv)[2][8], int wave,
+// AS_WAVES instantiations carry the row bound and the super-tiles per wave in
+// the RP template slot: RP = 10 * rows + tiles.
+__host__ __device__ constexpr int waves_rows(int rp) { return rp / 10; }
+__host__ __device__ constexpr int waves_tpw(int rp) { return rp % 10; }
+// 64-lane slots of 8-value groups that hold a wave's slice of one row
+__host__ __device__ constexpr int waves_nsl(int rp) { return (waves_tpw(rp) * 16 + 63) / 64; }
+
+// AS_WAVES prologue of wave `wave` in a block of W waves: the wave's slice of
+// each row, K values [128 TPW wave, 128 TPW (wave + 1)), as 8-value groups
+// (lane l: groups l, l + 64, ..).  y = x * pre_scale; the wave's own maximum
+// |y| of row m sets its shift row_s[m W + wave], its sum of y^2 goes to
+// ssw[m W + wave] for the epilogue's RMSNorm factor.  A row's arithmetic
+// does not depend on the other rows, so a row gives the same limbs, shifts
+// and sums in a launch of any row count.  The limbs go to the block's limb
+// rows in the wave's K range only, which the wave alone reads, so no block
+// barrier.  The rows' loads are waited for before the first weights go out
+// (kw): they would otherwise queue behind the weights.  yv keeps y for the
+// epilogue (the normalized rows, block 0).
+template <int TPW, int MR, int W, class KW>
+__device__ inline void wave_rows_quant(const RowSrc &rs, int M, int8_t *limbs, int ldl,
+                                       int32_t *row_s, float *ssw,
+                                       float (&yv)[MR][(TPW * 16 + 63) / 64][8], int wave,
                                        int lane, KW kw) {
   constexpr int NG8 = TPW * 16;
+  constexpr int NSL = (NG8 + 63) / 64;
   const int k0 = wave * TPW * 128;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int gq = lane + 64 * r;
+  for (int m = 0; m < MR; ++m)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) yv[r][e] = 0.f;
-    if (gq < NG8) {
-      const float *p = rs.x + k0 + 8 * gq;
-      const float4 a = ldg<float4>(p), b = ldg<float4>(p + 4);
-      yv[r][0] = a.x; yv[r][1] = a.y; yv[r][2] = a.z; yv[r][3] = a.w;
-      yv[r][4] = b.x; yv[r][5] = b.y; yv[r][6] = b.z; yv[r][7] = b.w;
+    for (int r = 0; r < NSL; ++r) {
+      const int gq = lane + 64 * r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) yv[m][r][e] = 0.f;
+      if ((MR == 1 || m < M) && gq < NG8) {
+        const float *p = rs.x + (size_t)m * rs.ld + k0 + 8 * gq;
+        const float4 a = ldg<float4>(p), b = ldg<float4>(p + 4);
+        yv[m][r][0] = a.x; yv[m][r][1] = a.y; yv[m][r][2] = a.z; yv[m][r][3] = a.w;
+        yv[m][r][4] = b.x; yv[m][r][5] = b.y; yv[m][r][6] = b.z; yv[m][r][7] = b.w;
+      }
     }
-  }
-  asm volatile("" ::"v"(yv[0][0]), "v"(yv[1][7]) : "memory");
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+    asm volatile("" ::"v"(yv[m][0][0]), "v"(yv[m][NSL - 1][7]) : "memory");
   kw();
-  float mx = 0.f, ss = 0.f;
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int m = 0; m < MR; ++m) {
+    if (MR > 1 && m >= M) break;
+    float mx = 0.f, ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float y = yv[r][e] * rs.pre_scale;
-      yv[r][e] = y;
-      ss += y * y;
-      mx = fmaxf(mx, fabsf(y));
+    for (int r = 0; r < NSL; ++r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = yv[m][r][e] * rs.pre_scale;
+        yv[m][r][e] = y;
+        ss += y * y;
+        mx = fmaxf(mx, fabsf(y));
+      }
+    mx = wave_max(mx);
+    ss = wave_sum(ss);
+    const int s = row_shift(mx);
+    const float mul = ldexpf(1.0f, s);
+#pragma unroll
+    for (int r = 0; r < NSL; ++r) {
+      const int gq = lane + 64 * r;
+      if (gq < NG8) {
+        uint32_t lo[4], hi[4];
+        quant8<false>(yv[m][r], mul, lo, hi);
+        const int pos = limb_pos8(k0 + 8 * gq);
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+          *reinterpret_cast<uint2 *>(limbs + (size_t)(4 * m + l) * ldl + pos) =
+              uint2{lo[l], hi[l]};
+      }
     }
-  mx = wave_max(mx);
-  ss = wave_sum(ss);
-  const int s = row_shift(mx);
-  const float mul = ldexpf(1.0f, s);
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int gq = lane + 64 * r;
-    if (gq < NG8) {
-      uint32_t lo[4], hi[4];
-      quant8<false>(yv[r], mul, lo, hi);
-      const int pos = limb_pos8(k0 + 8 * gq);
-#pragma unroll
-      for (int l = 0; l < 4; ++l)
-        *reinterpret_cast<uint2 *>(limbs + (size_t)l * ldl + pos) = uint2{lo[l], hi[l]};
+    if (lane == 0) {
+      row_s[m * W + wave] = s;
+      ssw[m * W + wave] = ss;
     }
   }
-  if (lane == 0) {
-    row_s[wave] = s;
-    ssw[wave] = ss;
-  }
-  (void)K;
   // this wave's limb stores before its own operand reads
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
@@ -812,7 +835,8 @@ __device__ inline double lanes_sum_d(double v) {
 // C: 16-row MFMA groups (4 limb rows per activation row: M <= 4C).
 // P: panels per block.  AS: GemvASource.  W: waves per block.  EPI: epilogue.
 // RP: activation rows whose loads the AS_ROWS prologue issues at once
-// (AS_ATTN: attention chunks per load batch).
+// (AS_ATTN: head dim and load batch, attn_hd / attn_nj; AS_WAVES: row bound
+// and super-tiles per wave, waves_rows / waves_tpw).
 //
 // Block pg = P panels of 16 columns over the whole K.  Wave w owns super-tiles
 // w, w+W, ...; each batch issues U of them (P panels each) before any is
@@ -821,13 +845,17 @@ __device__ inline double lanes_sum_d(double v) {
 template <int C, int P, int AS, int W, int EPI, int RP>
 __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ float sh[W > 8 ? 32 : (8 * W > 32 ? 8 * W : 32)];  // reduction scratch
+  // reduction scratch (AS_WAVES: a sum of squares per (row, wave))
+  __shared__ float sh[W > 4 ? 64 : 32];
   constexpr int NT = 64 * W;
   // AS_ATTN: the head's super-tiles, one batch
   // (AS_WAVES: the wave's RP super-tiles, one batch)
   constexpr int U = AS == AS_ATTN    ? attn_hd(RP) / 128
-                    : AS == AS_WAVES ? RP
+                    : AS == AS_WAVES ? waves_tpw(RP)
                                      : gemv_batch<C, P, AS, W>();
+  // rows a WAVE_K epilogue finishes (AS_ATTN: one)
+  constexpr int MR = AS == AS_WAVES ? waves_rows(RP) : 1;
+  constexpr int NSL = AS == AS_WAVES ? waves_nsl(RP) : 1;
   constexpr bool WAVE_K = AS == AS_ATTN || AS == AS_WAVES;  // contiguous K per wave
   // wave-uniform in a scalar register: tile predicates below are then scalar
   // branches, and loads behind them need no merge (and no wait) at the join
@@ -886,10 +914,15 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
 
   // WAVE_K, residual epilogue: the thread that finishes output (p, j) loads
   // its residual value now (a memory round trip off the epilogue's path)
-  float resid_pre = 0.f;
+  float resid_pre[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) resid_pre[m] = 0.f;
   if constexpr (WAVE_K && EPI == EPI_RESID) {
     const int t = threadIdx.x, w = t % W, p = (t / W) % P, j = t / (W * P);
-    if (t < 16 * P * W && w == 0 && wv[p]) resid_pre = ldg<float>(resid + col[p] + j);
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if ((MR == 1 || m < M) && t < 16 * P * W && w == 0 && wv[p])
+        resid_pre[m] = ldg<float>(resid + (size_t)m * ldo + col[p] + j);
   }
   int32_t *red = reinterpret_cast<int32_t *>(lds);
   float *vals = reinterpret_cast<float *>(lds + gemv_lds_red(W, P, C));
@@ -905,7 +938,7 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
 
   uint4 q[U][P];
   v4i af[AS == AS_QUANT ? U : 1][C][2];
-  float yv[2][8];  // AS_WAVES: the wave's y values (for the normalized row)
+  float yv[MR][NSL][8];  // AS_WAVES: the wave's y values (for the normalized rows)
   // Loads of super-tiles u0..u1-1 of batch bt; tiles past the end of K are
   // not loaded (their slots stay zero and are never consumed).
   auto tile = [&](int bt, int u) {
@@ -995,8 +1028,8 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
                                                    [&] { issue(0); });
   } else if constexpr (AS == AS_WAVES) {
     constexpr int kEarlyW = (4 / P) < 1 ? 1 : ((4 / P) < U ? (4 / P) : U);
-    wave_rows_quant<RP>(rs, K, limbs, ldl, row_s, sh, yv, wave, lane,
-                        [&] { issue_part(0, 0, kEarlyW); });
+    wave_rows_quant<U, MR, W>(rs, M, limbs, ldl, row_s, sh, yv, wave, lane,
+                              [&] { issue_part(0, 0, kEarlyW); });
     if constexpr (kEarlyW < U) issue_part(0, kEarlyW, U);
   } else {
     if ((int)threadIdx.x < M) row_s[threadIdx.x] = ldg<int32_t>(qr.shift + threadIdx.x);
@@ -1080,67 +1113,82 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   // int64, scale once.  Each output is finished by the thread that sums it
   // (no second pass through LDS).
   if constexpr (WAVE_K) {
-    // One row, one shift per wave: thread t takes column j, panel slot p and
-    // wave w (t = (j P + p) W + w), combines that wave's limb sums exactly and
-    // scales them by the wave's shift; the W lanes of (j, p) are then added.
+    // One shift per (row, wave): thread t takes column j, panel slot p and
+    // wave w (t = (j P + p) W + w), combines that wave's limb sums of a row
+    // exactly and scales them by the wave's shift; the W lanes of (j, p) are
+    // then added.  Rows one after another, each on its own.
     static_assert(16 * P * W <= NT, "one thread per (column, panel, wave)");
-    static_assert(EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_SWIGLU,
-                  "per-wave shifts: store, residual or SwiGLU epilogue");
+    static_assert(EPI == EPI_STORE || EPI == EPI_ACCUMULATE || EPI == EPI_RESID ||
+                      EPI == EPI_SWIGLU,
+                  "per-wave shifts: store, accumulate, residual or SwiGLU epilogue");
+    static_assert(C == 1, "per-wave shifts: at most four rows");
     const int t = threadIdx.x;
     const int w = t % W, p = (t / W) % P, j = t / (W * P);
     const bool on = t < 16 * P * W;
-    double v = 0.0;
-    if (on) {
-      long long tw = 0;
+    float inv[MR];
 #pragma unroll
-      for (int l = 0; l < 4; ++l)
-        tw += (long long)red[((size_t)w * P + p) * C * 256 + dfrag(l, j)] << (8 * l);
-      v = (double)tw * (double)ldexpf(1.0f, -row_s[w]);
-    }
-    v = lanes_sum_d<W>(v);
-    // RMSNorm of the row (rmsnorm_inplace kernels.mojo:474-489) as a factor on
-    // the products: y . W = inv (x . W)
-    float inv = 1.0f;
-    if (AS == AS_WAVES && rs.norm) {
-      float ssum = 0.f;
+    for (int m = 0; m < MR; ++m) {
+      if (MR > 1 && m >= M) break;
+      double v = 0.0;
+      if (on) {
+        long long tw = 0;
 #pragma unroll
-      for (int u = 0; u < W; ++u) ssum += sh[u];
-      inv = 1.0f / sqrtf(ssum / (float)K + 1e-6f);
-    }
-    if constexpr (EPI == EPI_SWIGLU) {
-      // gate (p = 0) and up (p = 1) of column j sit W lanes apart
-      const double vu = __shfl_down(v, W, 64);
-      if (on && w == 0 && p == 0) {
-        const float gt = (float)(v * (double)inv * (double)wsc[0]);
-        const float up = (float)(vu * (double)inv * (double)wsc[1]);
-        sw_out[col[0] + j] = up * gt * (1.0f / (1.0f + expf(-gt)));
+        for (int l = 0; l < 4; ++l)
+          tw += (long long)red[((size_t)w * P + p) * 256 + dfrag(4 * m + l, j)] << (8 * l);
+        v = (double)tw * (double)ldexpf(1.0f, -row_s[m * W + w]);
       }
-    } else {
-      if (on && w == 0 && wv[p]) {
-        const float val = (float)(v * (double)inv * (double)wsc[p]);
-        const size_t oi = (size_t)col[p] + j;
-        if constexpr (EPI == EPI_STORE) {
-          out[oi] = val;
-        } else {
-          // x = x + proj (gemma4_e4b.mojo:522,538)
-          const float x = resid_pre + val;
-          out[oi] = x;
-          if (out2) out2[oi] = x;
+      v = lanes_sum_d<W>(v);
+      // RMSNorm of the row (rmsnorm_inplace kernels.mojo:474-489) as a factor
+      // on the products: y . W = inv (x . W)
+      inv[m] = 1.0f;
+      if (AS == AS_WAVES && rs.norm) {
+        float ssum = 0.f;
+#pragma unroll
+        for (int u = 0; u < W; ++u) ssum += sh[m * W + u];
+        inv[m] = 1.0f / sqrtf(ssum / (float)K + 1e-6f);
+      }
+      if constexpr (EPI == EPI_SWIGLU) {
+        // gate (p = 0) and up (p = 1) of column j sit W lanes apart
+        const double vu = __shfl_down(v, W, 64);
+        if (on && w == 0 && p == 0) {
+          const float gt = (float)(v * (double)inv[m] * (double)wsc[0]);
+          const float up = (float)(vu * (double)inv[m] * (double)wsc[1]);
+          sw_out[(size_t)m * ldo_sw + col[0] + j] = up * gt * (1.0f / (1.0f + expf(-gt)));
+        }
+      } else {
+        if (on && w == 0 && wv[p]) {
+          const float val = (float)(v * (double)inv[m] * (double)wsc[p]);
+          const size_t oi = (size_t)m * ldo + col[p] + j;
+          if constexpr (EPI == EPI_STORE) {
+            out[oi] = val;
+          } else if constexpr (EPI == EPI_ACCUMULATE) {
+            out[oi] += val;
+          } else {
+            // x = x + proj (gemma4_e4b.mojo:522,538)
+            const float x = resid_pre[m] + val;
+            out[oi] = x;
+            if (out2) out2[oi] = x;
+          }
         }
       }
     }
     if constexpr (AS == AS_WAVES) {
-      // the normalized row, y * inv (block 0): the next projections' residual
+      // the normalized rows, y * inv (block 0): the next projections' residual
       if (blockIdx.x == 0 && rs.y_out) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int gq = lane + 64 * r;
-          if (gq < RP * 16) {
-            float *o = rs.y_out + wave * RP * 128 + 8 * gq;
-            *reinterpret_cast<float4 *>(o) = float4{yv[r][0] * inv, yv[r][1] * inv,
-                                                    yv[r][2] * inv, yv[r][3] * inv};
-            *reinterpret_cast<float4 *>(o + 4) = float4{yv[r][4] * inv, yv[r][5] * inv,
-                                                        yv[r][6] * inv, yv[r][7] * inv};
+        for (int m = 0; m < MR; ++m) {
+          if (MR > 1 && m >= M) break;
+#pragma unroll
+          for (int r = 0; r < NSL; ++r) {
+            const int gq = lane + 64 * r;
+            if (gq < U * 16) {
+              float *o = rs.y_out + (size_t)m * K + wave * U * 128 + 8 * gq;
+              const float f = inv[m];
+              *reinterpret_cast<float4 *>(o) = float4{yv[m][r][0] * f, yv[m][r][1] * f,
+                                                      yv[m][r][2] * f, yv[m][r][3] * f};
+              *reinterpret_cast<float4 *>(o + 4) = float4{yv[m][r][4] * f, yv[m][r][5] * f,
+                                                          yv[m][r][6] * f, yv[m][r][7] * f};
+            }
           }
         }
       }
@@ -1285,6 +1333,23 @@ size_t gemv_lds_need(const GemvArgs &a) {
   return b;
 }
 
+bool wave_shape_ok(const GemvArgs &a) {
+  const int w = a.waves;
+  if (w <= 0 || a.K % (w * kSuperK) != 0) return false;
+  const int tpw = a.K / (w * kSuperK);
+  switch (a.epi) {
+    case EPI_STORE:
+      return a.P == 1 && ((w == 4 && (tpw == 2 || tpw == 5)) ||
+                          (w == 8 && (tpw == 1 || tpw == 2 || tpw == 4)));
+    case EPI_ACCUMULATE: return a.P == 1 && w == 8 && (tpw == 1 || tpw == 2 || tpw == 4);
+    case EPI_SWIGLU: return a.P == 2 && w == 4 && (tpw == 2 || tpw == 5);
+    case EPI_RESID:
+      return a.P == 1 && ((w == 16 && (tpw == 2 || tpw == 5)) ||
+                          (w == 8 && (tpw == 1 || tpw == 2 || tpw == 4)));
+    default: return false;
+  }
+}
+
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_CHECK_ARG(a.M >= 1 && a.M <= kGemvMaxM, "GEMV: 1 <= M <= 16");
   MS_CHECK_ARG(a.K >= kSuperK && a.K % kSuperK == 0, "GEMV: K % 128 != 0");
@@ -1303,13 +1368,11 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
                  "GEMV: row prologue needs rows (no gamma)");
     MS_CHECK_ARG(a.K <= 8 * rows_ng(a.waves) * 64 * a.waves, "GEMV: row prologue: row too long");
   } else if (a.asrc == AS_WAVES) {
-    MS_CHECK_ARG(a.M == 1 && a.rows.x && !a.rows.gamma && !a.rows.x_out &&
-                     a.K == a.waves * kWaveTiles * kSuperK &&
-                     ((a.epi == EPI_STORE && a.P == 1 && a.waves == 4) ||
-                      (a.epi == EPI_SWIGLU && a.P == 2 && a.waves == 4) ||
-                      (a.epi == EPI_RESID && a.P == 1 && a.waves == 16)),
-                 "GEMV: per-wave rows: one row, K = waves * 640, store (4 waves), "
-                 "SwiGLU (4 waves) or residual (16 waves)");
+    MS_CHECK_ARG(a.M <= kWaveRowsMax && a.rows.x && a.rows.ld >= a.K && !a.rows.gamma &&
+                     !a.rows.x_out && wave_shape_ok(a),
+                 "GEMV: per-wave rows: at most 4 rows, K = waves * tpw * 128 with tpw 1, 2, "
+                 "4 or 5, and store or accumulate (4 or 8 waves), SwiGLU (4 waves) or "
+                 "residual (8 or 16 waves)");
   } else if (a.asrc == AS_ATTN) {
     MS_CHECK_ARG(a.M == 1 && a.P == 1 && a.waves == 8 && a.epi == EPI_RESID,
                  "GEMV: attention source: one row, one panel per block, 8 waves, residual");
@@ -1358,10 +1421,32 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_GEMV(EPI_RESID, 1, AS_ROWS, 16)
   MS_GEMV(EPI_RESID, 1, AS_QUANT, 4)
   if (!ok && a.asrc == AS_WAVES) {
-    if (a.epi == EPI_STORE) MS_GEMV_L(1, EPI_STORE, 1, AS_WAVES, 4, kWaveTiles);
-    else if (a.epi == EPI_SWIGLU) MS_GEMV_L(1, EPI_SWIGLU, 2, AS_WAVES, 4, kWaveTiles);
-    else MS_GEMV_L(1, EPI_RESID, 1, AS_WAVES, 16, kWaveTiles);
-    ok = true;
+    // RP = 10 * row bound + super-tiles per wave; one row has instantiations
+    // of its own (fewer registers)
+    const int tpw = a.K / (a.waves * kSuperK);
+#define MS_GEMV_W(EP, PP, WW, T)                                       \
+  if (!ok && a.epi == EP && a.waves == WW && tpw == T) {               \
+    if (a.M == 1) MS_GEMV_L(1, EP, PP, AS_WAVES, WW, 10 + T);          \
+    else MS_GEMV_L(1, EP, PP, AS_WAVES, WW, 10 * kWaveRowsMax + T);     \
+    ok = true;                                                         \
+  }
+    MS_GEMV_W(EPI_STORE, 1, 4, 5)
+    MS_GEMV_W(EPI_STORE, 1, 4, 2)
+    MS_GEMV_W(EPI_SWIGLU, 2, 4, 5)
+    MS_GEMV_W(EPI_SWIGLU, 2, 4, 2)
+    MS_GEMV_W(EPI_RESID, 1, 16, 5)
+    MS_GEMV_W(EPI_RESID, 1, 16, 2)
+    MS_GEMV_W(EPI_RESID, 1, 8, 1)
+    MS_GEMV_W(EPI_RESID, 1, 8, 2)
+    MS_GEMV_W(EPI_RESID, 1, 8, 4)
+    MS_GEMV_W(EPI_STORE, 1, 8, 1)
+    MS_GEMV_W(EPI_STORE, 1, 8, 2)
+    MS_GEMV_W(EPI_STORE, 1, 8, 4)
+    MS_GEMV_W(EPI_ACCUMULATE, 1, 8, 1)
+    MS_GEMV_W(EPI_ACCUMULATE, 1, 8, 2)
+    MS_GEMV_W(EPI_ACCUMULATE, 1, 8, 4)
+#undef MS_GEMV_W
+    MS_CHECK_ARG(ok, "GEMV: per-wave rows: no instantiation for this shape");
   }
   if (!ok && a.asrc == AS_ATTN) {
     // the row-prologue template slot carries the head dim and the load pairs
@@ -1515,6 +1600,27 @@ static int q4_matmul_impl(float *d_C, const float *d_A, const uint8_t *d_packed,
     g.out = d_C;
     g.ldo = N;
     return launch_gemm(g, st);
+  }
+  if (M <= kWaveRowsMax) {
+    // one launch: each wave quantizes its own K slice of the rows (a shift
+    // per row and wave), no quantization pass before the GEMV
+    GemvArgs a{};
+    a.epi = accumulate ? EPI_ACCUMULATE : EPI_STORE;
+    a.asrc = AS_WAVES;
+    a.K = K;
+    a.M = M;
+    a.rows.x = d_A;
+    a.rows.ld = K;
+    a.rows.pre_scale = 1.f;
+    a.seg[0] = GemvSeg{d_packed, scale, N, 0};
+    a.nseg = 1;
+    a.P = 1;
+    a.out = d_C;
+    a.ldo = N;
+    for (const int w : {8, 4}) {
+      a.waves = w;
+      if (wave_shape_ok(a) && gemv_lds_need(a) <= 150 * 1024) return launch_gemv(a, st);
+    }
   }
   const int chunk = kGemvMaxM;
   const int P = (N / 16) % 4 == 0 && N >= 4 * 16 * 512 ? 4 : 1;

@@ -88,7 +88,9 @@ def test_q4_matmul_vs_f64(gpu, oracle, M, K, N):
                                    (2048, 1024, 2560)])
 def test_q4_gemm_rows_equal_gemv_rows(gpu, M, K, N):
     """The GEMM (M > 16) and the GEMV (row chunks of <= 16) use the same exact
-    integer operands and the same scaling, so every row must agree bit for bit."""
+    integer operands and the same scaling, so every row must agree bit for bit.
+    (Calls of at most four rows quantize each slice of K with its own shift,
+    finer than one shift per row; they are checked against the f64 oracle.)"""
     ms = gpu
     say(f"GEMM vs GEMV rows M={M} K={K} N={N}")
     q4 = ms.host_random_u8(K * N // 2, 31, K + N).reshape(K, N // 2)
