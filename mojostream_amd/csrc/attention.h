@@ -34,6 +34,10 @@ struct AttnArgs {
   // beyond the launched chunks: the host must keep the bound.
   int pos_bound;
   int grid_chunks;  // set by the launcher
+  // decode partials: cos and sin of the RoPE angles at the row's position,
+  // [2][rot / 2] (written before the launch: by the one-row Q|K|V projection
+  // or by launch_rope_cur), read at kernel entry instead of the tables
+  const float *rope_cur;
 };
 
 constexpr int kAttnChunk = 16;
@@ -52,7 +56,8 @@ inline size_t attn_part_floats(int B, int n_kv, int n_chunks, int T, int G, int 
 // the block holding the current slot appends the row's k and v to the cache.
 // The O projection merges the chunks (AttnSrc in q4.h).  Per sequence, at
 // a.part: o [kDecPartMaxChunks][n_heads][hd], then (m, l)
-// [kDecPartMaxChunks][n_heads][2].  Needs G <= 4 and at most kDecPartMaxChunks
+// [kDecPartMaxChunks][n_heads][2].  Needs G <= 4, head dim 256 or 512 and at
+// most kDecPartMaxChunks
 // launched chunks (dec_part_ok).
 constexpr int kDecPartChunk = 32;
 constexpr int kDecPartMaxChunks = 64;
@@ -63,6 +68,8 @@ inline size_t dec_part_floats(int B, int n_heads, int hd) {
 int dec_part_chunks(const AttnArgs &a);
 bool dec_part_ok(const AttnArgs &a);
 int launch_attention_partials(const AttnArgs &a, hipStream_t st);
+// a.rope_cur from the tables at the position of sequence 0 (one block)
+int launch_rope_cur(const AttnArgs &a, hipStream_t st);
 
 // T == 1 (decode): one launch; the chunk blocks append the row to the cache and
 // the last block of each (sequence, kv head) merges the chunks (needs a.ctr).

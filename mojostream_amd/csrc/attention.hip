@@ -38,6 +38,17 @@ __device__ inline float4 aldg<float4>(const void *p) {
   return float4{v.x, v.y, v.z, v.w};
 }
 
+// A value that is the same for every lane, loaded per lane (an opaque zero
+// offset): the compiler keeps it in a vector register instead of waiting for
+// it at once to move it into a scalar register, so the loads issued after it
+// go out before it arrives.
+template <class T>
+__device__ inline T aldg_lane(const T *p) {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return aldg<T>(p + z);
+}
+
 // Launch parameters as scalars, read once at kernel entry (an opaque register
 // move keeps the compiler from re-reading the argument struct later).
 template <class T>
@@ -50,7 +61,7 @@ struct AttnP {
   int T, q_dim, kv_dim, n_heads, n_kv, G, rot, half, circular, cache_len, clamp, ld, apply_rope,
       n_chunks, write_cache, grid_chunks;
   float scale;
-  const float *qkv, *cos_t, *sin_t;
+  const float *qkv, *cos_t, *sin_t, *rope_cur;
   const int32_t *pos;
   float *kc, *vc, *part, *out;
   unsigned *ctr;
@@ -77,6 +88,7 @@ __device__ inline AttnP load_params(const AttnArgs &a) {
   p.grid_chunks = keep(a.grid_chunks);
   p.scale = keep(a.scale);
   p.qkv = keep(a.qkv);
+  p.rope_cur = keep(a.rope_cur);
   p.cos_t = keep(a.cos_t);
   p.sin_t = keep(a.sin_t);
   p.pos = keep(a.pos);
@@ -1026,6 +1038,13 @@ __device__ inline void rope_cs(const AttnP &p, int d, int pos, float &c, float &
   c = rot ? aldg<float>(p.cos_t + ti) : 1.f;
   s = rot ? aldg<float>(p.sin_t + ti) : 0.f;
 }
+// rope_cs from the factors prepared for the row's position ([2][rot / 2])
+__device__ inline void rope_cur_cs(const AttnP &p, int d, float &c, float &s) {
+  const bool rot = p.apply_rope && d < p.rot;
+  const int i = d < p.half ? d : d - p.half;
+  c = rot ? aldg<float>(p.rope_cur + i) : 1.f;
+  s = rot ? aldg<float>(p.rope_cur + p.half + i) : 0.f;
+}
 __device__ inline float rope_mix(const AttnP &p, int d, float x, float y, float c, float s) {
   if (!(p.apply_rope && d < p.rot)) return x;
   return d < p.half ? x * c - y * s : y * s + x * c;
@@ -1075,7 +1094,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
   // host launches only the chunks its bound on the position can reach, so
   // the rows are loaded before the position arrives (slots past it are
   // zeroed below).
-  const int base = aldg<int32_t>(p.pos + b);
+  const int base = aldg_lane<int32_t>(p.pos + b);
   float4 kr[F4], vr[F4];
 #pragma unroll
   for (int j = 0; j < F4; ++j) {
@@ -1386,95 +1405,119 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
 
 // ------------------------------------------------------------------------------
 // k_attn_part: the decode attention of one row per sequence without the merge.
-// Block (c, b x h): cache slots 32c..32c+31 of sequence b, kv head h, for its
-// G <= 4 query heads.  Like k_attn_decode, the chunk's cached rows, q and the
-// fresh k, v are loaded before the position arrives (the host launches only
-// the chunks below its bound on the position), rows past the attended ones
-// are zeroed, and the slot of the current position takes the fresh row (and
-// appends it to the cache).  Then scores (dot over the head dim, 8 lanes per
-// key), the chunk's softmax numerators (max and sum over its keys) and
-// o = sum_k e^(s_k - m) v_k, stored with (m, l) per query head.  The consumer
-// (the O projection) merges the chunks, so no block waits for another.
+// Block (c, b x h), 1024 threads: cache slots 32c..32c+31 of sequence b, kv
+// head h, for its G <= 4 query heads.  The chunk's cached rows, q, the fresh
+// k, v and the RoPE factors prepared for the position are loaded before the
+// position arrives (branch-free range-checked loads; the host launches only
+// the chunks below its bound on the position); rows past the attended ones
+// are zeroed and the slot of the current position takes the fresh row (and
+// appends it to the cache).  Thread t holds dims of key t / 32 (32 lanes per
+// key, coalesced 16-byte pieces): the scores are its partial dots summed over
+// the key's lanes, then the chunk's softmax numerators (max and sum over its
+// keys), and o = sum_k e^(s_k - m) v_k over groups of keys (V through LDS),
+// stored with (m, l) per query head.  The consumer (the O projection) merges
+// the chunks, so no block waits for another.  Sixteen waves keep every SIMD
+// busy and every dependent step short.
 // ------------------------------------------------------------------------------
-// sum / max over the 8 lanes of each half-row (quad permutes, then the
-// half-row mirror)
-__device__ inline float row8_sum(float v) {
-  v += adpp<0xB1>(v);
-  v += adpp<0x4E>(v);
-  return v + adpp<0x141>(v);
-}
-
-template <int HD, int CH>
-__global__ __launch_bounds__(256) void k_attn_part(AttnArgs args) {
+template <int HD, int GQ>
+__global__ __launch_bounds__(1024) void k_attn_part(AttnArgs args) {
   extern __shared__ __align__(16) float lds[];
-  static_assert(CH == 16 || CH == 32, "16 or 32 keys per chunk");
-  constexpr int LPK = 256 / CH;          // lanes per key in the scores
-  constexpr int TGM = 4;
-  constexpr int F4 = CH * HD / 4 / 256;  // float4 of K (and of V) per thread
-  constexpr int NV = HD / (4 * LPK);     // float4 per thread per key (scores)
-  constexpr int DPT = (HD + 255) / 256;  // head dims per thread (fresh row)
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int CH = kDecPartChunk;
+  static_assert(CH == 32, "32 keys per chunk: one key per 32 lanes");
+  constexpr int NT = 1024;
   constexpr int H4 = HD / 4;
-  constexpr int UPT = (TGM * H4 + 255) / 256;  // P.V float4 units per thread
-  // key rows in LDS at a pitch of HD + 32 floats: the 16 lanes of one LDS
-  // read pass (two keys, eight dim groups each) fall in distinct banks
-  constexpr int KP = HD + 32;
+  constexpr int NF = HD / 128;                  // float4 of a key row per thread
+  constexpr int QPT = (GQ * HD + NT - 1) / NT;   // q elements per thread (staging)
+  constexpr int NU = GQ * H4;                   // P.V float4 units (head, dims)
+  constexpr int NKG = NT / NU;                  // key groups of the P.V sums
+  constexpr int KPG = CH / NKG;                 // keys per group
+  static_assert(NF >= 1 && NKG >= 1 && CH % NKG == 0, "head dim 256 or 512");
+  constexpr uint32_t kOut = 0x80000000u;
   const AttnP p = load_params(args);
   const int tid = threadIdx.x;
   const int c = blockIdx.x;
-  const int b = (int)blockIdx.y / p.n_kv, h = (int)blockIdx.y % p.n_kv;
   const int G = p.G;
+  // blockIdx.y = (b n_kv + h) NS + s: query heads s GQ .. s GQ + GQ - 1 of
+  // kv head h (the G heads of a kv head split over NS blocks)
+  const int NS = G > GQ ? G / GQ : 1;
+  const int s = (int)blockIdx.y % NS, bh = (int)blockIdx.y / NS;
+  const int b = bh / p.n_kv, h = bh % p.n_kv;
+  const int g0 = s * GQ;                 // first query head of the block
+  const int Gl = min(GQ, G - g0);        // its query heads
   const int L = p.cache_len;
-  const int nq = G * HD;
+  const int nq = Gl * HD;
+  const int key = tid >> 5, j = tid & 31;
 
-  float *sk = lds;              // [CH][KP] keys of the chunk
-  float *sv = sk + CH * KP;     // [CH][HD] values
-  float *sq = sv + CH * HD;     // [TGM][HD] rotated queries
-  float *ss = sq + TGM * HD;    // [TGM][CH] scores -> numerators
-  float *sm = ss + TGM * CH;    // [TGM]
-  float *sl = sm + TGM;         // [TGM]
+  float *sv = lds;               // [CH][HD] values
+  float *sq = sv + CH * HD;      // [GQ][HD] rotated queries
+  float *sf = sq + GQ * HD;      // [HD] fresh key, rotated
+  float *ss = sf + HD;           // [GQ][CH] scores -> numerators
+  float *sm = ss + GQ * CH;      // [GQ]
+  float *sl = sm + 4;            // [GQ]
+  float4 *so = reinterpret_cast<float4 *>(sl + 4);  // [NKG][NU] partial o
   const size_t cbase = (size_t)b * p.cache_seq_stride;
   const float *qrow = p.qkv + (size_t)b * p.ld;
 
   // ---- loads that do not depend on the position
-  const int base = aldg<int32_t>(p.pos + b);
-  float4 kr[F4], vr[F4];
+  const int base = aldg_lane<int32_t>(p.pos + b);
+  const uint32_t cbytes = (uint32_t)L * (uint32_t)p.kv_dim * 4u;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(p.kc + cbase, 0, cbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(p.vc + cbase, 0, cbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(qrow), 0, (uint32_t)p.ld * 4u, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(p.rope_cur), 0, (uint32_t)p.rot * 4u, 0x00020000);
+  const int slot = c * CH + key;
+  float4 kr[NF], vr[NF];
 #pragma unroll
-  for (int j = 0; j < F4; ++j) {
-    kr[j] = float4{0.f, 0.f, 0.f, 0.f};
-    vr[j] = float4{0.f, 0.f, 0.f, 0.f};
-    const int f = tid + 256 * j;
-    const int slot = c * CH + f / H4, d4 = f % H4;
-    if (slot < L) {
-      const size_t off = cbase + (size_t)slot * p.kv_dim + h * HD + 4 * d4;
-      kr[j] = aldg<float4>(p.kc + off);
-      vr[j] = aldg<float4>(p.vc + off);
-    }
+  for (int i = 0; i < NF; ++i) {
+    const uint32_t off =
+        slot < L ? ((uint32_t)slot * (uint32_t)p.kv_dim + (uint32_t)(h * HD + 4 * (i * 32 + j))) * 4u
+                 : kOut;
+    const f32x4 kv = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+    const f32x4 vv = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    kr[i] = float4{kv.x, kv.y, kv.z, kv.w};
+    vr[i] = float4{vv.x, vv.y, vv.z, vv.w};
   }
-  constexpr int QPT = TGM * HD / 256;  // q elements per thread
-  float qx[QPT], qy[QPT];
+  auto ld1 = [&](const __amdgpu_buffer_rsrc_t &r, bool on, int idx) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, on ? (uint32_t)idx * 4u : kOut, 0, 0));
+  };
+  // q element e = tid + NT u: head e / HD, dim e % HD; its RoPE partner and
+  // factors
+  float qx[QPT], qy[QPT], qc[QPT], qs[QPT];
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
-    const int e = tid + 256 * u;
-    qx[u] = qy[u] = 0.f;
-    if (e < nq) {
-      const int g = e / HD, d = e % HD;
-      const float *qh = qrow + (h * G + g) * HD;
-      qx[u] = aldg<float>(qh + d);
-      qy[u] = aldg<float>(qh + rope_partner(p, d));
-    }
+    const int e = tid + NT * u;
+    const int g = e / HD, d = e % HD;
+    const int q0 = (h * G + g0 + g) * HD;
+    const bool on = e < nq;
+    qx[u] = ld1(rq, on, q0 + d);
+    qy[u] = ld1(rq, on, q0 + rope_partner(p, d));
+    const bool rot = p.apply_rope && d < p.rot;
+    const int ri = d < p.half ? d : d - p.half;
+    const float cv = ld1(rr, rot, ri);
+    qs[u] = ld1(rr, rot, p.half + ri);
+    qc[u] = rot ? cv : 1.f;
   }
-  float kx[DPT], ky[DPT], vx[DPT];
-#pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int d = tid + 256 * j;
-    kx[j] = ky[j] = vx[j] = 0.f;
-    if (d < HD) {
-      const float *kh = qrow + p.q_dim + h * HD;
-      kx[j] = aldg<float>(kh + d);
-      ky[j] = aldg<float>(kh + rope_partner(p, d));
-      vx[j] = aldg<float>(qrow + p.q_dim + p.kv_dim + h * HD + d);
-    }
-  }
+  // fresh k, v: dim tid (threads below HD)
+  const int df = tid < HD ? tid : 0;
+  const int k0 = p.q_dim + h * HD;
+  const float kx = ld1(rq, tid < HD, k0 + df);
+  const float ky = ld1(rq, tid < HD, k0 + rope_partner(p, df));
+  const float vx = ld1(rq, tid < HD, p.q_dim + p.kv_dim + h * HD + df);
+  const bool krot = p.apply_rope && df < p.rot;
+  const int kri = df < p.half ? df : df - p.half;
+  const float kcv = ld1(rr, krot, kri);
+  const float ks_ = ld1(rr, krot, p.half + kri);
+  const float kc_ = krot ? kcv : 1.f;
+  // every load above goes out here, before the position arrives (the
+  // compiler would otherwise sink the fresh row's loads past the position
+  // test into the block that uses them, one memory round trip later)
+  asm volatile("" ::: "memory");
 
   // ---- the position: attended slots [0, nslots), the slot of this row
   int lo, hi;
@@ -1484,96 +1527,74 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs args) {
   if (c >= n_active) return;
   const int fslot = p.circular ? base % L : base;
   const bool fresh_here = fslot < nslots && fslot / CH == c;
-  float qc[QPT], qs[QPT];
+  const int kf = fslot - c * CH;  // key of the fresh row in this chunk
+  const bool own_fresh = fresh_here && key == kf;
+  if (slot >= nslots) {
 #pragma unroll
-  for (int u = 0; u < QPT; ++u) {
-    const int e = tid + 256 * u;
-    qc[u] = 1.f;
-    qs[u] = 0.f;
-    if (e < nq) rope_cs(p, e % HD, base, qc[u], qs[u]);
-  }
-  float kc_[DPT], ks_[DPT];
-#pragma unroll
-  for (int j = 0; j < DPT; ++j) {
-    const int d = tid + 256 * j;
-    kc_[j] = 1.f;
-    ks_[j] = 0.f;
-    if (fresh_here && d < HD) rope_cs(p, d, base, kc_[j], ks_[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < F4; ++j) {
-    const int f = tid + 256 * j;
-    const int slot = c * CH + f / H4;
-    if (slot >= nslots) {
-      kr[j] = float4{0.f, 0.f, 0.f, 0.f};
-      vr[j] = float4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NF; ++i) {
+      kr[i] = float4{0.f, 0.f, 0.f, 0.f};
+      vr[i] = float4{0.f, 0.f, 0.f, 0.f};
     }
-    if (!(fresh_here && slot == fslot)) {
-      const int kl = f / H4;  // key of the chunk
-      *reinterpret_cast<float4 *>(sk + kl * KP + 4 * (f % H4)) = kr[j];
-      reinterpret_cast<float4 *>(sv)[f] = vr[j];
-    }
+  }
+  if (!own_fresh) {
+#pragma unroll
+    for (int i = 0; i < NF; ++i)
+      *reinterpret_cast<float4 *>(sv + key * HD + 4 * (i * 32 + j)) = vr[i];
   }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
-    const int e = tid + 256 * u;
-    sq[e] = e < nq ? rope_mix(p, e % HD, qx[u], qy[u], qc[u], qs[u]) : 0.f;
+    const int e = tid + NT * u;
+    if (e < GQ * HD) sq[e] = e < nq ? rope_mix(p, e % HD, qx[u], qy[u], qc[u], qs[u]) : 0.f;
   }
-  if (fresh_here) {
+  if (fresh_here && tid < HD) {
     // write_kv_sliding / write_kv_full (gemma4_e4b.mojo:211-249)
-    const int kf = fslot - c * CH;
-    const size_t off = cbase + (size_t)fslot * p.kv_dim + h * HD;
-#pragma unroll
-    for (int j = 0; j < DPT; ++j) {
-      const int d = tid + 256 * j;
-      if (d < HD) {
-        const float kv = rope_mix(p, d, kx[j], ky[j], kc_[j], ks_[j]);
-        sk[kf * KP + d] = kv;
-        sv[kf * HD + d] = vx[j];
-        if (p.write_cache) {
-          p.kc[off + d] = kv;
-          p.vc[off + d] = vx[j];
-        }
-      }
+    const float kv = rope_mix(p, tid, kx, ky, kc_, ks_);
+    sf[tid] = kv;
+    sv[kf * HD + tid] = vx;
+    if (p.write_cache && s == 0) {
+      const size_t off = cbase + (size_t)fslot * p.kv_dim + h * HD + tid;
+      p.kc[off] = kv;
+      p.vc[off] = vx;
     }
   }
   __syncthreads();
 
-  // ---- scores: thread (key kk, dim group dg of LPK lanes), sums by DPP
-  const int kk = tid / LPK, dg = tid % LPK;
-  float acc[TGM];
+  // ---- scores: the thread's dims of its key against the G queries, summed
+  // over the key's 32 lanes
+  if (own_fresh) {
 #pragma unroll
-  for (int t = 0; t < TGM; ++t) acc[t] = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int d = dg * 4 + 4 * LPK * i;
-    const float4 kv = *reinterpret_cast<const float4 *>(sk + kk * KP + d);
-#pragma unroll
-    for (int t = 0; t < TGM; ++t) {
-      const float4 qq = *reinterpret_cast<const float4 *>(sq + t * HD + d);
-      acc[t] += qq.x * kv.x + qq.y * kv.y + qq.z * kv.z + qq.w * kv.w;
-    }
+    for (int i = 0; i < NF; ++i) kr[i] = *reinterpret_cast<const float4 *>(sf + 4 * (i * 32 + j));
   }
+  float acc[GQ];
 #pragma unroll
-  for (int t = 0; t < TGM; ++t) acc[t] = LPK == 8 ? row8_sum(acc[t]) : row16_sum(acc[t]);
-  if (dg == 0) {
-    const bool ok = c * CH + kk < nslots;
+  for (int t = 0; t < GQ; ++t) {
+    acc[t] = 0.f;
 #pragma unroll
-    for (int t = 0; t < TGM; ++t)
-      if (t < G) ss[t * CH + kk] = ok ? acc[t] * p.scale : -INFINITY;
+    for (int i = 0; i < NF; ++i) {
+      const float4 qq = *reinterpret_cast<const float4 *>(sq + t * HD + 4 * (i * 32 + j));
+      acc[t] += qq.x * kr[i].x + qq.y * kr[i].y + qq.z * kr[i].z + qq.w * kr[i].w;
+    }
+    acc[t] = row16_sum(acc[t]);
+    acc[t] += __shfl_xor(acc[t], 16, 64);
+  }
+  if (j == 0) {
+    const bool ok = slot < nslots;
+#pragma unroll
+    for (int t = 0; t < GQ; ++t)
+      if (t < Gl) ss[t * CH + key] = ok ? acc[t] * p.scale : -INFINITY;
   }
   __syncthreads();
   // numerators of the chunk: query head t on CH lanes, lane = key; max and
   // sum over the chunk's keys (a row of 16 by DPP, two rows by one exchange)
-  if (tid < CH * TGM) {
+  if (tid < CH * GQ) {
     const int t = tid / CH, k = tid % CH;
-    const float sc = t < G ? ss[t * CH + k] : -INFINITY;
+    const float sc = t < Gl ? ss[t * CH + k] : -INFINITY;
     float m = row16_max(sc);
-    if (CH == 32) m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
     const float pr = (sc == -INFINITY) ? 0.f : expf(sc - m);
     float l = row16_sum(pr);
-    if (CH == 32) l += __shfl_xor(l, 16, 64);
-    if (t < G) {
+    l += __shfl_xor(l, 16, 64);
+    if (t < Gl) {
       ss[t * CH + k] = pr;
       if (k == 0) {
         sm[t] = m;
@@ -1583,30 +1604,43 @@ __global__ __launch_bounds__(256) void k_attn_part(AttnArgs args) {
   }
   __syncthreads();
 
-  // ---- P.V on float4 units (head t, dims 4u..4u+3), stored per query head
+  // ---- P.V: unit u = (head t, dims 4d4..4d4+3) over key group kq
+  const int u = tid % NU, kq = tid / NU;
+  const int t = u / H4, d4 = u % H4;
+  {
+    const float4 *sv4 = reinterpret_cast<const float4 *>(sv);
+    float4 o = float4{0.f, 0.f, 0.f, 0.f};
+    if (t < Gl) {
+#pragma unroll
+      for (int k = kq * KPG; k < kq * KPG + KPG; ++k) {
+        const float pk = ss[t * CH + k];
+        const float4 v = sv4[k * H4 + d4];
+        o.x += pk * v.x;
+        o.y += pk * v.y;
+        o.z += pk * v.z;
+        o.w += pk * v.w;
+      }
+    }
+    so[kq * NU + u] = o;
+  }
+  __syncthreads();
   const int nhq = p.n_heads;
   float *po = p.part + (size_t)b * kDecPartMaxChunks * nhq * (HD + 2);
   float *pml = po + (size_t)kDecPartMaxChunks * nhq * HD;
-  const float4 *sv4 = reinterpret_cast<const float4 *>(sv);
+  if (tid < NU && t < Gl) {
+    float4 o = so[u];
 #pragma unroll
-  for (int j = 0; j < UPT; ++j) {
-    const int u = tid + 256 * j;
-    if (u >= G * H4) break;
-    const int t = u / H4, d4 = u % H4;
-    float4 o = float4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int k = 0; k < CH; ++k) {
-      const float pk = ss[t * CH + k];
-      const float4 v = sv4[k * H4 + d4];
-      o.x += pk * v.x;
-      o.y += pk * v.y;
-      o.z += pk * v.z;
-      o.w += pk * v.w;
+    for (int g = 1; g < NKG; ++g) {
+      const float4 w = so[g * NU + u];
+      o.x += w.x;
+      o.y += w.y;
+      o.z += w.z;
+      o.w += w.w;
     }
-    *reinterpret_cast<float4 *>(po + ((size_t)c * nhq + h * G + t) * HD + 4 * d4) = o;
+    *reinterpret_cast<float4 *>(po + ((size_t)c * nhq + h * G + g0 + t) * HD + 4 * d4) = o;
   }
-  if (tid < G)
-    *reinterpret_cast<float2 *>(pml + ((size_t)c * nhq + h * G + tid) * 2) =
+  if (tid < Gl)
+    *reinterpret_cast<float2 *>(pml + ((size_t)c * nhq + h * G + g0 + tid) * 2) =
         float2{sm[tid], sl[tid]};
 }
 
@@ -1617,24 +1651,47 @@ int dec_part_chunks(const AttnArgs &a) {
 
 bool dec_part_ok(const AttnArgs &a) {
   const int G = a.n_kv > 0 ? a.n_heads / a.n_kv : 0;
-  return a.T == 1 && G >= 1 && G <= 4 && a.n_heads % a.n_kv == 0 &&
-         (a.hd == 128 || a.hd == 256 || a.hd == 512) && a.rot % 2 == 0 && a.rot <= a.hd &&
+  return a.T == 1 && G >= 1 && G <= 4 && G != 3 && a.n_heads % a.n_kv == 0 &&
+         (a.hd == 256 || a.hd == 512) && a.rot % 2 == 0 && a.rot <= a.hd &&
          a.ld >= a.q_dim + 2 * a.kv_dim && dec_part_chunks(a) <= kDecPartMaxChunks;
+}
+
+// cos, sin rows of the tables at the position of sequence 0 (rope_table_host's
+// angles, kernels.mojo:563-577), copied to a.rope_cur
+__global__ __launch_bounds__(256) void k_rope_cur(AttnArgs args) {
+  const int half = args.rot >> 1;
+  const int pos = aldg<int32_t>(args.pos);
+  float *o = const_cast<float *>(args.rope_cur);
+  for (int i = threadIdx.x; i < half; i += 256) {
+    o[i] = aldg<float>(args.cos_t + (size_t)pos * half + i);
+    o[half + i] = aldg<float>(args.sin_t + (size_t)pos * half + i);
+  }
+}
+
+int launch_rope_cur(const AttnArgs &a, hipStream_t st) {
+  MS_CHECK_ARG(a.rope_cur && a.pos && a.cos_t && a.sin_t && a.rot >= 0,
+               "rope factors: missing buffers");
+  hipLaunchKernelGGL(k_rope_cur, dim3(1), dim3(256), 0, st, a);
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
 }
 
 int launch_attention_partials(const AttnArgs &a, hipStream_t st) {
   MS_CHECK_ARG(dec_part_ok(a), "attention partials: unsupported shape");
-  MS_CHECK_ARG(a.qkv && a.part && a.pos && a.kc && a.vc, "attention partials: missing buffers");
+  MS_CHECK_ARG(a.qkv && a.part && a.pos && a.kc && a.vc && a.rope_cur,
+               "attention partials: missing buffers");
   AttnArgs a2 = a;
   a2.grid_chunks = dec_part_chunks(a);
-  const dim3 grid(a2.grid_chunks, a.B * a.n_kv);
+  // two query heads per block: the G heads of a kv head over G / 2 blocks
+  constexpr int GQ = 2;
+  const int G = a.n_heads / a.n_kv;
+  const int ns = G > GQ ? G / GQ : 1;
+  const dim3 grid(a2.grid_chunks, a.B * a.n_kv * ns);
   constexpr int CH = kDecPartChunk;
-  const size_t shmem = (size_t)(CH * (2 * a.hd + 32) + 4 * a.hd + 4 * CH + 8) * 4;
-  switch (a.hd) {
-    case 128: hipLaunchKernelGGL((k_attn_part<128, CH>), grid, dim3(256), shmem, st, a2); break;
-    case 256: hipLaunchKernelGGL((k_attn_part<256, CH>), grid, dim3(256), shmem, st, a2); break;
-    default: hipLaunchKernelGGL((k_attn_part<512, CH>), grid, dim3(256), shmem, st, a2); break;
-  }
+  // sv, sq, sf, ss, sm / sl (4 + 4 floats), so (16 KB at every head dim)
+  const size_t shmem = (size_t)(CH * a.hd + GQ * a.hd + a.hd + GQ * CH + 8) * 4 + 16384;
+  if (a.hd == 256) hipLaunchKernelGGL((k_attn_part<256, GQ>), grid, dim3(1024), shmem, st, a2);
+  else hipLaunchKernelGGL((k_attn_part<512, GQ>), grid, dim3(1024), shmem, st, a2);
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }

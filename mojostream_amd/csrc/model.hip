@@ -113,6 +113,7 @@ struct ms_model {
   void *quant = nullptr;
   int quant_k = 0;
   float *qkv = nullptr, *attn_part = nullptr;
+  float *rope_cur = nullptr;  // one-row decode: RoPE factors at the position [2][256]
   unsigned *attn_ctr = nullptr;  // decode chunk counters [seq][kv head], kept zero
   // prefill: rows per chunk (0: no prefill workspace), attention rows per
   // launch inside a chunk and their base positions on the device
@@ -336,6 +337,40 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
   const int D = m->d.hidden, F = m->d.ffn;
   const int ld = d.q_dim + 2 * d.kv_dim;
 
+  AttnArgs attn{};
+  attn.B = rc.B;
+  attn.T = rc.T;
+  attn.q_dim = d.q_dim;
+  attn.kv_dim = d.kv_dim;
+  attn.hd = d.head_dim;
+  attn.n_heads = d.n_heads;
+  attn.n_kv = d.n_kv_heads;
+  attn.rot = d.rot_dim;
+  attn.cache_kind = d.cache_kind;
+  attn.cache_len = d.cache_len;
+  attn.clamp = d.clamp_reads;
+  attn.scale = 1.0f / sqrtf((float)d.head_dim);
+  attn.qkv = m->qkv;
+  attn.ld = ld;
+  attn.apply_rope = 1;
+  attn.cos_t = m->ropes[Ly.rope].cs;
+  attn.sin_t = m->ropes[Ly.rope].sn;
+  attn.pos = m->pos + rc.seq0;
+  attn.kc = Ly.kc + (size_t)rc.seq0 * Ly.cache_seq_stride;
+  attn.vc = Ly.vc + (size_t)rc.seq0 * Ly.cache_seq_stride;
+  attn.cache_seq_stride = Ly.cache_seq_stride;
+  attn.n_chunks = Ly.n_chunks;
+  attn.part = m->attn_part;
+  attn.ctr = m->attn_ctr;
+  attn.out = m->aO;
+  attn.write_cache = 1;
+  attn.plan_pos = rc.plan_pos;
+  attn.pos_bound = rc.pos_bound;
+  attn.rope_cur = m->rope_cur;
+  // one decode row: chunk partials (k_attn_part), merged in the O projection
+  const bool use_part = rc.one_row && rc.B == 1 && rc.T == 1 && d.n_heads == 8 &&
+                        d.q_dim == 8 * d.head_dim && dec_part_ok(attn);
+
   // 1. x = rmsnorm(ple * x) in the prologue, fused Q|K|V projection
   //    (gemma4_e4b.mojo:473-487)
   {
@@ -357,44 +392,34 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
     a.out = m->qkv;
     a.ldo = ld;
     ProfScope ps(PC_QKV, (double)D * ld / 2, st);
-    if (int rc2 = launch_proj_row(m, rc, a, r, 8, 4, st)) return rc2;
+    GemvArgs w = a;
+    w.asrc = AS_WAVES;
+    w.rows = r;
+    w.waves = 4;
+    const int tpw = D % (4 * kSuperK) == 0 ? D / (4 * kSuperK) : 0;
+    if (use_part && (tpw == 2 || tpw == 5) && wave_shape_ok(w) &&
+        gemv_lds_need(w) <= kLdsLimit) {
+      // one launch also prepares the attention's RoPE factors
+      w.pf.pos = attn.pos;
+      w.pf.cos_t = attn.cos_t;
+      w.pf.sin_t = attn.sin_t;
+      w.pf.half = d.rot_dim / 2;
+      w.pf.rope_rows = m->d.max_pos;
+      w.pf.rope_cur = m->rope_cur;
+      if (int rc2 = launch_gemv_rec(w, st)) return rc2;
+    } else {
+      if (int rc2 = launch_proj_row(m, rc, a, r, 8, 4, st)) return rc2;
+      if (use_part)
+        if (int rc2 = launch_rope_cur(attn, st)) return rc2;
+    }
   }
   // 2. attention (chunks + merge/cache append)
   bool merged_in_o = false;
   {
-    AttnArgs a{};
-    a.B = rc.B;
-    a.T = rc.T;
-    a.q_dim = d.q_dim;
-    a.kv_dim = d.kv_dim;
-    a.hd = d.head_dim;
-    a.n_heads = d.n_heads;
-    a.n_kv = d.n_kv_heads;
-    a.rot = d.rot_dim;
-    a.cache_kind = d.cache_kind;
-    a.cache_len = d.cache_len;
-    a.clamp = d.clamp_reads;
-    a.scale = 1.0f / sqrtf((float)d.head_dim);
-    a.qkv = m->qkv;
-    a.ld = ld;
-    a.apply_rope = 1;
-    a.cos_t = m->ropes[Ly.rope].cs;
-    a.sin_t = m->ropes[Ly.rope].sn;
-    a.pos = m->pos + rc.seq0;
-    a.kc = Ly.kc + (size_t)rc.seq0 * Ly.cache_seq_stride;
-    a.vc = Ly.vc + (size_t)rc.seq0 * Ly.cache_seq_stride;
-    a.cache_seq_stride = Ly.cache_seq_stride;
-    a.n_chunks = Ly.n_chunks;
-    a.part = m->attn_part;
-    a.ctr = m->attn_ctr;
-    a.out = m->aO;
-    a.write_cache = 1;
-    a.plan_pos = rc.plan_pos;
-    a.pos_bound = rc.pos_bound;
+    AttnArgs a = attn;
     // KV bytes read at the current position are counted by bench.py
     ProfScope ps(PC_ATTN, 0.0, st);
-    if (rc.one_row && rc.B == 1 && rc.T == 1 && d.n_heads == 8 &&
-        d.q_dim == 8 * d.head_dim && dec_part_ok(a)) {
+    if (use_part) {
       // chunk partials only; the O projection below merges them
       if (g_prof.on) {
         const int k = d.cache_kind == MS_CACHE_CIRCULAR ? 1 : 0;
@@ -852,6 +877,7 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   }
   if ((rc = dmalloc(m, (void **)&m->qkv, (size_t)M * m->qkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
+      (rc = dmalloc(m, (void **)&m->rope_cur, 512 * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_ctr, (size_t)d.max_seqs * m->nkv_max * 4)) ||
 
       (rc = dmalloc(m, (void **)&m->pos, 64 * 4)) ||
@@ -1548,6 +1574,13 @@ static int attn_sweep(ms_model *m, int passes, double *avg_us, double *bytes_per
   double bytes = 0;
   long n = 0;
   int rc = MS_OK;
+  if (g_prof.attn_part[k]) {
+    // the RoPE factors of the swept layers (one table for the kind)
+    AttnArgs a = base;
+    a.cos_t = m->ropes[Lr.rope].cs;
+    a.sin_t = m->ropes[Lr.rope].sn;
+    if ((rc = launch_rope_cur(a, st))) return rc;
+  }
   MS_HIP_TRY(hipEventRecord(e0, st));
   for (int p = 0; p < passes && rc == MS_OK; ++p)
     for (int l : layers) {

@@ -50,6 +50,17 @@ struct AttnSrc {
   int chunks;           // chunks the attention launch covered
 };
 
+// What the one-row Q|K|V projection prepares for the decode attention
+// (k_attn_part) of the same layer: block 0 writes the RoPE factors of the
+// row's position to rope_cur, so that the attention loads them at entry
+// instead of after the position.  rope_cur == null: nothing.
+struct AttnPrep {
+  const int32_t *pos;          // position of the row
+  const float *cos_t, *sin_t;  // [rope_rows][half]
+  int half, rope_rows;
+  float *rope_cur;             // [2][half]: cos, sin at the position
+};
+
 // fp32 rows and the transform applied before quantization:
 // y = x * pre_scale; if norm: y *= 1/sqrt(mean(y^2) + 1e-6); if gamma: y *= gamma.
 struct RowSrc {
@@ -79,6 +90,7 @@ struct GemvArgs {
   RowSrc rows;    // AS_ROWS, AS_WAVES (no gamma, no x_out)
   QuantRows q;    // AS_QUANT
   AttnSrc at;     // AS_ATTN
+  AttnPrep pf;    // AS_WAVES, one row, store epilogue: the decode attention's inputs
   GemvSeg seg[3];
   int nseg;
   int P;          // panels per block (EPI_SWIGLU: 2, gate and up)

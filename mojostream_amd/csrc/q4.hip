@@ -729,9 +729,11 @@ __device__ inline void attn_merge_quant(const AttnSrc &at_, int8_t *limbs, int l
 }
 
 // AS_WAVES instantiations carry the row bound and the super-tiles per wave in
-// the RP template slot: RP = 10 * rows + tiles.
-__host__ __device__ constexpr int waves_rows(int rp) { return rp / 10; }
+// the RP template slot: RP = 10 * rows + tiles (+ 100 with AttnPrep).
+__host__ __device__ constexpr int waves_rows(int rp) { return (rp / 10) % 10; }
 __host__ __device__ constexpr int waves_tpw(int rp) { return rp % 10; }
+// + 100: one row, store epilogue, preparing the decode attention (AttnPrep)
+__host__ __device__ constexpr bool waves_pf(int rp) { return rp >= 100; }
 // 64-lane slots of 8-value groups that hold a wave's slice of one row
 __host__ __device__ constexpr int waves_nsl(int rp) { return (waves_tpw(rp) * 16 + 63) / 64; }
 
@@ -882,6 +884,24 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   const int ldo_sw = (EPI == EPI_SWIGLU) ? launder(a.ldo_sw) : 0;
   float *arg_val = (EPI == EPI_ARGMAX) ? launder(a.arg_val) : nullptr;
   int32_t *arg_idx = (EPI == EPI_ARGMAX) ? launder(a.arg_idx) : nullptr;
+  // the decode attention's RoPE factors (one-row Q|K|V projection)
+  constexpr bool PF = AS == AS_WAVES && waves_pf(RP);
+  static_assert(!PF || (EPI == EPI_STORE && P == 1 && MR == 1), "AttnPrep: one row, store");
+  AttnPrep pf{};
+  int pf_base = 0;
+  if constexpr (PF) {
+    pf.cos_t = launder(a.pf.cos_t);
+    pf.sin_t = launder(a.pf.sin_t);
+    pf.half = launder(a.pf.half);
+    pf.rope_rows = launder(a.pf.rope_rows);
+    pf.rope_cur = launder(a.pf.rope_cur);
+    // first load of the kernel: it has arrived when the weights have gone
+    // out.  Loaded per lane (an opaque zero offset), so that no wait for it
+    // is placed here to move it into a scalar register.
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    pf_base = ldg<int32_t>(launder(a.pf.pos) + z);
+  }
   RowSrc rs{};
   QuantRows qr{};
   if (AS == AS_ROWS || AS == AS_WAVES) {
@@ -937,6 +957,7 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   for (int c = 0; c < C; ++c) a_on[c] = 16 * c + i < 4 * M;
 
   uint4 q[U][P];
+  float pf_cs[2];  // PF: cos, sin at the position (block 0)
   v4i af[AS == AS_QUANT ? U : 1][C][2];
   float yv[MR][NSL][8];  // AS_WAVES: the wave's y values (for the normalized rows)
   // Loads of super-tiles u0..u1-1 of batch bt; tiles past the end of K are
@@ -1031,6 +1052,22 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
     wave_rows_quant<U, MR, W>(rs, M, limbs, ldl, row_s, sh, yv, wave, lane,
                               [&] { issue_part(0, 0, kEarlyW); });
     if constexpr (kEarlyW < U) issue_part(0, kEarlyW, U);
+    if constexpr (PF) {
+      __builtin_amdgcn_sched_barrier(0);
+      // block 0: the RoPE factors at the position (range-checked loads: the
+      // other threads and blocks read nothing)
+      const uint32_t tb = (uint32_t)pf.rope_rows * (uint32_t)pf.half * 4u;
+      const __amdgpu_buffer_rsrc_t rc_ =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(pf.cos_t), 0, tb, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rs_ =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(pf.sin_t), 0, tb, 0x00020000);
+      const bool rl = blockIdx.x == 0 && (int)threadIdx.x < pf.half;
+      const uint32_t ro = rl ? ((uint32_t)pf_base * (uint32_t)pf.half + threadIdx.x) * 4u
+                             : 0x80000000u;
+      pf_cs[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rc_, ro, 0, 0));
+      pf_cs[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_, ro, 0, 0));
+      __builtin_amdgcn_sched_barrier(0);
+    }
   } else {
     if ((int)threadIdx.x < M) row_s[threadIdx.x] = ldg<int32_t>(qr.shift + threadIdx.x);
     issue(0);
@@ -1191,6 +1228,12 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
             }
           }
         }
+      }
+    }
+    if constexpr (PF) {
+      if (blockIdx.x == 0 && (int)threadIdx.x < pf.half) {
+        pf.rope_cur[threadIdx.x] = pf_cs[0];
+        pf.rope_cur[pf.half + threadIdx.x] = pf_cs[1];
       }
     }
     return;
@@ -1424,6 +1467,16 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     // RP = 10 * row bound + super-tiles per wave; one row has instantiations
     // of its own (fewer registers)
     const int tpw = a.K / (a.waves * kSuperK);
+    if (a.pf.rope_cur) {
+      // one row preparing the decode attention's RoPE factors (Q|K|V)
+      MS_CHECK_ARG(a.M == 1 && a.epi == EPI_STORE && a.P == 1 && a.waves == 4 &&
+                       (tpw == 5 || tpw == 2) && a.pf.pos && a.pf.cos_t && a.pf.sin_t &&
+                       a.pf.half >= 0 && a.pf.half <= 256 && a.pf.rope_rows >= 1,
+                   "GEMV: attention preparation: one row, store, 4 waves, K = 1024 or 2560");
+      if (tpw == 5) MS_GEMV_L(1, EPI_STORE, 1, AS_WAVES, 4, 115);
+      else MS_GEMV_L(1, EPI_STORE, 1, AS_WAVES, 4, 112);
+      ok = true;
+    }
 #define MS_GEMV_W(EP, PP, WW, T)                                       \
   if (!ok && a.epi == EP && a.waves == WW && tpw == T) {               \
     if (a.M == 1) MS_GEMV_L(1, EP, PP, AS_WAVES, WW, 10 + T);          \

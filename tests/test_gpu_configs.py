@@ -166,6 +166,23 @@ def test_c3_plain_batch1_teacher_forced(gpu, oracle16):
           "does not depend on its input)")
 
 
+def test_c3_balanced_batch1_teacher_forced(gpu, oracle16):
+    """Batch 1 on the balanced weights, whose output depends on every
+    attention row: the one-row decode path (chunk partials merged in the O
+    projection, K/V rows and RoPE factors prepared by the Q|K|V projection)
+    at positions 128..191, hidden rows at 128, 160 and 191."""
+    ms = gpu
+    say("C3 E4B balanced weights, batch 1: 128-token prompt + 64 steps, taps on")
+    steps, keep = 64, (0, 32, 63)
+    max_pos = PROMPT + STEPS + 8
+    prompt = prompt_ids(PROMPT, 262144, 1)
+    pre, ids, logits, hid = gpu_decode(ms, True, [prompt], steps, keep, max_pos, penalty=1.2)
+    hw = HostWeights(ms.arch_e4b(max_full_seq=max_pos), SEED, balanced=True)
+    seq = check_sequence(hw.model(oracle16), prompt, pre[0], ids, logits, hid, 0, keep,
+                         "balanced b1", penalty=1.2)
+    assert len(set(seq)) > 8, "the balanced model's greedy ids should vary"
+
+
 @pytest.fixture(scope="module")
 def c3_balanced_batch4(gpu):
     ms = gpu
