@@ -31,6 +31,8 @@
 // second half the up panels of the same columns; the gate values pass through
 // LDS and the up waves write up * gate * sigmoid(gate) (swiglu_inplace,
 // kernels.mojo:519-532).
+#include <algorithm>
+
 #include "devutil.h"
 #include "q4.h"
 
@@ -209,27 +211,51 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
     rz[a] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
   }
 
-  // Ring of kStages K steps: step G + 2 is issued into the stage step G - 1
+  // K steps of this block: all of them, or part blockIdx.z of ksplit
+  const int ks = launder(g.ksplit) > 1 ? launder(g.ksplit) : 1;
+  const int G0 = (int)((long)KG * blockIdx.z / ks), NG = (int)((long)KG * (blockIdx.z + 1) / ks) - G0;
+
+  // Ring of kStages K steps: step i + 2 is issued into the stage step i - 1
   // used, once every wave has passed the barrier after computing it.  The
-  // barrier is a bare s_barrier: this wave's own loads of step G are waited
-  // for explicitly, and those of step G + 1 stay in flight (a __syncthreads
+  // barrier is a bare s_barrier: this wave's own loads of step i are waited
+  // for explicitly, and those of step i + 1 stay in flight (a __syncthreads
   // would wait for them too).
-  issue(0, 0);
-  if (KG > 1) issue(1, 1);
-  for (int G = 0; G < KG; ++G) {
-    if (G + 1 < KG)
+  issue(G0, 0);
+  if (NG > 1) issue(G0 + 1, 1);
+  for (int i = 0; i < NG; ++i) {
+    if (i + 1 < NG)
       __builtin_amdgcn_s_waitcnt(0x0F70 | kLoads);  // vmcnt(6)
     else
       __builtin_amdgcn_s_waitcnt(0x0F70);           // vmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (G + 2 < KG) issue(G + 2, (G + 2) % kStages);
-    compute(G % kStages);
+    if (i + 2 < NG) issue(G0 + i + 2, (i + 2) % kStages);
+    compute(i % kStages);
   }
 
   // ---- epilogue: lane (column jc, row rr of each A tile)
   const int jc = lane & 15, rr = lane >> 4;
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ACCUMULATE) {
+    if (ks > 1) {
+      // this part's exact sums d0 + 2^8 d1 + 2^16 d2 + 2^24 d3 (k_gemm_kcombine)
+      int64_t *kp = launder(g.kpart) + (size_t)blockIdx.z * M * ldo;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int row = r0 + 4 * (4 * wa + a) + rr;
+        if (row >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (!pv[j]) continue;
+          const v4i d = acc[a][j];
+          kp[(size_t)row * ldo + col[j] + jc] =
+              (int64_t)d[0] + ((int64_t)d[1] << 8) + ((int64_t)d[2] << 16) +
+              ((int64_t)d[3] << 24);
+        }
+      }
+      return;
+    }
+  }
   float v[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
@@ -578,6 +604,40 @@ void launch_big(const GemmArgs &g, int np, hipStream_t st) {
 
 }  // namespace
 
+// The K parts of a split GEMM added and scaled: row `blockIdx.y`, 256
+// columns per block.  The int64 sum is the exact integer the unsplit kernel
+// forms with limb_combine, so every output equals the unsplit one.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_kcombine(GemmArgs g) {
+  const int M = g.M, N = g.ldo, ks = g.ksplit;
+  const int row = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= N) return;
+  long long t = 0;
+  for (int z = 0; z < ks; ++z) t += ldg<long long>(g.kpart + ((size_t)z * M + row) * N + c);
+  const double z8 = (double)(8 * ldg<long long>(g.a.xsum + row));
+  const float sc = ldexpf(1.0f, -ldg<int32_t>(g.a.shift + row));
+  const float v = (float)(((double)t - z8) * (double)sc * (double)g.seg[0].scale);
+  float *o = g.out + (size_t)row * N + c;
+  if constexpr (EPI == EPI_STORE) *o = v;
+  else *o += v;
+}
+
+int gemm_ksplit(int M, int K, int N) {
+  if (M <= kGemvMaxM || K % 128 != 0 || N % 16 != 0) return 1;
+  GemmArgs g{};
+  g.epi = EPI_STORE;
+  g.M = M;
+  g.K = K;
+  g.nseg = 1;
+  const int np = N / 16;
+  if (gemm_pick(g, np) != 0) return 1;
+  const long blocks = (long)((np + 4 * kWB - 1) / (4 * kWB)) * ((M + kBM - 1) / kBM);
+  const long cus = ctx().n_cu > 0 ? ctx().n_cu : 256;
+  long ks = cus / blocks;
+  ks = std::min<long>(ks, std::min(8, K / 128 / 8));  // at least 8 K steps a part
+  return ks > 1 ? (int)ks : 1;
+}
+
 int launch_gemm(const GemmArgs &g, hipStream_t st) {
   MS_CHECK_ARG(g.M >= 1 && g.K >= 128 && g.K % 128 == 0 && g.K <= kQuantMaxK,
                "GEMM: K must be a multiple of 128 in [128, 16384]");
@@ -598,6 +658,22 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
   int np = 0;
   for (int i = 0; i < g.nseg; ++i) np += g.seg[i].n_cols / 16;
   const bool swiglu = g.epi == EPI_SWIGLU;
+  if (g.ksplit > 1) {
+    MS_CHECK_ARG((g.epi == EPI_STORE || g.epi == EPI_ACCUMULATE) && g.nseg == 1 && g.kpart &&
+                     g.ldo == g.seg[0].n_cols && g.ksplit <= g.K / 128,
+                 "GEMM: K split needs one segment, store or accumulate, ldo = N");
+    const dim3 grid((np + 4 * kWB - 1) / (4 * kWB), (g.M + kBM - 1) / kBM, g.ksplit);
+    const dim3 cgrid((g.ldo + 255) / 256, g.M);
+    if (g.epi == EPI_STORE) {
+      hipLaunchKernelGGL(k_gemm<EPI_STORE>, grid, dim3(kNT), kGemmLds, st, g);
+      hipLaunchKernelGGL(k_gemm_kcombine<EPI_STORE>, cgrid, dim3(256), 0, st, g);
+    } else {
+      hipLaunchKernelGGL(k_gemm<EPI_ACCUMULATE>, grid, dim3(kNT), kGemmLds, st, g);
+      hipLaunchKernelGGL(k_gemm_kcombine<EPI_ACCUMULATE>, cgrid, dim3(256), 0, st, g);
+    }
+    MS_HIP_TRY(hipGetLastError());
+    return MS_OK;
+  }
   const int pick = gemm_pick(g, np);
   if (pick == kGPan) {
     launch_big<kGPan>(g, np, st);

@@ -134,6 +134,11 @@ struct GemmArgs {
   float *out2;         // EPI_RESID: optional copy
   float *sw_out;       // EPI_SWIGLU: [M][ldo_sw]
   int ldo_sw;
+  // K split over ksplit block groups (> 1: one segment, store or accumulate):
+  // each group stores its exact partial sums, int64 [ksplit][M][N], and a
+  // combine kernel adds them and scales (the same value as without the split)
+  int ksplit;
+  int64_t *kpart;
 };
 
 constexpr int kGemvMaxM = 16;
@@ -160,6 +165,9 @@ QuantRows quant_rows_view(void *buf, int M, int K);
 int pack_device(uint8_t *dst, const uint8_t *src, int K, int N, hipStream_t st);
 int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st);
 int launch_gemm(const GemmArgs &g, hipStream_t st);
+// K parts for C = A deq(W) with M rows, one segment: > 1 where the 32-row
+// GEMM would leave most CUs idle (a few row and column tiles, long K)
+int gemm_ksplit(int M, int K, int N);
 // Rows a GEMM reads from its quantized operand (M rounded up to the row tile).
 int gemm_row_pad(int M);
 

@@ -1626,23 +1626,34 @@ int q4_noalloc_init(int device) {
 }
 
 // Scratch bytes a q4 matmul of M rows of length K uses for its quantized rows.
-static size_t q4_matmul_scratch_bytes(int M, int K) {
-  return M > kGemvMaxM ? quant_rows_bytes(gemm_row_pad(M), K)
-                       : quant_rows_bytes(kGemvMaxM, K);
+// The K split's partial sums follow the quantized rows, 256-byte aligned.
+static size_t q4_matmul_rows_bytes(int M, int K) {
+  const size_t b = M > kGemvMaxM ? quant_rows_bytes(gemm_row_pad(M), K)
+                                 : quant_rows_bytes(kGemvMaxM, K);
+  return (b + 255) & ~(size_t)255;
+}
+static size_t q4_matmul_scratch_bytes(int M, int K, int N, int ks) {
+  return q4_matmul_rows_bytes(M, K) + (ks > 1 ? (size_t)ks * M * N * 8 : 0);
 }
 
-// C (+)= A . deq(W) with the quantized rows in `buf` (q4_matmul_scratch_bytes).
+// C (+)= A . deq(W) with the quantized rows (and, with ks > 1 K parts, their
+// partial sums) in `buf` (q4_matmul_scratch_bytes).
 static int q4_matmul_impl(float *d_C, const float *d_A, const uint8_t *d_packed, int M, int K,
-                          int N, float scale, int accumulate, void *buf) {
+                          int N, float scale, int accumulate, void *buf, int ks) {
   hipStream_t st = ctx().stream;
   if (M > kGemvMaxM) {
-    // many rows: quantize all of them once, then the MFMA GEMM
+    // many rows: quantize all of them once, then the MFMA GEMM (its K split
+    // over ks block groups when few tiles would leave most CUs idle)
     const int Mp = gemm_row_pad(M);
     GemmArgs g{};
     g.epi = accumulate ? EPI_ACCUMULATE : EPI_STORE;
     g.M = M;
     g.K = K;
     g.a = quant_rows_view(buf, Mp, K);
+    g.ksplit = ks;
+    if (ks > 1)
+      g.kpart = reinterpret_cast<int64_t *>(static_cast<uint8_t *>(buf) +
+                                            q4_matmul_rows_bytes(M, K));
     RowSrc r{};
     r.x = d_A;
     r.ld = K;
@@ -1716,9 +1727,10 @@ extern "C" int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packe
   using namespace ms;
   if (int rc = require_init()) return rc;
   if (int rc = q4_matmul_check(M, K, N)) return rc;
+  const int ks = gemm_ksplit(M, K, N);
   void *buf = nullptr;
-  if (int rc = ms::scratch(q4_matmul_scratch_bytes(M, K), &buf)) return rc;
-  return q4_matmul_impl(d_C, d_A, d_packed, M, K, N, scale, accumulate, buf);
+  if (int rc = ms::scratch(q4_matmul_scratch_bytes(M, K, N, ks), &buf)) return rc;
+  return q4_matmul_impl(d_C, d_A, d_packed, M, K, N, scale, accumulate, buf, ks);
 }
 
 extern "C" int ms_bench_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_w0,
@@ -1729,18 +1741,20 @@ extern "C" int ms_bench_q4_matmul(float *d_C, const float *d_A, const uint8_t *d
   if (int rc = q4_matmul_check(M, K, N)) return rc;
   MS_CHECK_ARG(d_C && d_A && d_w0 && n_w >= 1 && reps >= 1 && avg_us, "bench_q4_matmul: bad args");
   MS_CHECK_ARG(n_w == 1 || w_stride >= (size_t)K * N / 2, "bench_q4_matmul: stride < matrix bytes");
+  const int ks = gemm_ksplit(M, K, N);
   void *buf = nullptr;
-  if (int rc = ms::scratch(q4_matmul_scratch_bytes(M, K), &buf)) return rc;
+  if (int rc = ms::scratch(q4_matmul_scratch_bytes(M, K, N, ks), &buf)) return rc;
   hipStream_t st = ctx().stream;
   // one untimed call (code objects, caches of the activations)
-  if (int rc = q4_matmul_impl(d_C, d_A, d_w0, M, K, N, scale, 0, buf)) return rc;
+  if (int rc = q4_matmul_impl(d_C, d_A, d_w0, M, K, N, scale, 0, buf, ks)) return rc;
   hipEvent_t e0, e1;
   MS_HIP_TRY(hipEventCreate(&e0));
   MS_HIP_TRY(hipEventCreate(&e1));
   MS_HIP_TRY(hipEventRecord(e0, st));
   int rc = MS_OK;
   for (int r = 0; r < reps && rc == MS_OK; ++r)
-    rc = q4_matmul_impl(d_C, d_A, d_w0 + (size_t)(r % n_w) * w_stride, M, K, N, scale, 0, buf);
+    rc = q4_matmul_impl(d_C, d_A, d_w0 + (size_t)(r % n_w) * w_stride, M, K, N, scale, 0, buf,
+                        ks);
   (void)hipEventRecord(e1, st);
   (void)hipEventSynchronize(e1);
   float ms_ = 0.f;
@@ -1757,13 +1771,17 @@ extern "C" int ms_q4_matmul_noalloc(float *d_C, const float *d_A, const uint8_t 
   using namespace ms;
   if (int rc = require_init()) return rc;
   if (int rc = q4_matmul_check(M, K, N)) return rc;
-  const size_t need = q4_matmul_scratch_bytes(M, K);
+  // the K split only where its partial sums fit too (the result is the same
+  // either way)
+  int ks = gemm_ksplit(M, K, N);
+  if (q4_matmul_scratch_bytes(M, K, N, ks) > kNoAllocScratchBytes) ks = 1;
+  const size_t need = q4_matmul_scratch_bytes(M, K, N, ks);
   if (need > kNoAllocScratchBytes)
     return fail(MS_E_INVALID, "q4_matmul_noalloc: " + std::to_string(M) + " rows of " +
                                   std::to_string(K) + " need " + std::to_string(need) +
                                   " bytes of scratch, above its 4 MiB maximum");
   void *buf = g_noalloc_ptr[ctx().device];
   if (!buf) return fail(MS_E_STATE, "q4_matmul_noalloc: scratch address not set up");
-  return q4_matmul_impl(d_C, d_A, d_packed, M, K, N, scale, accumulate, buf);
+  return q4_matmul_impl(d_C, d_A, d_packed, M, K, N, scale, accumulate, buf, ks);
 }
 

@@ -132,6 +132,17 @@ def test_q4_matmul_accumulates(gpu, oracle):
     ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pk.ptr, M, K, N, 0.1, 1))
     ref = C0 + oracle.matmul_f64(A, q4, N, 0.1)
     assert rel_max(dC.download(np.float32, (M, N)), ref) < 1e-5
+    # few tiles and a long K: the K split (partial sums added by the combine)
+    Ms, Ks = 24, 4096
+    q4s = ms.host_random_u8(Ks * N // 2, 6, 6).reshape(Ks, N // 2)
+    _, d_pks = packed(ms, q4s, Ks, N)
+    A = RNG.standard_normal((Ms, Ks)).astype(np.float32)
+    C0 = RNG.standard_normal((Ms, N)).astype(np.float32)
+    dA = ms.DeviceBuffer.from_array(A)
+    dC = ms.DeviceBuffer.from_array(C0)
+    ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pks.ptr, Ms, Ks, N, 0.1, 1))
+    ref = C0 + oracle.matmul_f64(A, q4s, N, 0.1)
+    assert rel_max(dC.download(np.float32, (Ms, N)), ref) < 1e-5
     # and the big-tile GEMM (enough blocks, ragged M and N)
     M, N = 600, 16432
     q4 = ms.host_random_u8(K * N // 2, 5, 5).reshape(K, N // 2)
