@@ -1094,7 +1094,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
   // host launches only the chunks its bound on the position can reach, so
   // the rows are loaded before the position arrives (slots past it are
   // zeroed below).
-  const int base = aldg_lane<int32_t>(p.pos + b);
+  const int base = aldg<int32_t>(p.pos + b);
   float4 kr[F4], vr[F4];
 #pragma unroll
   for (int j = 0; j < F4; ++j) {
