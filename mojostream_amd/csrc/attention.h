@@ -68,6 +68,12 @@ inline size_t dec_part_floats(int B, int n_heads, int hd) {
 int dec_part_chunks(const AttnArgs &a);
 bool dec_part_ok(const AttnArgs &a);
 int launch_attention_partials(const AttnArgs &a, hipStream_t st);
+// Two to four rows of one sequence on a linear cache (attn_rows_ok): the
+// chunk scheme of the decode step per row (k_attn_rows), then the chunks
+// merged per row and query head into a.out [T][q_dim].  The partials need
+// dec_part_floats(T, ...).
+bool attn_rows_ok(const AttnArgs &a);
+int launch_attention_rows(const AttnArgs &a, hipStream_t st);
 // a.rope_cur from the tables at the position of sequence 0 (one block)
 int launch_rope_cur(const AttnArgs &a, hipStream_t st);
 

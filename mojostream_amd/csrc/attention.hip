@@ -1644,6 +1644,303 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs args) {
         float2{sm[tid], sl[tid]};
 }
 
+// ------------------------------------------------------------------------------
+// k_attn_rows: T = 2..4 rows of one sequence at positions base .. base + T - 1
+// on a linear cache (a harness step of a few rows), the decode chunk scheme
+// per row.  Block (c, (t n_kv + h) NS + s), 1024 threads: cache slots
+// 32c..32c+31 for row t and query heads s GQ .. s GQ + GQ - 1 of kv head h.
+// Slots base .. base + t are this call's rows 0 .. t: their keys and values
+// come from the q|k|v rows (rotated here), never from the cache, which the
+// block of row t' writes at slot base + t' (head split 0 only), so no block
+// reads a slot another block writes.  Slots past base + t are masked.  The
+// chunk's (o, m, l) per query head go to the row's partials (region t), which
+// k_attn_rows_merge combines.
+// ------------------------------------------------------------------------------
+constexpr int kRowsMax = 4;
+
+template <int HD, int GQ>
+__global__ __launch_bounds__(1024) void k_attn_rows(AttnArgs args) {
+  extern __shared__ __align__(16) float lds[];
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int CH = kDecPartChunk;
+  static_assert(CH == 32, "32 keys per chunk: one key per 32 lanes");
+  constexpr int NT = 1024;
+  constexpr int H4 = HD / 4;
+  constexpr int NF = HD / 128;                        // float4 of a key row per thread
+  constexpr int QPT = (GQ * HD + NT - 1) / NT;         // q elements per thread
+  constexpr int FPT = (kRowsMax * HD + NT - 1) / NT;   // fresh row elements per thread
+  constexpr int NU = GQ * H4;
+  constexpr int NKG = NT / NU;
+  constexpr int KPG = CH / NKG;
+  static_assert(NF >= 1 && NKG >= 1 && CH % NKG == 0, "head dim 128, 256 or 512");
+  constexpr uint32_t kOut = 0x80000000u;
+  const AttnP p = load_params(args);
+  const int tid = threadIdx.x;
+  const int c = blockIdx.x;
+  const int G = p.G, T = p.T;
+  const int NS = G > GQ ? G / GQ : 1;
+  const int s = (int)blockIdx.y % NS, r = (int)blockIdx.y / NS;
+  const int h = r % p.n_kv, t = r / p.n_kv;
+  const int g0 = s * GQ, Gl = min(GQ, G - g0);
+  const int L = p.cache_len;
+  const int nq = Gl * HD;
+  const int key = tid >> 5, j = tid & 31;
+
+  float *sv = lds;                      // [CH][HD] values
+  float *sq = sv + CH * HD;             // [GQ][HD] rotated queries
+  float *sf = sq + GQ * HD;             // [kRowsMax][HD] this call's keys, rotated
+  float *ss = sf + kRowsMax * HD;       // [GQ][CH] scores -> numerators
+  float *sm = ss + GQ * CH;             // [GQ]
+  float *sl = sm + 4;                   // [GQ]
+  float4 *so = reinterpret_cast<float4 *>(sl + 4);  // [NKG][NU] partial o
+
+  // ---- loads that do not depend on the position (branch-free, range-checked)
+  const int base = aldg_lane<int32_t>(p.pos);
+  const uint32_t cbytes = (uint32_t)L * (uint32_t)p.kv_dim * 4u;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(p.kc, 0, cbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(p.vc, 0, cbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(p.qkv), 0, (uint32_t)(T * p.ld) * 4u, 0x00020000);
+  const int slot = c * CH + key;
+  float4 kr[NF], vr[NF];
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    const uint32_t off =
+        slot < L ? ((uint32_t)slot * (uint32_t)p.kv_dim + (uint32_t)(h * HD + 4 * (i * 32 + j))) * 4u
+                 : kOut;
+    const f32x4 kv = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+    const f32x4 vv = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    kr[i] = float4{kv.x, kv.y, kv.z, kv.w};
+    vr[i] = float4{vv.x, vv.y, vv.z, vv.w};
+  }
+  auto ld1 = [&](const __amdgpu_buffer_rsrc_t &rs, bool on, int idx) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rs, on ? (uint32_t)idx * 4u : kOut, 0, 0));
+  };
+  float qx[QPT], qy[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int e = tid + NT * u;
+    const int g = e / HD, d = e % HD;
+    const int q0 = t * p.ld + (h * G + g0 + g) * HD;
+    qx[u] = ld1(rq, e < nq, q0 + d);
+    qy[u] = ld1(rq, e < nq, q0 + rope_partner(p, d));
+  }
+  // this call's keys and values: element e = (row e / HD, dim e % HD)
+  float kx[FPT], ky[FPT], vx[FPT];
+#pragma unroll
+  for (int u = 0; u < FPT; ++u) {
+    const int e = tid + NT * u;
+    const int tf = e / HD, d = e % HD;
+    const bool on = tf < T;
+    const int k0 = tf * p.ld + p.q_dim + h * HD;
+    kx[u] = ld1(rq, on, k0 + d);
+    ky[u] = ld1(rq, on, k0 + rope_partner(p, d));
+    vx[u] = ld1(rq, on, tf * p.ld + p.q_dim + p.kv_dim + h * HD + d);
+  }
+  asm volatile("" ::: "memory");
+
+  // ---- the position: row t attends slots [0, base + t]
+  const int pos_t = base + t;
+  const int nslots = min(pos_t + 1, L);
+  const int n_active = min((nslots + CH - 1) / CH, p.grid_chunks);
+  if (c >= n_active) return;
+  // RoPE factors of row t (queries) and of this call's rows (keys)
+  float qc[QPT], qs[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) rope_cs(p, (tid + NT * u) % HD, pos_t, qc[u], qs[u]);
+  const bool own_fresh = slot >= base && slot < nslots;
+  if (slot >= nslots) {
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      kr[i] = float4{0.f, 0.f, 0.f, 0.f};
+      vr[i] = float4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  if (!own_fresh) {
+#pragma unroll
+    for (int i = 0; i < NF; ++i)
+      *reinterpret_cast<float4 *>(sv + key * HD + 4 * (i * 32 + j)) = vr[i];
+  }
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int e = tid + NT * u;
+    if (e < GQ * HD) sq[e] = e < nq ? rope_mix(p, e % HD, qx[u], qy[u], qc[u], qs[u]) : 0.f;
+  }
+#pragma unroll
+  for (int u = 0; u < FPT; ++u) {
+    const int e = tid + NT * u;
+    const int tf = e / HD, d = e % HD;
+    const int sf_slot = base + tf;  // rows 0 .. t of this call in this chunk
+    if (tf <= t && sf_slot >= c * CH && sf_slot < c * CH + CH) {
+      float cs, sn;
+      rope_cs(p, d, sf_slot, cs, sn);
+      // write_kv_full (gemma4_e4b.mojo:211-249)
+      const float kv = rope_mix(p, d, kx[u], ky[u], cs, sn);
+      sf[tf * HD + d] = kv;
+      sv[(sf_slot - c * CH) * HD + d] = vx[u];
+      if (p.write_cache && tf == t && s == 0) {
+        const size_t off = (size_t)sf_slot * p.kv_dim + h * HD + d;
+        p.kc[off] = kv;
+        p.vc[off] = vx[u];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- scores, numerators, P.V (as k_attn_part)
+  if (own_fresh) {
+#pragma unroll
+    for (int i = 0; i < NF; ++i)
+      kr[i] = *reinterpret_cast<const float4 *>(sf + (slot - base) * HD + 4 * (i * 32 + j));
+  }
+  float acc[GQ];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    acc[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      const float4 qq = *reinterpret_cast<const float4 *>(sq + g * HD + 4 * (i * 32 + j));
+      acc[g] += qq.x * kr[i].x + qq.y * kr[i].y + qq.z * kr[i].z + qq.w * kr[i].w;
+    }
+    acc[g] = row16_sum(acc[g]);
+    acc[g] += __shfl_xor(acc[g], 16, 64);
+  }
+  if (j == 0) {
+    const bool ok = slot < nslots;
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+      if (g < Gl) ss[g * CH + key] = ok ? acc[g] * p.scale : -INFINITY;
+  }
+  __syncthreads();
+  if (tid < CH * GQ) {
+    const int g = tid / CH, k = tid % CH;
+    const float sc = g < Gl ? ss[g * CH + k] : -INFINITY;
+    float m = row16_max(sc);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    const float pr = (sc == -INFINITY) ? 0.f : expf(sc - m);
+    float l = row16_sum(pr);
+    l += __shfl_xor(l, 16, 64);
+    if (g < Gl) {
+      ss[g * CH + k] = pr;
+      if (k == 0) {
+        sm[g] = m;
+        sl[g] = l;
+      }
+    }
+  }
+  __syncthreads();
+  const int u = tid % NU, kq = tid / NU;
+  const int g = u / H4, d4 = u % H4;
+  {
+    const float4 *sv4 = reinterpret_cast<const float4 *>(sv);
+    float4 o = float4{0.f, 0.f, 0.f, 0.f};
+    if (g < Gl) {
+#pragma unroll
+      for (int k = kq * KPG; k < kq * KPG + KPG; ++k) {
+        const float pk = ss[g * CH + k];
+        const float4 v = sv4[k * H4 + d4];
+        o.x += pk * v.x;
+        o.y += pk * v.y;
+        o.z += pk * v.z;
+        o.w += pk * v.w;
+      }
+    }
+    so[kq * NU + u] = o;
+  }
+  __syncthreads();
+  const int nhq = p.n_heads;
+  float *po = p.part + (size_t)t * kDecPartMaxChunks * nhq * (HD + 2);
+  float *pml = po + (size_t)kDecPartMaxChunks * nhq * HD;
+  if (tid < NU && g < Gl) {
+    float4 o = so[u];
+#pragma unroll
+    for (int q = 1; q < NKG; ++q) {
+      const float4 w = so[q * NU + u];
+      o.x += w.x;
+      o.y += w.y;
+      o.z += w.z;
+      o.w += w.w;
+    }
+    *reinterpret_cast<float4 *>(po + ((size_t)c * nhq + h * G + g0 + g) * HD + 4 * d4) = o;
+  }
+  if (tid < Gl)
+    *reinterpret_cast<float2 *>(pml + ((size_t)c * nhq + h * G + g0 + tid) * 2) =
+        float2{sm[tid], sl[tid]};
+}
+
+// The chunks of k_attn_rows merged per (query head, row) (log-sum-exp over
+// the chunks the row attends): out [T][q_dim].  H4 threads, a float4 of dims
+// each.
+template <int HD>
+__global__ __launch_bounds__(128) void k_attn_rows_merge(AttnArgs args) {
+  constexpr int H4 = HD / 4;
+  const int hq = blockIdx.x, t = blockIdx.y, d4 = threadIdx.x;
+  const int nhq = args.n_heads;
+  const int base = aldg<int32_t>(args.pos);
+  const int nslots = min(base + t + 1, args.cache_len);
+  const int n_act = min((nslots + kDecPartChunk - 1) / kDecPartChunk, args.grid_chunks);
+  const float *po = args.part + (size_t)t * kDecPartMaxChunks * nhq * (HD + 2);
+  const float *pml = po + (size_t)kDecPartMaxChunks * nhq * HD;
+  float M = -INFINITY;
+  for (int c = 0; c < n_act; ++c) M = fmaxf(M, aldg<float>(pml + ((size_t)c * nhq + hq) * 2));
+  float l = 0.f;
+  float4 o = float4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < n_act; ++c) {
+    const float mc = aldg<float>(pml + ((size_t)c * nhq + hq) * 2);
+    const float lc = aldg<float>(pml + ((size_t)c * nhq + hq) * 2 + 1);
+    const float w = expf(mc - M);
+    l += lc * w;
+    if (d4 < H4) {
+      const float4 v = aldg<float4>(po + ((size_t)c * nhq + hq) * HD + 4 * d4);
+      o.x += w * v.x;
+      o.y += w * v.y;
+      o.z += w * v.z;
+      o.w += w * v.w;
+    }
+  }
+  if (d4 < H4) {
+    const float inv = 1.0f / l;
+    *reinterpret_cast<float4 *>(args.out + (size_t)t * args.q_dim + hq * HD + 4 * d4) =
+        float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+  }
+}
+
+bool attn_rows_ok(const AttnArgs &a) {
+  const int G = a.n_kv > 0 ? a.n_heads / a.n_kv : 0;
+  return a.B == 1 && a.T >= 2 && a.T <= kRowsMax && G >= 1 && G <= 4 && G != 3 &&
+         a.n_heads % a.n_kv == 0 && (a.hd == 128 || a.hd == 256 || a.hd == 512) &&
+         a.rot % 2 == 0 && a.rot <= a.hd && a.cache_kind != MS_CACHE_CIRCULAR &&
+         a.ld >= a.q_dim + 2 * a.kv_dim && a.pos_bound > 0 && a.pos_bound <= a.cache_len &&
+         dec_part_chunks(a) <= kDecPartMaxChunks;
+}
+
+int launch_attention_rows(const AttnArgs &a, hipStream_t st) {
+  MS_CHECK_ARG(attn_rows_ok(a), "attention rows: unsupported shape");
+  MS_CHECK_ARG(a.qkv && a.part && a.pos && a.kc && a.vc && a.out && a.cos_t && a.sin_t,
+               "attention rows: missing buffers");
+  AttnArgs a2 = a;
+  a2.grid_chunks = dec_part_chunks(a);
+  constexpr int GQ = 2;
+  const int G = a.n_heads / a.n_kv;
+  const int ns = G > GQ ? G / GQ : 1;
+  const dim3 grid(a2.grid_chunks, a.T * a.n_kv * ns);
+  constexpr int CH = kDecPartChunk;
+  const size_t shmem =
+      (size_t)(CH * a.hd + GQ * a.hd + kRowsMax * a.hd + GQ * CH + 8) * 4 + 16384;
+  if (a.hd == 128) hipLaunchKernelGGL((k_attn_rows<128, GQ>), grid, dim3(1024), shmem, st, a2);
+  else if (a.hd == 256) hipLaunchKernelGGL((k_attn_rows<256, GQ>), grid, dim3(1024), shmem, st, a2);
+  else hipLaunchKernelGGL((k_attn_rows<512, GQ>), grid, dim3(1024), shmem, st, a2);
+  MS_HIP_TRY(hipGetLastError());
+  const dim3 mgrid(a.n_heads, a.T);
+  const int mthreads = a.hd / 4 < 64 ? 64 : a.hd / 4;
+  if (a.hd == 128) hipLaunchKernelGGL(k_attn_rows_merge<128>, mgrid, dim3(mthreads), 0, st, a2);
+  else if (a.hd == 256) hipLaunchKernelGGL(k_attn_rows_merge<256>, mgrid, dim3(mthreads), 0, st, a2);
+  else hipLaunchKernelGGL(k_attn_rows_merge<512>, mgrid, dim3(mthreads), 0, st, a2);
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
+}
+
 int dec_part_chunks(const AttnArgs &a) {
   const int reach = a.pos_bound > 0 ? std::min(a.pos_bound, a.cache_len) : a.cache_len;
   return std::max(1, (reach + kDecPartChunk - 1) / kDecPartChunk);

@@ -430,6 +430,9 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
       }
       if (int rc2 = launch_attention_partials(a, st)) return rc2;
       merged_in_o = true;
+    } else if (attn_rows_ok(a)) {
+      // two to four rows of one sequence: chunk partials per row, merged
+      if (int rc2 = launch_attention_rows(a, st)) return rc2;
     } else if (rc.B == 1 && rc.T > kGemvMaxM && m->fq && prefill_flash_ok(a)) {
       // prefill rows: flash attention on fp32 MFMA
       if (int rc2 = launch_attention_prefill(a, m->fq, m->fk, m->fpart, m->fpart_floats, st))
@@ -842,8 +845,10 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
     const int G = ld.n_heads / ld.n_kv_heads;
     max_part = std::max(max_part, attn_part_floats(d.max_seqs, ld.n_kv_heads, Ly.n_chunks,
                                                    attn_rows, G, ld.head_dim));
-    // a batch-1 decode step's chunk partials, merged in the O projection
-    max_part = std::max(max_part, dec_part_floats(1, ld.n_heads, ld.head_dim));
+    // a batch-1 decode step's chunk partials, merged in the O projection, or
+    // those of two to four rows of one sequence
+    max_part = std::max(max_part, dec_part_floats(std::min(d.max_rows, 4), ld.n_heads,
+                                                  ld.head_dim));
     m->qkv_max = std::max(m->qkv_max, ncols_qkv);
     m->q_max = std::max(m->q_max, ld.q_dim);
     m->quant_k = std::max(m->quant_k, std::max(std::max(d.hidden, d.ffn), ld.q_dim));

@@ -77,17 +77,31 @@ def test_demo_harness_100_steps(gpu, fast_oracle):
     m.close()
 
 
-def test_demo_teacher_forced_layers(gpu, fast_oracle):
+@pytest.mark.parametrize("T", [4, 3, 2])
+def test_demo_teacher_forced_layers(gpu, fast_oracle, T):
+    """Steps of T rows of one sequence (T = 2..4: the chunk partials per row
+    and their merge, k_attn_rows), layer by layer against the oracle, at bases
+    0, T and 63 (a step across a 32-key chunk boundary)."""
     ms = gpu
     arch = ms.arch_demo(max_len=512, n_layers=6)
-    say("demo teacher-forced, 6 layers x 2 steps")
+    say(f"demo teacher-forced, 6 layers x 3 steps of {T} rows")
     m = build(ms, arch, max_seqs=1, max_rows=4, max_pos=512)
     om = synthetic_oracle_model(fast_oracle, arch, SEED, with_lm=False)
-    for step in range(2):
-        x = ms.host_normal(4 * 1024, 77 + step, 2).reshape(4, 1024)
+    for step, base in enumerate((0, T, 63)):
+        if step == 2:
+            # fill positions 2T .. 62 so that the step at 63 attends written rows
+            fill = ms.host_normal((63 - 2 * T) * 1024, 90, 2).reshape(63 - 2 * T, 1024)
+            for r0 in range(0, fill.shape[0], 4):
+                rows = fill[r0:r0 + 4]
+                xr = rows
+                for l in range(arch.n_layers):
+                    ref = om.layer_forward(l, xr, 2 * T + r0)
+                    m.layer_forward(l, xr, [2 * T + r0], T=rows.shape[0])
+                    xr = ref
+        x = ms.host_normal(T * 1024, 77 + step, 2).reshape(T, 1024)
         for l in range(arch.n_layers):
-            ref = om.layer_forward(l, x, 4 * step)
-            got = m.layer_forward(l, x, [4 * step], T=4)
+            ref = om.layer_forward(l, x, base)
+            got = m.layer_forward(l, x, [base], T=T)
             e = rel_rmse(got, ref)
             assert e < 1e-4, (step, l, e)
             x = ref  # feed the oracle's output to the next GPU layer
