@@ -1,31 +1,33 @@
 // Q4 GEMM for prefill rows (M > 16) on v_mfma_i32_16x16x64_i8.
 //
-// The A operand is that of the GEMV in q4.hip: activation rows quantized by
-// launch_quant_rows into four int8 limbs per value (limb row 4m + l, MFMA
-// fragment order inside each 128-row super-tile of K).  The weights enter as
-// the unsigned nibbles n straight from the panel layout (a mask per dword,
-// where the GEMV's signed n - 8 takes three operations: the conversion is
-// most of this kernel's VALU work), and the zero point comes back per row:
-// sum_k X_k (n_k - 8) = sum_k X_k n_k - 8 * xsum, with xsum = sum_k X_k from
-// the quantization.  Each limb row's dot product is exact in int32; the four
-// limbs of an output combine exactly (limb_combine: an integer below 2^51,
-// formed in double), minus 8 * xsum, and are scaled by 2^-s and the tensor
-// scale with the GEMV's expression, so a row gets the same value from these
-// kernels as from the GEMV.  launch_gemm picks the 32-row kernel (k_gemm) or
-// the big tile (k_gemm_big, described further down) per launch.
+// The A operand: activation rows quantized by launch_quant_rows3 to 22-bit
+// fixed point, X = rint(y 2^s) with max |y| 2^s < 2^22 (s per row), in three
+// balanced int8 limbs stored as limb planes (plane l: limb l of every row, in
+// the MFMA fragment order of the GEMV's limb rows inside each 128-row
+// super-tile of K).  An A tile is 16 rows of one limb plane, so the D fragment
+// of limb l gives lane j + 16r the limb-l sums of rows 4r .. 4r + 3 at column
+// j, and the three limbs of an output meet in one lane.  (The GEMV's four
+// limbs, 31-bit fixed point, would cost a third more MFMAs here, where the
+// MFMAs set the time; 22 bits keep every row within 2^-23 of its maximum,
+// the rounding of an fp32 product.)  The weights enter as the unsigned
+// nibbles n straight from the panel layout (a mask per dword), and the zero
+// point comes back per row: sum_k X_k (n_k - 8) = sum_k X_k n_k - 8 * xsum,
+// with xsum = sum_k X_k from the quantization.  Each limb's dot product is
+// exact in int32; the three limbs of an output combine exactly
+// (limb_combine3), minus 8 * xsum, and are scaled by 2^-s and the tensor
+// scale.  launch_gemm picks the 32-row kernel (k_gemm) or the big tile
+// (k_gemm_big, described further down) per launch.
 //
-// k_gemm tiling: a block computes kBM = 32 activation rows (128 limb rows, 8 MFMA A
-// tiles) by 4 kWB panels (8 panels, 128 columns).  Wave (wa, wb) owns A tiles
-// 4wa..4wa+3 and panels 4wb..4wb+3: 16 accumulators and 32 MFMAs per 128-row
-// step of K.  Both operands of a step (A 128 limb rows x 128 bytes, B one
-// 1 KiB super-tile of each panel) go from global memory straight into LDS
-// (global_load_lds: each wave instruction fills 1 KiB), in a ring of three
-// steps; loads run two steps ahead of the MFMAs, which a step's MFMA time
-// alone does not cover.  A limb rows are stored without padding, chunk c of
-// row r at chunk position c ^ ((r >> 1) & 7), so the 16 rows one fragment
-// read touches fall in 16 different bank groups.  In the D fragment of an A
-// tile, lane j + 16r holds the four limbs of activation row r, column j, so
-// the limbs combine inside the lane and no cross-wave reduction is needed.
+// k_gemm tiling: a block computes kBM = 32 activation rows (96 limb rows, 6 MFMA A
+// tiles) by 4 kWB panels (8 panels, 128 columns).  Wave (wa, wb) owns rows
+// 16wa..16wa+15 (one A tile per limb) and panels 4wb..4wb+3: 12 accumulators
+// and 24 MFMAs per 128-row step of K.  Both operands of a step (A 96 limb rows
+// x 128 bytes, B one 1 KiB super-tile of each panel) go from global memory
+// straight into LDS (global_load_lds: each wave instruction fills 1 KiB), in
+// a ring of three steps; loads run two steps ahead of the MFMAs, which a
+// step's MFMA time alone does not cover.  A limb rows are stored without
+// padding, chunk c of row r at chunk position c ^ ((r >> 1) & 7), so the 16
+// rows one fragment read touches fall in 16 different bank groups.
 //
 // EPI_SWIGLU: the first half of the wave columns computes gate panels, the
 // second half the up panels of the same columns; the gate values pass through
@@ -42,26 +44,23 @@ namespace {
 constexpr int kBM = 32;                  // activation rows per block
 constexpr int kWB = 2;                   // wave columns: 4 panels each
 constexpr int kNT = 128 * kWB;           // threads (2 wave rows x kWB wave columns)
-constexpr int kAstage = 4 * kBM * 128;   // one K step of A: 128 limb rows x 128 bytes
+constexpr int kLimbs = 3;                // limb planes of the A operand
+constexpr int kAstage = kLimbs * kBM * 128;  // one K step of A: 96 limb rows x 128 bytes
 constexpr int kBstage = 8 * 1024;        // one super-tile of each of the 8 panels
 constexpr int kStage = kAstage + kBstage;
 constexpr int kStages = 3;               // K steps resident in LDS
-constexpr int kGemmLds = kStages * kStage;  // 72 KiB
-constexpr int kLoads = 6;                // direct loads per thread per K step
+constexpr int kGemmLds = kStages * kStage;  // 60 KiB
+constexpr int kLoads = 5;                // direct loads per thread per K step
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void gbl_void;
 
-// Exact limb combine of one D fragment value, minus the zero-point term z:
-// each limb's int32 dot product is below 2^25 in magnitude (K <= 16384,
-// |limb| <= 128, nibble <= 15), so d0 + 2^8 d1 + 2^16 d2 + 2^24 d3 - z is an
-// integer below 2^51, formed exactly in double by FMAs: the same double the
-// 64-bit integer path produces, in fewer instructions.
-__device__ inline double limb_combine(const v4i d, double z) {
-  return __builtin_fma((double)d[3], 16777216.0,
-                       __builtin_fma((double)d[2], 65536.0,
-                                     __builtin_fma((double)d[1], 256.0, (double)d[0]))) -
-         z;
+// Exact limb combine of one output, minus the zero-point term z: each limb's
+// int32 dot product is below 2^25 in magnitude (K <= 16384, |limb| <= 128,
+// nibble <= 15), so d0 + 2^8 d1 + 2^16 d2 - z is an integer below 2^43,
+// formed exactly in double by FMAs.
+__device__ inline double limb_combine3(int d0, int d1, int d2, double z) {
+  return __builtin_fma((double)d2, 65536.0, __builtin_fma((double)d1, 256.0, (double)d0)) - z;
 }
 
 template <int EPI>
@@ -139,25 +138,26 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
     slot(2 * wave + j, &lw[j], &sc, &cl, &ok);
   }
 
-  // A: this wave fills LDS blocks 4 wave + i (limb rows 8q .. 8q + 7) of a
-  // stage; lane l writes row 8q + l / 8 at chunk position l % 8, which holds
-  // chunk (l % 8) ^ ((row >> 1) & 7) of the row, so the 16 rows one fragment
-  // read touches fall in 16 different bank groups
-  const int8_t *abase = limbs + (size_t)(4 * r0) * K;
-  const int8_t *asrc[4];
+  // A: a stage holds limb rows 32l + m (limb l of block row m); this wave
+  // fills LDS blocks 3 wave + i (stage rows 8q .. 8q + 7); lane l writes row
+  // 8q + l / 8 at chunk position l % 8, which holds chunk (l % 8) ^
+  // ((row >> 1) & 7) of the row, so the 16 rows one fragment read touches
+  // fall in 16 different bank groups
+  const int pr = launder(g.a.plane_rows);
+  const int8_t *asrc[kLimbs];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 8 * (4 * wave + i) + (lane >> 3);
+  for (int i = 0; i < kLimbs; ++i) {
+    const int row = 8 * (kLimbs * wave + i) + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
-    asrc[i] = abase + (size_t)row * K + c * 16;
+    asrc[i] = limbs + ((size_t)(row >> 5) * pr + r0 + (row & 31)) * K + c * 16;
   }
   // K step G into stage stg: global memory straight into LDS
   auto issue = [&](int G, int stg) {
     uint8_t *sa = lds + stg * kStage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kLimbs; ++i)
       __builtin_amdgcn_global_load_lds((gbl_void *)(asrc[i] + (size_t)G * 128),
-                                       (lds_void *)(sa + (4 * wave + i) * 1024), 16, 0, 0);
+                                       (lds_void *)(sa + (kLimbs * wave + i) * 1024), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       __builtin_amdgcn_global_load_lds((gbl_void *)(lw[j] + (size_t)G * 1024 + lane * 16),
@@ -165,9 +165,10 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
                                        0, 0);
   };
 
-  v4i acc[4][4];
+  // acc[l][j]: limb l of block rows 16 wa .. 16 wa + 15, panel 4 wb + j
+  v4i acc[kLimbs][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < kLimbs; ++a)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[a][j] = v4i{0, 0, 0, 0};
 
@@ -190,8 +191,8 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
       }
       const int pos = (2 * lg + h) ^ swz;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const v4i af = *reinterpret_cast<const v4i *>(sa + (16 * (4 * wa + a) + li) * 128 +
+      for (int a = 0; a < kLimbs; ++a) {
+        const v4i af = *reinterpret_cast<const v4i *>(sa + (32 * a + 16 * wa + li) * 128 +
                                                       pos * 16);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -200,15 +201,16 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
     }
   };
 
-  // the epilogue's row shifts and sums, loaded before the K loop (rows past
-  // M: shift 0, sum 0; their outputs are not stored)
+  // the epilogue's row shifts and sums, loaded before the K loop: lane
+  // j + 16 rr holds rows 16 wa + 4 rr + i of column j (rows past M: shift
+  // 0, sum 0; their outputs are not stored)
   int32_t rsh[4];
   double rz[4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int row = r0 + 4 * (4 * wa + a) + (lane >> 4);
-    rsh[a] = row < M ? ldg<int32_t>(shift + row) : 0;
-    rz[a] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
+  for (int i = 0; i < 4; ++i) {
+    const int row = r0 + 16 * wa + 4 * (lane >> 4) + i;
+    rsh[i] = row < M ? ldg<int32_t>(shift + row) : 0;
+    rz[i] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
   }
 
   // K steps of this block: all of them, or part blockIdx.z of ksplit
@@ -238,31 +240,31 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   const int jc = lane & 15, rr = lane >> 4;
   if constexpr (EPI == EPI_STORE || EPI == EPI_ACCUMULATE) {
     if (ks > 1) {
-      // this part's exact sums d0 + 2^8 d1 + 2^16 d2 + 2^24 d3 (k_gemm_kcombine)
+      // this part's exact sums d0 + 2^8 d1 + 2^16 d2 (k_gemm_kcombine)
       int64_t *kp = launder(g.kpart) + (size_t)blockIdx.z * M * ldo;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int row = r0 + 4 * (4 * wa + a) + rr;
+      for (int i = 0; i < 4; ++i) {
+        const int row = r0 + 16 * wa + 4 * rr + i;
         if (row >= M) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           if (!pv[j]) continue;
-          const v4i d = acc[a][j];
-          kp[(size_t)row * ldo + col[j] + jc] =
-              (int64_t)d[0] + ((int64_t)d[1] << 8) + ((int64_t)d[2] << 16) +
-              ((int64_t)d[3] << 24);
+          kp[(size_t)row * ldo + col[j] + jc] = (int64_t)acc[0][j][i] +
+                                                ((int64_t)acc[1][j][i] << 8) +
+                                                ((int64_t)acc[2][j][i] << 16);
         }
       }
       return;
     }
   }
-  float v[4][4];
+  float v[4][4];  // [row i][panel j]
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const float sc = ldexpf(1.0f, -rsh[a]);
+  for (int i = 0; i < 4; ++i) {
+    const float sc = ldexpf(1.0f, -rsh[i]);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      v[a][j] = (float)(limb_combine(acc[a][j], rz[a]) * (double)sc * (double)wsc[j]);
+      v[i][j] = (float)(limb_combine3(acc[0][j][i], acc[1][j][i], acc[2][j][i], rz[i]) *
+                        (double)sc * (double)wsc[j]);
   }
   if constexpr (EPI == EPI_SWIGLU) {
     // gate values of wave (wa, sub) -> LDS -> up wave (wa, sub)
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
     if (half == 1) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const int row = r0 + 4 * (4 * wa + a) + rr;
+        const int row = r0 + 16 * wa + 4 * rr + a;
         if (row >= M) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -292,7 +294,7 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   } else {
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      const int row = r0 + 4 * (4 * wa + a) + rr;
+      const int row = r0 + 16 * wa + 4 * rr + a;
       if (row >= M) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -314,24 +316,24 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 
 // ------------------------------------------------------------------------------
 // Big-tile variant for GEMMs with many blocks.  A block computes kGBM = 32
-// activation rows (128 limb rows) by kGPan = 16 panel slots (SwiGLU: the gate
-// and the up panels of 8 column groups).  Four waves; wave (wr, wc) owns limb
-// rows 64wr..64wr+63 (4 A tiles) and 8 panel slots: 32 accumulators.  Both
-// operands of a K step (A 16 KiB, B 16 KiB) go from global memory straight
-// into LDS (global_load_lds_dwordx4: each wave instruction fills 1 KiB, lane l
-// the 16 bytes at l * 16), in a ring of two steps: 64 KiB, so two blocks share
-// a CU and one block's barriers, pipeline start and epilogue overlap the
-// other's MFMAs (with one 8-wave block per CU, the per-step barrier and the
-// epilogue left the MFMA units idle for a third of the time).  A limb rows are
-// stored without padding, the 16-byte chunk c of row r at chunk position
-// c ^ ((r >> 1) & 7): the 16 rows one A fragment read touches then fall in 16
-// different bank groups.
+// activation rows (96 limb rows) by kGPan = 16 panel slots (SwiGLU: the gate
+// and the up panels of 8 column groups).  Four waves; wave (wr, wc) owns rows
+// 16wr..16wr+15 (one A tile per limb) and 8 panel slots: 24 accumulators.
+// Both operands of a K step (A 12 KiB, B 16 KiB) go from global memory
+// straight into LDS (global_load_lds_dwordx4: each wave instruction fills
+// 1 KiB, lane l the 16 bytes at l * 16), in a ring of two steps: 56 KiB, so
+// two blocks share a CU and one block's barriers, pipeline start and epilogue
+// overlap the other's MFMAs (with one 8-wave block per CU, the per-step
+// barrier and the epilogue left the MFMA units idle for a third of the time).
+// A limb rows are stored without padding, the 16-byte chunk c of row r at
+// chunk position c ^ ((r >> 1) & 7): the 16 rows one A fragment read touches
+// then fall in 16 different bank groups.
 //
 // EPI_SWIGLU: wave column wc holds the gate panels of column groups
 // 4wc..4wc+3 (slots j < 4) and the up panels of the same groups (j >= 4), so
 // each output's gate and up values meet in one lane.
 //
-// PS = 16 panel slots per block, or 10 (wave tile 4 A tiles x 5 panels) for
+// PS = 16 panel slots per block, or 10 (wave tile 3 A tiles x 5 panels) for
 // launches whose 16-slot tiles leave a last round of blocks mostly empty: O
 // and Down at 2048 rows (N = 160 panels) make 1024 ten-slot tiles, two full
 // rounds, against 640 sixteen-slot ones.
@@ -339,7 +341,7 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 constexpr int kGBM = 32;                     // activation rows per block
 constexpr int kGPan = 16;                    // panel slots per block (wide tile)
 constexpr int kGPanNarrow = 10;              // panel slots per block (narrow tile)
-constexpr int kGStageA = 4 * kGBM * 128;     // limb rows x 128 bytes
+constexpr int kGStageA = kLimbs * kGBM * 128;  // 96 limb rows x 128 bytes
 constexpr int kGStages = 2;
 constexpr int kGNT = 256;                    // threads per block
 // one super-tile per panel slot after the A step; two stages
@@ -415,23 +417,24 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
     bool ok;
     slot(wave + 4 * j < PS ? wave + 4 * j : wave, &lw[j], &sc, &col, &ok);
   }
-  // A: this wave fills LDS blocks 4 wave + i (limb rows 8q .. 8q + 7); lane l
-  // writes row 8q + l / 8 at chunk position l % 8, which holds chunk
-  // (l % 8) ^ ((row >> 1) & 7) of the row
-  const int8_t *abase = limbs + (size_t)(4 * r0) * K;
-  const int8_t *asrc[4];
+  // A: a stage holds limb rows 32l + m (limb l of block row m); this wave
+  // fills LDS blocks 3 wave + i (stage rows 8q .. 8q + 7); lane l writes row
+  // 8q + l / 8 at chunk position l % 8, which holds chunk (l % 8) ^
+  // ((row >> 1) & 7) of the row
+  const int pr = launder(g.a.plane_rows);
+  const int8_t *asrc[kLimbs];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 8 * (4 * wave + i) + (lane >> 3);
+  for (int i = 0; i < kLimbs; ++i) {
+    const int row = 8 * (kLimbs * wave + i) + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
-    asrc[i] = abase + (size_t)row * K + c * 16;
+    asrc[i] = limbs + ((size_t)(row >> 5) * pr + r0 + (row & 31)) * K + c * 16;
   }
   auto issue = [&](int G, int stg) {
     uint8_t *sa = lds + stg * kGStage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kLimbs; ++i)
       __builtin_amdgcn_global_load_lds((gbl_void *)(asrc[i] + (size_t)G * 128),
-                                       (lds_void *)(sa + (4 * wave + i) * 1024), 16, 0, 0);
+                                       (lds_void *)(sa + (kLimbs * wave + i) * 1024), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < kBL; ++j)
       if (wave + 4 * j < PS)
@@ -440,9 +443,10 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
                                          0, 0);
   };
 
-  v4i acc[4][PW];
+  // acc[l][j]: limb l of block rows 16 wr .. 16 wr + 15, panel slot wslot(j)
+  v4i acc[kLimbs][PW];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < kLimbs; ++a)
 #pragma unroll
     for (int j = 0; j < PW; ++j) acc[a][j] = v4i{0, 0, 0, 0};
 
@@ -465,8 +469,8 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
       }
       const int pos = (2 * lg + h) ^ swz;
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const v4i af = *reinterpret_cast<const v4i *>(sa + (64 * wr + 16 * a + li) * 128 +
+      for (int a = 0; a < kLimbs; ++a) {
+        const v4i af = *reinterpret_cast<const v4i *>(sa + (32 * a + 16 * wr + li) * 128 +
                                                       pos * 16);
 #pragma unroll
         for (int j = 0; j < PW; ++j)
@@ -490,12 +494,13 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
 
   // ---- epilogue: lane (column jc, row rr of each A tile)
   const int jc = lane & 15, rr = lane >> 4;
+  // lane j + 16 rr holds rows 16 wr + 4 rr + i of column j
   double rsc[4], rz[4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int row = r0 + 16 * wr + 4 * a + (lane >> 4);
-    rsc[a] = row < M ? (double)ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.0;
-    rz[a] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
+  for (int i = 0; i < 4; ++i) {
+    const int row = r0 + 16 * wr + 4 * (lane >> 4) + i;
+    rsc[i] = row < M ? (double)ldexpf(1.0f, -ldg<int32_t>(shift + row)) : 0.0;
+    rz[i] = row < M ? (double)(8 * ldg<long long>(xsum + row)) : 0.0;
   }
   float wsc[PW];
   int col[PW];
@@ -505,13 +510,14 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
     const uint8_t *w;
     slot(wslot(j), &w, &wsc[j], &col[j], &pv[j]);
   }
-  auto value = [&](int a, int j) {
-    return (float)(limb_combine(acc[a][j], rz[a]) * rsc[a] * (double)wsc[j]);
+  auto value = [&](int i, int j) {
+    return (float)(limb_combine3(acc[0][j][i], acc[1][j][i], acc[2][j][i], rz[i]) * rsc[i] *
+                   (double)wsc[j]);
   };
   if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      const int row = r0 + 16 * wr + 4 * a + rr;
+      const int row = r0 + 16 * wr + 4 * rr + a;
       if (row >= M) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -523,7 +529,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
   } else {
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      const int row = r0 + 16 * wr + 4 * a + rr;
+      const int row = r0 + 16 * wr + 4 * rr + a;
       if (row >= M) continue;
 #pragma unroll
       for (int j = 0; j < PW; ++j) {

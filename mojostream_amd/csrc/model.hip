@@ -277,12 +277,12 @@ constexpr size_t kLdsLimit = 150 * 1024;  // LDS of a GEMV launch with its limb 
 
 static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipStream_t st) {
   if (a.M > kGemvMaxM) {
-    // prefill rows: quantize every row once, then the MFMA GEMM
+    // prefill rows: quantize every row once (three limbs), then the MFMA GEMM
     GemmArgs g{};
     g.epi = a.epi;
     g.M = a.M;
     g.K = a.K;
-    g.a = quant_rows_view(m->quant, gemm_row_pad(a.M), a.K);
+    g.a = quant_rows3_view(m->quant, gemm_row_pad(a.M), a.K);
     for (int i = 0; i < 3; ++i) g.seg[i] = a.seg[i];
     g.nseg = a.nseg;
     g.out = a.out;
@@ -291,7 +291,7 @@ static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipS
     g.out2 = a.out2;
     g.sw_out = a.sw_out;
     g.ldo_sw = a.ldo_sw;
-    if (int rc = launch_quant_rows(r, a.M, a.K, g.a, st)) return rc;
+    if (int rc = launch_quant_rows3(r, a.M, a.K, g.a, st)) return rc;
     return launch_gemm(g, st);
   }
   a.asrc = AS_ROWS;

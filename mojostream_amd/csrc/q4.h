@@ -75,12 +75,15 @@ struct RowSrc {
 
 // Quantized rows in global memory: limb l of row m at
 // limbs[(4m + l) * K + limb position of k] (MFMA fragment order per 128-row
-// super-tile), shift[m] = s.
+// super-tile), shift[m] = s.  The GEMM's operand (launch_quant_rows3) has
+// three limbs in planes: limb l of row m at limbs[(l * plane_rows + m) * K +
+// limb position of k].
 struct QuantRows {
   int8_t *limbs;
   int32_t *shift;
   int64_t *xsum;  // sum over the row of X (launch_quant_rows); the GEMM feeds
                   // unsigned nibbles n and subtracts 8 * xsum
+  int plane_rows; // three-limb planes: rows per plane (0: four limbs per row)
 };
 
 struct GemvArgs {
@@ -162,6 +165,11 @@ int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStre
 size_t quant_rows_bytes(int M, int K);
 // Carve a QuantRows view out of one buffer of quant_rows_bytes(M, K).
 QuantRows quant_rows_view(void *buf, int M, int K);
+// The GEMM's operand: M rows (of Mp = gemm_row_pad(M) in the planes) as 22-bit
+// fixed point (max |y| 2^s < 2^22) in three int8 limbs, limb planes of Mp
+// rows.  The view fits in a buffer of quant_rows_bytes(Mp, K).
+QuantRows quant_rows3_view(void *buf, int Mp, int K);
+int launch_quant_rows3(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st);
 int pack_device(uint8_t *dst, const uint8_t *src, int K, int N, hipStream_t st);
 int launch_argmax_fin(const ArgmaxFin &f, hipStream_t st);
 int launch_gemm(const GemmArgs &g, hipStream_t st);

@@ -209,12 +209,13 @@ __device__ inline void quant8(const float (&v)[8], float mul, uint32_t (&lo)[4],
   byte_transpose4(E[2], E[6], E[3], E[7], hi);
 }
 
-// Per-row shift s with max|y| * 2^s < 2^30.
+// Per-row shift s with max|y| * 2^s < 2^30 (four limbs; 2^22 with three).
+template <int LIMBS = 4>
 __device__ inline int row_shift(float amax) {
   if (!(amax > 0.f)) return 0;
   int ex;
   (void)frexpf(amax, &ex);  // amax < 2^ex
-  return 30 - ex;
+  return (LIMBS == 4 ? 30 : 22) - ex;
 }
 
 // One row through NT threads, NG 8-row groups per thread (K <= 8 * NG * NT).
@@ -281,14 +282,15 @@ __device__ inline void block_sum_max(float &ss, float &mx, float *sh, bool fresh
 // Transform (x * pre_scale, rmsnorm, gamma: rmsnorm_inplace kernels.mojo:474-489,
 // ple_scale_inplace :506-516, rmsnorm_weighted_inplace :598-613), optional
 // fp32 stores by `writer`, quantization and limb stores: limb l of row m goes
-// to dst + (4m + l) * ld_dst + limb position.  Returns the row shift s.
+// to dst + (4m + l) * ld_dst + limb position (LIMBS 3: dst + (l * planes + m)
+// * ld_dst).  Returns the row shift s.
 // XS: also the row's sum of X, exact (integer partial sums below 2^53 add
 // exactly in double), into *xsum_out for every thread.
-template <int NT, int NG, bool GAM, bool XS = false>
+template <int NT, int NG, bool GAM, bool XS = false, int LIMBS = 4>
 __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
                                   RowRegs<NT, NG, GAM> &R, int8_t *dst, size_t ld_dst,
                                   float *sh, int *s_out, double *xsum_out = nullptr,
-                                  bool sh_fresh = false) {
+                                  bool sh_fresh = false, int planes = 0) {
   const int nq = K >> 3;
   float y[NG][8];
   float ss = 0.f, mx = 0.f;
@@ -327,7 +329,7 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
     // mx * inv can round below the largest |y * inv|; one ulp of headroom
     amax = amax * (1.0f + 1.0f / 4194304.0f);
   }
-  const int s = row_shift(amax);
+  const int s = row_shift<LIMBS>(amax);
   const float mul = ldexpf(1.0f, s);
   long long xs = 0;
 #pragma unroll
@@ -351,8 +353,10 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
     quant8<XS>(y[gi], mul, lo, hi, &xs);
     const int pos = limb_pos8(8 * q);
 #pragma unroll
-    for (int l = 0; l < 4; ++l)
-      *reinterpret_cast<uint2 *>(dst + (size_t)(4 * m + l) * ld_dst + pos) = uint2{lo[l], hi[l]};
+    for (int l = 0; l < LIMBS; ++l) {
+      const size_t row = LIMBS == 4 ? (size_t)(4 * m + l) : (size_t)l * planes + m;
+      *reinterpret_cast<uint2 *>(dst + row * ld_dst + pos) = uint2{lo[l], hi[l]};
+    }
   }
   *s_out = s;
   if constexpr (XS) {
@@ -370,8 +374,8 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
   }
 }
 
-// One row per block of NT threads (K <= 16 NT).
-template <bool GAM, int NT>
+// One row per block of NT threads (K <= 16 NT).  LIMBS 3: the GEMM's planes.
+template <bool GAM, int NT, int LIMBS = 4>
 __global__ __launch_bounds__(NT) void k_quant_rows(RowSrc r, int K, QuantRows q) {
   __shared__ __align__(8) float sh[32];  // also 16 doubles (row sum)
   RowRegs<NT, 2, GAM> R;
@@ -379,7 +383,8 @@ __global__ __launch_bounds__(NT) void k_quant_rows(RowSrc r, int K, QuantRows q)
   row_load<NT, 2, GAM>(r, K, m, R);
   int s;
   double xs;
-  row_finish<NT, 2, GAM, true>(r, K, m, true, R, q.limbs, K, sh, &s, &xs, true);
+  row_finish<NT, 2, GAM, true, LIMBS>(r, K, m, true, R, q.limbs, K, sh, &s, &xs, true,
+                                      q.plane_rows);
   if (threadIdx.x == 0) {
     q.shift[m] = s;
     q.xsum[m] = (int64_t)xs;
@@ -391,7 +396,7 @@ size_t quant_rows_bytes(int M, int K) {
 }
 
 QuantRows quant_rows_view(void *buf, int M, int K) {
-  QuantRows q;
+  QuantRows q{};
   uint8_t *b = static_cast<uint8_t *>(buf);
   q.limbs = reinterpret_cast<int8_t *>(b);
   const size_t o1 = ((size_t)4 * M * K + 63) & ~(size_t)63;
@@ -399,6 +404,31 @@ QuantRows quant_rows_view(void *buf, int M, int K) {
   const size_t o2 = (o1 + (size_t)M * 4 + 63) & ~(size_t)63;
   q.xsum = reinterpret_cast<int64_t *>(b + o2);
   return q;
+}
+
+QuantRows quant_rows3_view(void *buf, int Mp, int K) {
+  QuantRows q = quant_rows_view(buf, Mp, K);  // limbs first; three planes fit in four
+  q.plane_rows = Mp;
+  return q;
+}
+
+int launch_quant_rows3(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st) {
+  MS_CHECK_ARG(M >= 1 && K >= 8 && K % 8 == 0 && K <= kQuantMaxK,
+               "quant: row length must be a multiple of 8 in [8, 16384]");
+  MS_CHECK_ARG(r.x && r.ld >= K && q.limbs && q.shift && q.xsum && q.plane_rows >= M,
+               "quant: missing buffers");
+  if (K <= 16 * 256 && M >= 64) {
+    if (r.gamma)
+      hipLaunchKernelGGL((k_quant_rows<true, 256, 3>), dim3(M), dim3(256), 0, st, r, K, q);
+    else
+      hipLaunchKernelGGL((k_quant_rows<false, 256, 3>), dim3(M), dim3(256), 0, st, r, K, q);
+  } else if (r.gamma) {
+    hipLaunchKernelGGL((k_quant_rows<true, 1024, 3>), dim3(M), dim3(1024), 0, st, r, K, q);
+  } else {
+    hipLaunchKernelGGL((k_quant_rows<false, 1024, 3>), dim3(M), dim3(1024), 0, st, r, K, q);
+  }
+  MS_HIP_TRY(hipGetLastError());
+  return MS_OK;
 }
 
 int launch_quant_rows(const RowSrc &r, int M, int K, const QuantRows &q, hipStream_t st) {
@@ -1649,7 +1679,7 @@ static int q4_matmul_impl(float *d_C, const float *d_A, const uint8_t *d_packed,
     g.epi = accumulate ? EPI_ACCUMULATE : EPI_STORE;
     g.M = M;
     g.K = K;
-    g.a = quant_rows_view(buf, Mp, K);
+    g.a = quant_rows3_view(buf, Mp, K);
     g.ksplit = ks;
     if (ks > 1)
       g.kpart = reinterpret_cast<int64_t *>(static_cast<uint8_t *>(buf) +
@@ -1658,7 +1688,7 @@ static int q4_matmul_impl(float *d_C, const float *d_A, const uint8_t *d_packed,
     r.x = d_A;
     r.ld = K;
     r.pre_scale = 1.f;
-    if (int rc = launch_quant_rows(r, M, K, g.a, st)) return rc;
+    if (int rc = launch_quant_rows3(r, M, K, g.a, st)) return rc;
     g.seg[0] = GemvSeg{d_packed, scale, N, 0};
     g.nseg = 1;
     g.out = d_C;
