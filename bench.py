@@ -29,7 +29,7 @@ sys.path.insert(0, ROOT)
 METRIC = "E4B-shape Q4 decode tokens/s (batch 1/4), TTFT ms; achieved HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 # GEMV kernel of the Gate|Up projection (dominant decode kernel by bytes)
-GATEUP_KERNEL = "k_gemv<1, 2, 0, 4, 2, 1>"
+GATEUP_KERNEL = "k_gemv<1, 2, 3, 4, 2, 15>"
 
 
 def log(msg):
