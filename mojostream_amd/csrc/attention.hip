@@ -1870,38 +1870,67 @@ __global__ __launch_bounds__(1024) void k_attn_rows(AttnArgs args) {
 }
 
 // The chunks of k_attn_rows merged per (query head, row) (log-sum-exp over
-// the chunks the row attends): out [T][q_dim].  H4 threads, a float4 of dims
-// each.
+// the chunks the row attends): out [T][q_dim].  One block per (query head,
+// row), max(64, HD / 4) threads, a float4 of dims each.  Every load goes out
+// at entry: the position, lane c's (m, l) of chunk c, and the o partials of
+// the first kMergeBatch chunks (range-checked buffer loads: chunks past the
+// launched ones read zeros without a memory access).  The weights
+// w_c = e^(m_c - M) and l = sum_c l_c w_c come from wave reductions; chunks
+// past the row's last attended one are dropped by selects, so a stale
+// partial never enters the sum.
+constexpr int kMergeBatch = 8;
 template <int HD>
 __global__ __launch_bounds__(128) void k_attn_rows_merge(AttnArgs args) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   constexpr int H4 = HD / 4;
-  const int hq = blockIdx.x, t = blockIdx.y, d4 = threadIdx.x;
-  const int nhq = args.n_heads;
-  const int base = aldg<int32_t>(args.pos);
-  const int nslots = min(base + t + 1, args.cache_len);
-  const int n_act = min((nslots + kDecPartChunk - 1) / kDecPartChunk, args.grid_chunks);
+  const int hq = blockIdx.x, t = blockIdx.y, d4 = threadIdx.x, lane = threadIdx.x & 63;
+  const int nhq = keep(args.n_heads), gc = keep(args.grid_chunks);
+  const int cache_len = keep(args.cache_len), q_dim = keep(args.q_dim);
   const float *po = args.part + (size_t)t * kDecPartMaxChunks * nhq * (HD + 2);
   const float *pml = po + (size_t)kDecPartMaxChunks * nhq * HD;
-  float M = -INFINITY;
-  for (int c = 0; c < n_act; ++c) M = fmaxf(M, aldg<float>(pml + ((size_t)c * nhq + hq) * 2));
-  float l = 0.f;
-  float4 o = float4{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < n_act; ++c) {
-    const float mc = aldg<float>(pml + ((size_t)c * nhq + hq) * 2);
-    const float lc = aldg<float>(pml + ((size_t)c * nhq + hq) * 2 + 1);
-    const float w = expf(mc - M);
-    l += lc * w;
-    if (d4 < H4) {
-      const float4 v = aldg<float4>(po + ((size_t)c * nhq + hq) * HD + 4 * d4);
-      o.x += w * v.x;
-      o.y += w * v.y;
-      o.z += w * v.z;
-      o.w += w * v.w;
+  const int base = aldg_lane<int32_t>(args.pos);
+  const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(pml), 0, gc * nhq * 8, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(po), 0, gc * nhq * HD * 4, 0x00020000);
+  const f32x2 ml = __builtin_bit_cast(
+      f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, (lane * nhq + hq) * 8, 0, 0));
+  const int od = d4 < H4 ? 16 * d4 : 0;  // idle lanes re-read dims 0..3
+  f32x4 v[kMergeBatch];
+#pragma unroll
+  for (int u = 0; u < kMergeBatch; ++u)
+    v[u] = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, (u * nhq + hq) * HD * 4 + od, 0, 0));
+  const int nslots = min(base + t + 1, cache_len);
+  const int n_act = min((nslots + kDecPartChunk - 1) / kDecPartChunk, gc);
+  const bool on = lane < n_act;
+  const float M = wave64_max(on ? ml.x : -INFINITY);
+  const float w = on ? expf(ml.x - M) : 0.f;
+  const float l = wave64_sum(on ? ml.y * w : 0.f);
+  f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kMergeBatch; ++u) {
+    const float wu = lane_of(w, u);
+    const f32x4 a = o + wu * v[u];
+    o = u < n_act ? a : o;
+  }
+  for (int c0 = kMergeBatch; c0 < n_act; c0 += kMergeBatch) {
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u)
+      v[u] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ((c0 + u) * nhq + hq) * HD * 4 + od,
+                                                        0, 0));
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const float wu = lane_of(w, c0 + u);
+      const f32x4 a = o + wu * v[u];
+      o = c0 + u < n_act ? a : o;
     }
   }
   if (d4 < H4) {
     const float inv = 1.0f / l;
-    *reinterpret_cast<float4 *>(args.out + (size_t)t * args.q_dim + hq * HD + 4 * d4) =
+    *reinterpret_cast<float4 *>(args.out + (size_t)t * q_dim + hq * HD + 4 * d4) =
         float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
   }
 }

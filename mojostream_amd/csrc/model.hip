@@ -297,6 +297,14 @@ static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipS
   a.asrc = AS_ROWS;
   a.rows = r;
   a.waves = waves;
+  if (a.M > 1 && a.M <= 4 && waves == 16 && a.K <= 8 * 2 * 64 * 8) {
+    // two to four rows: 8 waves, each row its own wave pair with the rows'
+    // loads in one batch (a 16-wave block takes the rows one after another;
+    // the demo model's Down at four rows: 1.165 -> 1.085 ms per harness step)
+    a.waves = 8;
+    if (gemv_lds_need(a) <= kLdsLimit) return launch_gemv_rec(a, st);
+    a.waves = waves;
+  }
   if (a.K <= 8 * 2 * 64 * waves && gemv_lds_need(a) <= kLdsLimit) return launch_gemv_rec(a, st);
   a.asrc = AS_QUANT;
   a.rows = RowSrc{};
