@@ -53,6 +53,23 @@ constexpr int kGemmLds = kStages * kStage;  // 60 KiB
 constexpr int kLoads = 5;                // direct loads per thread per K step
 
 typedef __attribute__((address_space(3))) void lds_void;
+
+// Panel pi of the GEMM's 1-3 weight segments (concatenated): its weights,
+// scale, first output column and whether it exists.  The candidates come in
+// as values: a lambda capturing them would keep them in private memory and
+// turn the block-uniform selects into an indexed scratch load.
+__device__ inline void seg_panel(int pi, int K, const uint8_t *w0, const uint8_t *w1,
+                                 const uint8_t *w2, float s0, float s1, float s2, int n0,
+                                 int n1, int n2, int c0, int c1, int c2, const uint8_t **w,
+                                 float *sc, int *col, bool *ok) {
+  const int si = pi < n0 ? 0 : (pi < n0 + n1 ? 1 : 2);
+  const int loc = pi - (si == 0 ? 0 : (si == 1 ? n0 : n0 + n1));
+  *ok = pi < n0 + n1 + n2;
+  const uint8_t *base = si == 0 ? w0 : (si == 1 ? w1 : w2);
+  *w = *ok ? base + (size_t)loc * K * 8 : w0;
+  *sc = si == 0 ? s0 : (si == 1 ? s1 : s2);
+  *col = (si == 0 ? c0 : (si == 1 ? c1 : c2)) + loc * 16;
+}
 typedef const __attribute__((address_space(1))) void gbl_void;
 
 // Exact limb combine of one output, minus the zero-point term z: each limb's
@@ -108,14 +125,8 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
       *sc = hf == 0 ? ss0 : ss1;
       *cl = cp * 16;
     } else {
-      const int pi = blockIdx.x * 8 + sl;
-      const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
-      const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
-      *ok = pi < sn0 + sn1 + sn2;
-      const uint8_t *base = si == 0 ? sw0 : (si == 1 ? sw1 : sw2);
-      *w = *ok ? base + (size_t)loc * K * 8 : sw0;
-      *sc = si == 0 ? ss0 : (si == 1 ? ss1 : ss2);
-      *cl = (si == 0 ? sc0 : (si == 1 ? sc1 : sc2)) + loc * 16;
+      seg_panel(blockIdx.x * 8 + sl, K, sw0, sw1, sw2, ss0, ss1, ss2, sn0, sn1, sn2, sc0, sc1,
+                sc2, w, sc, cl, ok);
     }
   };
   // the panels this wave computes: slots 4 wb .. 4 wb + 3
@@ -333,14 +344,17 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 // 4wc..4wc+3 (slots j < 4) and the up panels of the same groups (j >= 4), so
 // each output's gate and up values meet in one lane.
 //
-// PS = 16 panel slots per block, or 10 (wave tile 3 A tiles x 5 panels) for
-// launches whose 16-slot tiles leave a last round of blocks mostly empty: O
-// and Down at 2048 rows (N = 160 panels) make 1024 ten-slot tiles, two full
-// rounds, against 640 sixteen-slot ones.
+// PS = 16 panel slots per block, 20 (wave tile 3 A tiles x 10 panels) or 10
+// (3 x 5) for launches whose 16-slot tiles leave a last round of blocks
+// mostly empty: O and Down at 2048 rows (N = 160 panels) make 512
+// twenty-slot tiles, one full round at two blocks per CU, against 640
+// sixteen-slot ones (1.25 rounds).  The 20-slot tile also reads each A step
+// for 20 panels instead of 16 or 10.
 // ------------------------------------------------------------------------------
 constexpr int kGBM = 32;                     // activation rows per block
 constexpr int kGPan = 16;                    // panel slots per block (wide tile)
 constexpr int kGPanNarrow = 10;              // panel slots per block (narrow tile)
+constexpr int kGPanWide = 20;                // panel slots per block (20-slot tile)
 constexpr int kGStageA = kLimbs * kGBM * 128;  // 96 limb rows x 128 bytes
 constexpr int kGStages = 2;
 constexpr int kGNT = 256;                    // threads per block
@@ -350,7 +364,8 @@ constexpr int gemm_big_lds(int ps) { return kGStages * gemm_big_stage(ps); }
 
 template <int EPI, int PS>
 __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
-  static_assert(PS == kGPan || (PS == kGPanNarrow && EPI != EPI_SWIGLU), "panel slots");
+  static_assert(PS == kGPan || ((PS == kGPanNarrow || PS == kGPanWide) && EPI != EPI_SWIGLU),
+                "panel slots");
   constexpr int PW = PS / 2;                 // panel slots per wave
   constexpr int kGStage = gemm_big_stage(PS);
   extern __shared__ __align__(16) uint8_t lds[];
@@ -383,7 +398,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
   const int KG = K >> 7;
 
   // panel slot -> weights, scale, first column, valid (block-uniform selects)
-  auto slot = [&](int sl, const uint8_t **w, float *sc, int *col, bool *ok) {
+  auto slot = [=](int sl, const uint8_t **w, float *sc, int *col, bool *ok) {
     if constexpr (EPI == EPI_SWIGLU) {
       const int half = sl >> 3, cp = blockIdx.x * 8 + (sl & 7);
       *ok = cp < sn0;
@@ -391,14 +406,8 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
       *sc = half == 0 ? ss0 : ss1;
       *col = cp * 16;
     } else {
-      const int pi = blockIdx.x * PS + sl;
-      const int si = pi < sn0 ? 0 : (pi < sn0 + sn1 ? 1 : 2);
-      const int loc = pi - (si == 0 ? 0 : (si == 1 ? sn0 : sn0 + sn1));
-      *ok = pi < sn0 + sn1 + sn2;
-      const uint8_t *base = si == 0 ? sw0 : (si == 1 ? sw1 : sw2);
-      *w = *ok ? base + (size_t)loc * K * 8 : sw0;
-      *sc = si == 0 ? ss0 : (si == 1 ? ss1 : ss2);
-      *col = (si == 0 ? sc0 : (si == 1 ? sc1 : sc2)) + loc * 16;
+      seg_panel(blockIdx.x * PS + sl, K, sw0, sw1, sw2, ss0, ss1, ss2, sn0, sn1, sn2, sc0, sc1,
+                sc2, w, sc, col, ok);
     }
   };
   // the panel slot of this wave's accumulator column j
@@ -567,9 +576,13 @@ namespace {
 // exact partials meeting through a counter or in a second launch, was
 // slower: see the notes on the measured variants.)
 constexpr double kNarrowStepCost = 0.85;
+// the 20-slot tile's K step: its MFMA count, 1.25 of the 16-slot one (at 2048
+// rows O and Down make 512 twenty-slot tiles, one round: TTFT at 2048 tokens
+// 32.9 -> 32.4 ms)
+constexpr double kWideStepCost = 1.25;
 constexpr double kSmallStepCost = 0.8;
 
-// 0: the 32-row kernel; else the big tile's panel slots (16 or 10)
+// 0: the 32-row kernel; else the big tile's panel slots (16, 20 or 10)
 int gemm_pick(const GemmArgs &g, int np) {
   const bool swiglu = g.epi == EPI_SWIGLU;
   const long slots = 2L * (ctx().n_cu > 0 ? ctx().n_cu : 256);
@@ -580,8 +593,13 @@ int gemm_pick(const GemmArgs &g, int np) {
   const long small = (long)(swiglu ? (np / 2 + 2 * kWB - 1) / (2 * kWB)
                                    : (np + 4 * kWB - 1) / (4 * kWB)) *
                      ((g.M + kBM - 1) / kBM);
+  const long wide20 = (long)((np + kGPanWide - 1) / kGPanWide) * rows;
   int pick = kGPan;
   double cost = rounds(wide);
+  if (!swiglu && rounds(wide20) * kWideStepCost < cost) {
+    pick = kGPanWide;
+    cost = rounds(wide20) * kWideStepCost;
+  }
   if (!swiglu && rounds(narrow) * kNarrowStepCost < cost) {
     pick = kGPanNarrow;
     cost = rounds(narrow) * kNarrowStepCost;
@@ -683,6 +701,8 @@ int launch_gemm(const GemmArgs &g, hipStream_t st) {
   const int pick = gemm_pick(g, np);
   if (pick == kGPan) {
     launch_big<kGPan>(g, np, st);
+  } else if (pick == kGPanWide) {
+    launch_big<kGPanWide>(g, np, st);
   } else if (pick == kGPanNarrow) {
     launch_big<kGPanNarrow>(g, np, st);
   } else {
