@@ -688,10 +688,14 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
   // float4 LDS store each).  V (VK, head dim 256 and below): lanes take the
   // 16 keys of four dim quads, so the transposed stores of a wave fall in
   // different banks; with a wave over the dims of one key, lane l's V^T rows
-  // start 4 l * VP floats apart and each store instruction hits a few banks
-  // many times over.  At head dim 512 the V addresses of the key-fastest
-  // deal would spill registers, so V is dealt like K there.
+  // start 4 l * VP floats apart and each 4-byte store hits a few banks many
+  // times over.  At head dim 512 (the key-fastest deal's V addresses would
+  // spill registers) thread t takes a 4 x 4 block instead: keys 4 (t / (HD /
+  // 4)) .. + 3 of dim quad t % (HD / 4), four coalesced float4 loads, a
+  // transpose in registers and four float4 stores to V^T (rows 80 bytes
+  // apart: at most two lanes of a store phase share banks).
   constexpr bool VK = HD <= 256;
+  static_assert(VK || (NF == 4 && NT == 4 * (HD / 4)), "V blocks: 4 keys x 4 dims per thread");
   // (NT is a multiple of 16: with VK, a thread's V key is the same for every f)
   const int vkey = tid % 16;
   af32x4 kreg[NF], vreg[NF];
@@ -712,15 +716,27 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
         if (k < base) {
           const size_t o = (size_t)cache_slot(p, k) * p.kv_dim + h * HD + 4 * d4;
           kreg[f] = aldg<af32x4>(p.kc + o);
-          if (!VK) vreg[f] = aldg<af32x4>(p.vc + o);
         } else {
           const int rr = k - base;
           kreg[f] = aldg<af32x4>(kr + (size_t)rr * p.kv_dim + h * HD + 4 * d4);
-          if (!VK)
-            vreg[f] = aldg<af32x4>(p.qkv + (size_t)rr * p.ld + p.q_dim + p.kv_dim + h * HD + 4 * d4);
         }
       }
       if (VK && vrow) vreg[f] = aldg<af32x4>(vrow + 4 * (idx / 16));
+    }
+    if constexpr (!VK) {
+      // V block: keys k0 + 4 (tid / (HD / 4)) + r, dim quad tid % (HD / 4)
+      const int kq = tid / (HD / 4), d4 = tid % (HD / 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k = k0 + 4 * kq + r;
+        vreg[r] = af32x4{0.f, 0.f, 0.f, 0.f};
+        if (k <= khi)
+          vreg[r] = k < base
+                        ? aldg<af32x4>(p.vc + (size_t)cache_slot(p, k) * p.kv_dim + h * HD +
+                                       4 * d4)
+                        : aldg<af32x4>(p.qkv + (size_t)(k - base) * p.ld + p.q_dim +
+                                       p.kv_dim + h * HD + 4 * d4);
+      }
     }
   };
   auto tile_store = [&]() {
@@ -728,10 +744,18 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
     for (int f = 0; f < NF; ++f) {
       const int idx = tid + NT * f;
       const int key = idx / (HD / 4), d4 = idx % (HD / 4);
-      const int vr = VK ? vkey : key, vd4 = VK ? idx / 16 : d4;
       *reinterpret_cast<af32x4 *>(Ks + key * KP + 4 * d4) = kreg[f];
+      if constexpr (VK) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) VT[(4 * vd4 + c) * VP + vr] = vreg[f][c];
+        for (int c = 0; c < 4; ++c) VT[(4 * (idx / 16) + c) * VP + vkey] = vreg[f][c];
+      }
+    }
+    if constexpr (!VK) {
+      const int kq = tid / (HD / 4), d4 = tid % (HD / 4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<af32x4 *>(VT + (4 * d4 + c) * VP + 4 * kq) =
+            af32x4{vreg[0][c], vreg[1][c], vreg[2][c], vreg[3][c]};
     }
   };
 
