@@ -341,15 +341,17 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 // then fall in 16 different bank groups.
 //
 // EPI_SWIGLU: wave column wc holds the gate panels of column groups
-// 4wc..4wc+3 (slots j < 4) and the up panels of the same groups (j >= 4), so
-// each output's gate and up values meet in one lane.
+// CGW wc .. CGW wc + CGW - 1 (slots j < CGW, CGW = PS / 4) and the up panels
+// of the same groups (j >= CGW), so each output's gate and up values meet in
+// one lane.
 //
 // PS = 16 panel slots per block, 20 (wave tile 3 A tiles x 10 panels) or 10
 // (3 x 5) for launches whose 16-slot tiles leave a last round of blocks
 // mostly empty: O and Down at 2048 rows (N = 160 panels) make 512
 // twenty-slot tiles, one full round at two blocks per CU, against 640
 // sixteen-slot ones (1.25 rounds).  The 20-slot tile also reads each A step
-// for 20 panels instead of 16 or 10.
+// for 20 panels instead of 16 or 10.  For SwiGLU a block of PS slots holds
+// the gate and up panels of PS / 2 column groups, PS / 4 per wave column.
 // ------------------------------------------------------------------------------
 constexpr int kGBM = 32;                     // activation rows per block
 constexpr int kGPan = 16;                    // panel slots per block (wide tile)
@@ -364,9 +366,11 @@ constexpr int gemm_big_lds(int ps) { return kGStages * gemm_big_stage(ps); }
 
 template <int EPI, int PS>
 __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
-  static_assert(PS == kGPan || ((PS == kGPanNarrow || PS == kGPanWide) && EPI != EPI_SWIGLU),
+  static_assert(PS == kGPan || PS == kGPanWide || (PS == kGPanNarrow && EPI != EPI_SWIGLU),
                 "panel slots");
   constexpr int PW = PS / 2;                 // panel slots per wave
+  constexpr int CG = PS / 2;                 // SwiGLU: column groups per block
+  constexpr int CGW = CG / 2;                // SwiGLU: column groups per wave column
   constexpr int kGStage = gemm_big_stage(PS);
   extern __shared__ __align__(16) uint8_t lds[];
   const int M = launder(g.M), K = launder(g.K);
@@ -400,7 +404,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
   // panel slot -> weights, scale, first column, valid (block-uniform selects)
   auto slot = [=](int sl, const uint8_t **w, float *sc, int *col, bool *ok) {
     if constexpr (EPI == EPI_SWIGLU) {
-      const int half = sl >> 3, cp = blockIdx.x * 8 + (sl & 7);
+      const int half = sl / CG, cp = blockIdx.x * CG + sl % CG;
       *ok = cp < sn0;
       *w = (half == 0 ? sw0 : sw1) + (size_t)(*ok ? cp : 0) * K * 8;
       *sc = half == 0 ? ss0 : ss1;
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
   };
   // the panel slot of this wave's accumulator column j
   auto wslot = [&](int j) {
-    if constexpr (EPI == EPI_SWIGLU) return j < 4 ? 4 * wc + j : 8 + 4 * wc + (j - 4);
+    if constexpr (EPI == EPI_SWIGLU) return j < CGW ? CGW * wc + j : CG + CGW * wc + (j - CGW);
     else return PW * wc + j;
   };
   // this wave loads panel slots wave, wave + 4, .. (an invalid slot loads a
@@ -529,9 +533,9 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
       const int row = r0 + 16 * wr + 4 * rr + a;
       if (row >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < CGW; ++j) {
         if (!pv[j]) continue;
-        const float gt = value(a, j), up = value(a, j + 4);
+        const float gt = value(a, j), up = value(a, j + CGW);
         sw_out[(size_t)row * ldo_sw + col[j] + jc] = up * gt * (1.0f / (1.0f + expf(-gt)));
       }
     }
@@ -576,10 +580,12 @@ namespace {
 // exact partials meeting through a counter or in a second launch, was
 // slower: see the notes on the measured variants.)
 constexpr double kNarrowStepCost = 0.85;
-// the 20-slot tile's K step: its MFMA count, 1.25 of the 16-slot one (at 2048
-// rows O and Down make 512 twenty-slot tiles, one round: TTFT at 2048 tokens
-// 32.9 -> 32.4 ms)
-constexpr double kWideStepCost = 1.25;
+// the 20-slot tile's K step: 1.25 times the MFMAs of a 16-slot one, less the
+// A reads it saves (each A step serves 20 panels).  At 2048 rows O and Down
+// make 512 twenty-slot tiles, one round (TTFT at 2048 tokens 32.9 -> 32.4
+// ms), and Gate|Up 4096 tiles, 8 rounds against 10 (31.9 -> 31.4 ms; 512
+// tokens 10.5 -> 10.3 ms)
+constexpr double kWideStepCost = 1.2;
 constexpr double kSmallStepCost = 0.8;
 
 // 0: the 32-row kernel; else the big tile's panel slots (16, 20 or 10)
@@ -593,10 +599,12 @@ int gemm_pick(const GemmArgs &g, int np) {
   const long small = (long)(swiglu ? (np / 2 + 2 * kWB - 1) / (2 * kWB)
                                    : (np + 4 * kWB - 1) / (4 * kWB)) *
                      ((g.M + kBM - 1) / kBM);
-  const long wide20 = (long)((np + kGPanWide - 1) / kGPanWide) * rows;
+  const long wide20 =
+      (long)(swiglu ? (np / 2 + kGPanWide / 2 - 1) / (kGPanWide / 2)
+                    : (np + kGPanWide - 1) / kGPanWide) * rows;
   int pick = kGPan;
   double cost = rounds(wide);
-  if (!swiglu && rounds(wide20) * kWideStepCost < cost) {
+  if (rounds(wide20) * kWideStepCost < cost) {
     pick = kGPanWide;
     cost = rounds(wide20) * kWideStepCost;
   }
@@ -610,7 +618,7 @@ int gemm_pick(const GemmArgs &g, int np) {
 
 template <int PS>
 void launch_big(const GemmArgs &g, int np, hipStream_t st) {
-  const int gxb = g.epi == EPI_SWIGLU ? (np / 2 + 7) / 8 : (np + PS - 1) / PS;
+  const int gxb = g.epi == EPI_SWIGLU ? (np / 2 + PS / 2 - 1) / (PS / 2) : (np + PS - 1) / PS;
   const dim3 grid(gxb, gemm_row_pad(g.M) / kGBM);
   const size_t lds = gemm_big_lds(PS);
   switch (g.epi) {
@@ -620,7 +628,7 @@ void launch_big(const GemmArgs &g, int np, hipStream_t st) {
       break;
     case EPI_RESID: hipLaunchKernelGGL((k_gemm_big<EPI_RESID, PS>), grid, dim3(kGNT), lds, st, g); break;
     default:
-      if constexpr (PS == kGPan)
+      if constexpr (PS == kGPan || PS == kGPanWide)
         hipLaunchKernelGGL((k_gemm_big<EPI_SWIGLU, PS>), grid, dim3(kGNT), lds, st, g);
       break;
   }
