@@ -374,17 +374,18 @@ __device__ inline void row_finish(const RowSrc &r, int K, int m, bool writer,
   }
 }
 
-// One row per block of NT threads (K <= 16 NT).  LIMBS 3: the GEMM's planes.
-template <bool GAM, int NT, int LIMBS = 4>
+// One row per block of NT threads, NG groups of 8 values per thread
+// (K <= 8 NG NT).  LIMBS 3: the GEMM's planes.
+template <bool GAM, int NT, int LIMBS = 4, int NG = 2>
 __global__ __launch_bounds__(NT) void k_quant_rows(RowSrc r, int K, QuantRows q) {
   __shared__ __align__(8) float sh[32];  // also 16 doubles (row sum)
-  RowRegs<NT, 2, GAM> R;
+  RowRegs<NT, NG, GAM> R;
   const int m = blockIdx.x;
-  row_load<NT, 2, GAM>(r, K, m, R);
+  row_load<NT, NG, GAM>(r, K, m, R);
   int s;
   double xs;
-  row_finish<NT, 2, GAM, true, LIMBS>(r, K, m, true, R, q.limbs, K, sh, &s, &xs, true,
-                                      q.plane_rows);
+  row_finish<NT, NG, GAM, true, LIMBS>(r, K, m, true, R, q.limbs, K, sh, &s, &xs, true,
+                                       q.plane_rows);
   if (threadIdx.x == 0) {
     q.shift[m] = s;
     q.xsum[m] = (int64_t)xs;
@@ -422,6 +423,13 @@ int launch_quant_rows3(const RowSrc &r, int M, int K, const QuantRows &q, hipStr
       hipLaunchKernelGGL((k_quant_rows<true, 256, 3>), dim3(M), dim3(256), 0, st, r, K, q);
     else
       hipLaunchKernelGGL((k_quant_rows<false, 256, 3>), dim3(M), dim3(256), 0, st, r, K, q);
+  } else if (K <= 40 * 256 && M >= 64 && !r.gamma && !r.norm) {
+    // long rows without a norm (the Down input, K = 10240): 256 threads of
+    // five groups, so that more rows of a prompt chunk are resident at once
+    // (1024-thread blocks fit two per CU: 2048 rows took four rounds).  Only
+    // the maximum and the exact sum of X are reduced, so the limbs, shift
+    // and sum equal those of the 1024-thread kernel.
+    hipLaunchKernelGGL((k_quant_rows<false, 256, 3, 5>), dim3(M), dim3(256), 0, st, r, K, q);
   } else if (r.gamma) {
     hipLaunchKernelGGL((k_quant_rows<true, 1024, 3>), dim3(M), dim3(1024), 0, st, r, K, q);
   } else {
