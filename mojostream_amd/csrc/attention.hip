@@ -692,8 +692,10 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
   // times over.  At head dim 512 (the key-fastest deal's V addresses would
   // spill registers) thread t takes a 4 x 4 block instead: keys 4 (t / (HD /
   // 4)) .. + 3 of dim quad t % (HD / 4), four coalesced float4 loads, a
-  // transpose in registers and four float4 stores to V^T (rows 80 bytes
-  // apart: at most two lanes of a store phase share banks).
+  // transpose in registers and four float4 stores to V^T.  The four-key
+  // groups of V^T row r sit in slot group ^ ((r >> 4) & 3): the 16 lanes of
+  // a store phase (rows 4 d4 + c, 80 bytes apart) then cover 16 distinct
+  // bank quads, and a read of dims 16u .. 16u + 15 uses one rotation.
   constexpr bool VK = HD <= 256;
   static_assert(VK || (NF == 4 && NT == 4 * (HD / 4)), "V blocks: 4 keys x 4 dims per thread");
   // (NT is a multiple of 16: with VK, a thread's V key is the same for every f)
@@ -754,7 +756,7 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
       const int kq = tid / (HD / 4), d4 = tid % (HD / 4);
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<af32x4 *>(VT + (4 * d4 + c) * VP + 4 * kq) =
+        *reinterpret_cast<af32x4 *>(VT + (4 * d4 + c) * VP + 4 * (kq ^ ((d4 >> 2) & 3))) =
             af32x4{vreg[0][c], vreg[1][c], vreg[2][c], vreg[3][c]};
     }
   };
@@ -821,8 +823,10 @@ __global__ __launch_bounds__(256 * DS) void k_flash_prefill(AttnArgs args, const
     const af32x4 pa = *reinterpret_cast<const af32x4 *>(Pw + li * PP + 4 * lk);
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
+      // (head dim 512: the row's key groups are rotated by ((row >> 4) & 3))
+      const int vs = VK ? lk : lk ^ (((d0 >> 4) + u) & 3);
       const af32x4 vt =
-          *reinterpret_cast<const af32x4 *>(VT + (d0 + 16 * u + li) * VP + 4 * lk);
+          *reinterpret_cast<const af32x4 *>(VT + (d0 + 16 * u + li) * VP + 4 * vs);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         o[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[r], vt[r], o[u], 0, 0, 0);
