@@ -26,8 +26,8 @@
 // straight into LDS (global_load_lds: each wave instruction fills 1 KiB), in
 // a ring of three steps; loads run two steps ahead of the MFMAs, which a
 // step's MFMA time alone does not cover.  A limb rows are stored without
-// padding, chunk c of row r at chunk position c ^ ((r >> 1) & 7), so the 16
-// rows one fragment read touches fall in 16 different bank groups.
+// padding, chunk c of row r at chunk position c ^ a_swz(r), so the rows one
+// fragment read touches fall in different bank groups.
 //
 // EPI_SWIGLU: the first half of the wave columns computes gate panels, the
 // second half the up panels of the same columns; the gate values pass through
@@ -53,6 +53,13 @@ constexpr int kGemmLds = kStages * kStage;  // 60 KiB
 constexpr int kLoads = 5;                // direct loads per thread per K step
 
 typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS position of 16-byte chunk c of A limb row r: c ^ a_swz(r).  The rows
+// one A fragment read touches are r0 + 0..15; a 16-byte read goes in phases
+// of 8 lanes over 32 banks of 4 bytes (128 bytes per phase), so rows
+// r .. r + 7 must take 8 different chunk positions (r & 7), and rows r and
+// r + 8 of a 16-lane phase a different one again (the bit r >> 3).
+__device__ inline int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // Panel pi of the GEMM's 1-3 weight segments (concatenated): its weights,
 // scale, first output column and whether it exists.  The candidates come in
@@ -152,14 +159,14 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
   // A: a stage holds limb rows 32l + m (limb l of block row m); this wave
   // fills LDS blocks 3 wave + i (stage rows 8q .. 8q + 7); lane l writes row
   // 8q + l / 8 at chunk position l % 8, which holds chunk (l % 8) ^
-  // ((row >> 1) & 7) of the row, so the 16 rows one fragment read touches
-  // fall in 16 different bank groups
+  // a_swz(row) of the row, so the rows one fragment read touches fall in
+  // different bank groups
   const int pr = launder(g.a.plane_rows);
   const int8_t *asrc[kLimbs];
 #pragma unroll
   for (int i = 0; i < kLimbs; ++i) {
     const int row = 8 * (kLimbs * wave + i) + (lane >> 3);
-    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    const int c = (lane & 7) ^ a_swz(row);
     asrc[i] = limbs + ((size_t)(row >> 5) * pr + r0 + (row & 31)) * K + c * 16;
   }
   // K step G into stage stg: global memory straight into LDS
@@ -184,7 +191,7 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
     for (int j = 0; j < 4; ++j) acc[a][j] = v4i{0, 0, 0, 0};
 
   const int li = lane & 15, lg = lane >> 4;
-  const int swz = (li >> 1) & 7;  // (row >> 1) & 7 for every row this lane reads
+  const int swz = a_swz(li);  // a_swz(row) for every row this lane reads
   auto compute = [&](int stg) {
     const uint8_t *sa = lds + stg * kStage;
     u32x4 braw[4];
@@ -337,8 +344,8 @@ __global__ __launch_bounds__(kNT) void k_gemm(GemmArgs g) {
 // overlap the other's MFMAs (with one 8-wave block per CU, the per-step
 // barrier and the epilogue left the MFMA units idle for a third of the time).
 // A limb rows are stored without padding, the 16-byte chunk c of row r at
-// chunk position c ^ ((r >> 1) & 7): the 16 rows one A fragment read touches
-// then fall in 16 different bank groups.
+// chunk position c ^ a_swz(r): the rows one A fragment read touches then fall
+// in different bank groups.
 //
 // EPI_SWIGLU: wave column wc holds the gate panels of column groups
 // CGW wc .. CGW wc + CGW - 1 (slots j < CGW, CGW = PS / 4) and the up panels
@@ -433,13 +440,13 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
   // A: a stage holds limb rows 32l + m (limb l of block row m); this wave
   // fills LDS blocks 3 wave + i (stage rows 8q .. 8q + 7); lane l writes row
   // 8q + l / 8 at chunk position l % 8, which holds chunk (l % 8) ^
-  // ((row >> 1) & 7) of the row
+  // a_swz(row) of the row
   const int pr = launder(g.a.plane_rows);
   const int8_t *asrc[kLimbs];
 #pragma unroll
   for (int i = 0; i < kLimbs; ++i) {
     const int row = 8 * (kLimbs * wave + i) + (lane >> 3);
-    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    const int c = (lane & 7) ^ a_swz(row);
     asrc[i] = limbs + ((size_t)(row >> 5) * pr + r0 + (row & 31)) * K + c * 16;
   }
   auto issue = [&](int G, int stg) {
@@ -464,7 +471,7 @@ __global__ __launch_bounds__(kGNT, 2) void k_gemm_big(GemmArgs g) {
     for (int j = 0; j < PW; ++j) acc[a][j] = v4i{0, 0, 0, 0};
 
   const int li = lane & 15, lg = lane >> 4;
-  const int swz = (li >> 1) & 7;  // (row >> 1) & 7 for every row this lane reads
+  const int swz = a_swz(li);  // a_swz(row) for every row this lane reads
   auto compute = [&](int stg) {
     const uint8_t *sa = lds + stg * kGStage;
     const uint8_t *sb = sa + kGStageA + lane * 16;
