@@ -594,6 +594,43 @@ __device__ inline float row16_sum(float v) {
   return v + adpp<0x140>(v);
 }
 
+// The same on float4 units (the rotated half of a head a multiple of 4):
+// unit u of a head is four rotation pairs (dims i .. i + 3 and half + i ..,
+// both rotated from one float4 of each half and of the tables) or four dims
+// past the rotary ones (copied).  Same arithmetic per value as rope_apply.
+__global__ __launch_bounds__(256) void k_rope_rows4(AttnArgs args, float *qr, float *kr,
+                                                    int hd) {
+  const AttnP p = load_params(args);
+  const int r = blockIdx.x;
+  const int pos = aldg<int32_t>(p.pos) + r;
+  const int rot = p.apply_rope ? p.rot : 0, half = rot >> 1;
+  const int pq = half >> 2, per = pq + ((hd - rot) >> 2);  // units per head
+  const int nh = p.n_heads + p.n_kv;
+  const float *row = p.qkv + (size_t)r * p.ld;
+  const float *ct = p.cos_t + (size_t)pos * half, *st = p.sin_t + (size_t)pos * half;
+  for (int u = threadIdx.x; u < nh * per; u += 256) {
+    const int head = u / per, j = u - head * per;
+    const bool isq = head < p.n_heads;
+    const int hk = isq ? head : head - p.n_heads;
+    const float *src = row + (isq ? 0 : p.q_dim) + hk * hd;
+    float *dst = isq ? qr + (size_t)r * p.q_dim + hk * hd : kr + (size_t)r * p.kv_dim + hk * hd;
+    if (j < pq) {
+      const int i = 4 * j;
+      const float4 xl = aldg<float4>(src + i), xh = aldg<float4>(src + half + i);
+      const float4 c = aldg<float4>(ct + i), sn = aldg<float4>(st + i);
+      *reinterpret_cast<float4 *>(dst + i) =
+          float4{xl.x * c.x - xh.x * sn.x, xl.y * c.y - xh.y * sn.y, xl.z * c.z - xh.z * sn.z,
+                 xl.w * c.w - xh.w * sn.w};
+      *reinterpret_cast<float4 *>(dst + half + i) =
+          float4{xl.x * sn.x + xh.x * c.x, xl.y * sn.y + xh.y * c.y, xl.z * sn.z + xh.z * c.z,
+                 xl.w * sn.w + xh.w * c.w};
+    } else {
+      const int d = rot + 4 * (j - pq);
+      *reinterpret_cast<float4 *>(dst + d) = aldg<float4>(src + d);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_rope_rows(AttnArgs args, float *qr, float *kr, int hd) {
   const AttnP p = load_params(args);
   const int r = blockIdx.x;
@@ -1000,7 +1037,11 @@ int launch_attention_prefill(const AttnArgs &a, float *qr, float *kr, float *fpa
   const size_t need = flash_part_floats(a);
   if (need == 0 || !fpart || fpart_floats < need) fs.maxs = 1;  // no split
   fs.part = fpart;
-  hipLaunchKernelGGL(k_rope_rows, dim3(a.T), dim3(256), 0, st, a, qr, kr, a.hd);
+  if (a.hd % 4 == 0 && (!a.apply_rope || a.rot % 8 == 0) && a.ld % 4 == 0 && a.q_dim % 4 == 0 &&
+      a.kv_dim % 4 == 0)
+    hipLaunchKernelGGL(k_rope_rows4, dim3(a.T), dim3(256), 0, st, a, qr, kr, a.hd);
+  else
+    hipLaunchKernelGGL(k_rope_rows, dim3(a.T), dim3(256), 0, st, a, qr, kr, a.hd);
   const dim3 grid(fs.maxs * fs.n_rt * a.n_kv);
 #define MS_FLASH(HDV, DSV)                                                                \
   hipLaunchKernelGGL((k_flash_prefill<HDV, DSV>), grid, dim3(256 * DSV),                   \
