@@ -1353,42 +1353,82 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
 
 // Greedy id per row from the per-block maxima; blocks are visited in increasing
 // column order and ties keep the lowest index (lm_head.mojo:224-230).
+// (value, index) argmax step with the partner lane of DPP control CTRL: the
+// larger value, the lower index on ties (the greedy branch's first maximum)
+template <int CTRL>
+__device__ inline void argmax_dpp(float &v, int &i) {
+  const float pv = dpp_f<CTRL>(v);
+  const int pi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
+  if (pv > v || (pv == v && pi < i)) {
+    v = pv;
+    i = pi;
+  }
+}
+
+// Final argmax over the head's per-block maxima, one pass for all rows: each
+// thread scans its blocks for every row (M <= kFinRows per pass), each wave
+// reduces its lanes with DPP row steps and readlane, and thread m combines
+// the 16 waves' results of row m from LDS.  Then the state updates.
+constexpr int kFinRows = 4;
 __global__ __launch_bounds__(1024) void k_argmax_fin(ArgmaxFin f) {
-  __shared__ float sv[1024];
-  __shared__ int si[1024];
-  for (int m = 0; m < f.M; ++m) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    // ids chosen elsewhere (the sampler): only the state updates below
-    const int nb = f.ids_in ? 0 : f.n_blocks;
-    if (f.ids_in && threadIdx.x == 0) {
-      bv = 0.f;
-      bi = f.ids_in[m];
+  __shared__ float sv[kFinRows][16];
+  __shared__ int si[kFinRows][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // ids chosen elsewhere (the sampler): only the state updates below
+  const int nb = f.ids_in ? 0 : f.n_blocks;
+  for (int m0 = 0; m0 < f.M; m0 += kFinRows) {
+    float bv[kFinRows];
+    int bi[kFinRows];
+#pragma unroll
+    for (int r = 0; r < kFinRows; ++r) {
+      bv[r] = -INFINITY;
+      bi[r] = 0x7fffffff;
     }
-    for (int b = threadIdx.x; b < nb; b += 1024) {
-      const float v = f.arg_val[(size_t)b * f.M + m];
-      const int idx = f.arg_idx[(size_t)b * f.M + m];
-      if (v > bv || (v == bv && idx < bi)) {
-        bv = v;
-        bi = idx;
-      }
-    }
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int o = 512; o > 0; o >>= 1) {
-      if ((int)threadIdx.x < o) {
-        const float v = sv[threadIdx.x + o];
-        const int idx = si[threadIdx.x + o];
-        if (v > sv[threadIdx.x] || (v == sv[threadIdx.x] && idx < si[threadIdx.x])) {
-          sv[threadIdx.x] = v;
-          si[threadIdx.x] = idx;
+    for (int b = threadIdx.x; b < nb; b += 1024)
+#pragma unroll
+      for (int r = 0; r < kFinRows; ++r) {
+        if (m0 + r >= f.M) break;
+        const float v = f.arg_val[(size_t)b * f.M + m0 + r];
+        const int idx = f.arg_idx[(size_t)b * f.M + m0 + r];
+        if (v > bv[r] || (v == bv[r] && idx < bi[r])) {
+          bv[r] = v;
+          bi[r] = idx;
         }
       }
-      __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kFinRows; ++r) {
+      argmax_dpp<0xB1>(bv[r], bi[r]);   // quad_perm [1,0,3,2]
+      argmax_dpp<0x4E>(bv[r], bi[r]);   // quad_perm [2,3,0,1]
+      argmax_dpp<0x141>(bv[r], bi[r]);  // row_half_mirror
+      argmax_dpp<0x140>(bv[r], bi[r]);  // row_mirror
+      float v = lane_f(bv[r], 0);
+      int i = __builtin_amdgcn_readlane(bi[r], 0);
+#pragma unroll
+      for (int q = 16; q < 64; q += 16) {
+        const float qv = lane_f(bv[r], q);
+        const int qi = __builtin_amdgcn_readlane(bi[r], q);
+        if (qv > v || (qv == v && qi < i)) {
+          v = qv;
+          i = qi;
+        }
+      }
+      if (lane == 0) {
+        sv[r][w] = v;
+        si[r][w] = i;
+      }
     }
-    if (threadIdx.x == 0) {
-      const int id = si[0];
+    __syncthreads();
+    const int r = threadIdx.x;
+    if (r < kFinRows && m0 + r < f.M) {
+      const int m = m0 + r;
+      float v = sv[r][0];
+      int id = si[r][0];
+      for (int q = 1; q < 16; ++q)
+        if (sv[r][q] > v || (sv[r][q] == v && si[r][q] < id)) {
+          v = sv[r][q];
+          id = si[r][q];
+        }
+      if (f.ids_in) id = f.ids_in[m];
       if (f.ids_out) f.ids_out[m] = id;
       if (f.tok_state) f.tok_state[m] = id;
       if (f.pos_state) f.pos_state[m] += 1;
