@@ -294,6 +294,19 @@ static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipS
     if (int rc = launch_quant_rows3(r, a.M, a.K, g.a, st)) return rc;
     return launch_gemm(g, st);
   }
+  if (a.M <= kWaveRowsMax && waves == 16 && a.epi == EPI_RESID && a.P == 1 &&
+      a.K == 16 * 5 * kSuperK && !r.gamma && !r.x_out && !r.y_out) {
+    // one to four rows of the long residual projection (Down, K = 10240):
+    // per-wave slices quantized one super-tile at a time (the rows' limbs do
+    // not fit in LDS); the same limbs as the one-row per-wave GEMV, so a row
+    // gives the same result in a call of any row count.  (It replaced a
+    // quantization launch plus a GEMV reading the limbs from memory.)
+    GemvArgs w = a;
+    w.asrc = AS_WSTREAM;
+    w.rows = r;
+    w.waves = 16;
+    return launch_gemv_rec(w, st);
+  }
   a.asrc = AS_ROWS;
   a.rows = r;
   a.waves = waves;

@@ -35,6 +35,10 @@ enum GemvASource {
                  // K slice of every row with its own shift per row (no
                  // block-wide prologue); a row's RMSNorm factor is applied in
                  // the epilogue
+  AS_WSTREAM = 4,  // AS_WAVES with the same slices, shifts and limbs, but each
+                   // wave quantizes one 128-value super-tile of its rows at a
+                   // time into a wave-private LDS buffer just before that
+                   // tile's MFMAs (rows whose limbs would not fit in LDS)
 };
 
 // AS_ATTN: the chunk partials of one decode row (layout in attention.h:

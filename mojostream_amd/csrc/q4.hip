@@ -111,6 +111,12 @@ __device__ inline float row_sum16(float v) {
   v += dpp_f<0x140>(v);  // row_mirror
   return v;
 }
+__device__ inline float row_max16(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  return fmaxf(v, dpp_f<0x140>(v));
+}
 __device__ inline float wave_sum(float v) {
   v = row_sum16(v);
   return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
@@ -872,6 +878,60 @@ __device__ inline double lanes_sum_d(double v) {
   return v;
 }
 
+// AS_WSTREAM: wave-private limb buffer, one super-tile of 4 MR limb rows
+// (128 bytes each, 16 bytes of padding against bank conflicts).
+constexpr int kWsLd = 144;
+
+// AS_WSTREAM prologue of wave `wave` in a block of W waves (MR = 4 rows): the
+// wave's slice of each row, K values [128 TPW wave, 128 TPW (wave + 1)) as in
+// AS_WAVES, dealt so that lane l holds row l / 16, the 8-value group l % 16
+// of every super-tile u (values 128 u + 8 (l % 16) ..).  A row's values then
+// sit in one 16-lane DPP row: its maximum |y| and sum of y^2 are row16
+// reductions, and every lane quantizes one group per super-tile.  Rows past
+// M read zeros (range-checked loads).  The same maximum over the same values
+// as wave_rows_quant, so the same shift, limbs and integer sums (the sum of
+// squares, used by norm rows only, adds in another order).  Returns the
+// lane's row shift; ys keeps y for the per-tile quantization.
+template <int TPW, int W, class KW>
+__device__ inline int wave_stream_load(const RowSrc &rs, int M, int32_t *row_s, float *ssw,
+                                       float (&ys)[TPW][8], int wave, int lane, KW kw) {
+  const int m = lane >> 4, j = lane & 15;
+  const int k0 = wave * TPW * 128;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(rs.x), 0, (uint32_t)(M * rs.ld * 4), 0x00020000);
+  const uint32_t base = (uint32_t)((m * rs.ld + k0 + 8 * j) * 4);
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const f32x4 a = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, base + u * 512, 0, 0));
+    const f32x4 b = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, base + u * 512 + 16, 0, 0));
+    ys[u][0] = a.x; ys[u][1] = a.y; ys[u][2] = a.z; ys[u][3] = a.w;
+    ys[u][4] = b.x; ys[u][5] = b.y; ys[u][6] = b.z; ys[u][7] = b.w;
+  }
+  asm volatile("" ::"v"(ys[0][0]), "v"(ys[TPW - 1][7]) : "memory");
+  kw();
+  float mx = 0.f, ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < TPW; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = ys[u][e] * rs.pre_scale;
+      ys[u][e] = y;
+      ss += y * y;
+      mx = fmaxf(mx, fabsf(y));
+    }
+  mx = row_max16(mx);
+  ss = row_sum16(ss);
+  const int s = row_shift(mx);
+  if (j == 0) {
+    row_s[m * W + wave] = s;
+    ssw[m * W + wave] = ss;
+  }
+  return s;
+}
+
 // C: 16-row MFMA groups (4 limb rows per activation row: M <= 4C).
 // P: panels per block.  AS: GemvASource.  W: waves per block.  EPI: epilogue.
 // RP: activation rows whose loads the AS_ROWS prologue issues at once
@@ -890,13 +950,15 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   constexpr int NT = 64 * W;
   // AS_ATTN: the head's super-tiles, one batch
   // (AS_WAVES: the wave's RP super-tiles, one batch)
+  constexpr bool WS = AS == AS_WSTREAM;
   constexpr int U = AS == AS_ATTN    ? attn_hd(RP) / 128
-                    : AS == AS_WAVES ? waves_tpw(RP)
+                    : (AS == AS_WAVES || WS) ? waves_tpw(RP)
                                      : gemv_batch<C, P, AS, W>();
   // rows a WAVE_K epilogue finishes (AS_ATTN: one)
-  constexpr int MR = AS == AS_WAVES ? waves_rows(RP) : 1;
+  constexpr int MR = (AS == AS_WAVES || WS) ? waves_rows(RP) : 1;
   constexpr int NSL = AS == AS_WAVES ? waves_nsl(RP) : 1;
-  constexpr bool WAVE_K = AS == AS_ATTN || AS == AS_WAVES;  // contiguous K per wave
+  constexpr bool WAVE_K = AS == AS_ATTN || AS == AS_WAVES || WS;  // contiguous K per wave
+  static_assert(!WS || MR == 4, "streamed slices: four rows (lane l holds row l / 16)");
   // wave-uniform in a scalar register: tile predicates below are then scalar
   // branches, and loads behind them need no merge (and no wait) at the join
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -942,7 +1004,7 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   }
   RowSrc rs{};
   QuantRows qr{};
-  if (AS == AS_ROWS || AS == AS_WAVES) {
+  if (AS == AS_ROWS || AS == AS_WAVES || WS) {
     rs.x = launder(a.rows.x);
     rs.ld = launder(a.rows.ld);
     rs.pre_scale = launder(a.rows.pre_scale);
@@ -998,6 +1060,8 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   float pf_cs[2];  // PF: cos, sin at the position (block 0)
   v4i af[AS == AS_QUANT ? U : 1][C][2];
   float yv[MR][NSL][8];  // AS_WAVES: the wave's y values (for the normalized rows)
+  float ys[WS ? U : 1][8];  // AS_WSTREAM: the lane's group of each super-tile
+  int ws_s = 0;             // AS_WSTREAM: the lane's row shift
   // Loads of super-tiles u0..u1-1 of batch bt; tiles past the end of K are
   // not loaded (their slots stay zero and are never consumed).
   auto tile = [&](int bt, int u) {
@@ -1085,6 +1149,11 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
   } else if constexpr (AS == AS_ATTN) {
     attn_merge_quant<W, attn_hd(RP), attn_nj(RP)>(a.at, limbs, ldl, row_s, wave, lane,
                                                    [&] { issue(0); });
+  } else if constexpr (WS) {
+    constexpr int kEarlyW = (4 / P) < 1 ? 1 : ((4 / P) < U ? (4 / P) : U);
+    ws_s = wave_stream_load<U, W>(rs, M, row_s, sh, ys, wave, lane,
+                                  [&] { issue_part(0, 0, kEarlyW); });
+    if constexpr (kEarlyW < U) issue_part(0, kEarlyW, U);
   } else if constexpr (AS == AS_WAVES) {
     constexpr int kEarlyW = (4 / P) < 1 ? 1 : ((4 / P) < U ? (4 / P) : U);
     wave_rows_quant<U, MR, W>(rs, M, limbs, ldl, row_s, sh, yv, wave, lane,
@@ -1130,6 +1199,19 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
     for (int u = 0; u < U; ++u) {
       const int Gu = tile(bt, u);
       if (tile_on(bt, u)) {
+        // AS_WSTREAM: this super-tile's limbs, each lane quantizing its group
+        // of row lane / 16 into the wave's buffer (read back below)
+        int8_t *wb = limbs + (size_t)wave * 4 * MR * kWsLd;
+        if constexpr (WS) {
+          uint32_t lo[4], hi[4];
+          quant8<false>(ys[u], ldexpf(1.0f, ws_s), lo, hi);
+          const int pos = limb_pos8(8 * (lane & 15));
+#pragma unroll
+          for (int l = 0; l < 4; ++l)
+            *reinterpret_cast<uint2 *>(wb + (size_t)(4 * (lane >> 4) + l) * kWsLd + pos) =
+                uint2{lo[l], hi[l]};
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
         v4i al[C][2];
         if constexpr (AS == AS_ROWS || WAVE_K) {
 #pragma unroll
@@ -1137,7 +1219,8 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
             al[c][0] = v4i{0, 0, 0, 0};
             al[c][1] = v4i{0, 0, 0, 0};
             if (a_on[c]) {
-              const int8_t *ar = limbs + (size_t)(16 * c + i) * ldl + Gu * 128 + 32 * g;
+              const int8_t *ar = WS ? wb + (size_t)(16 * c + i) * kWsLd + 32 * g
+                                    : limbs + (size_t)(16 * c + i) * ldl + Gu * 128 + 32 * g;
               al[c][0] = *reinterpret_cast<const v4i *>(ar);
               al[c][1] = *reinterpret_cast<const v4i *>(ar + 16);
             }
@@ -1216,7 +1299,7 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
       // RMSNorm of the row (rmsnorm_inplace kernels.mojo:474-489) as a factor
       // on the products: y . W = inv (x . W)
       inv[m] = 1.0f;
-      if (AS == AS_WAVES && rs.norm) {
+      if ((AS == AS_WAVES || WS) && rs.norm) {
         float ssum = 0.f;
 #pragma unroll
         for (int u = 0; u < W; ++u) ssum += sh[m * W + u];
@@ -1451,6 +1534,8 @@ size_t gemv_lds_need(const GemvArgs &a) {
   size_t b = gemv_lds_fixed(a.waves, a.P, C, a.M);
   if (a.asrc == AS_ROWS || a.asrc == AS_ATTN || a.asrc == AS_WAVES)
     b += (size_t)4 * a.M * gemv_ldl(a.K);
+  else if (a.asrc == AS_WSTREAM)
+    b += (size_t)a.waves * 4 * kWaveRowsMax * kWsLd;
   return b;
 }
 
@@ -1475,7 +1560,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
   MS_CHECK_ARG(a.M >= 1 && a.M <= kGemvMaxM, "GEMV: 1 <= M <= 16");
   MS_CHECK_ARG(a.K >= kSuperK && a.K % kSuperK == 0, "GEMV: K % 128 != 0");
   MS_CHECK_ARG(a.asrc == AS_ROWS || a.asrc == AS_QUANT || a.asrc == AS_ATTN ||
-                   a.asrc == AS_WAVES,
+                   a.asrc == AS_WAVES || a.asrc == AS_WSTREAM,
                "GEMV: bad activation source");
   MS_CHECK_ARG(a.nseg >= 1 && a.nseg <= 3, "GEMV: 1 to 3 segments");
   MS_CHECK_ARG(a.epi != EPI_RESID || (a.resid && a.out), "GEMV: residual epilogue needs rows");
@@ -1494,6 +1579,11 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
                  "GEMV: per-wave rows: at most 4 rows, K = waves * tpw * 128 with tpw 1, 2, "
                  "4 or 5, and store or accumulate (4 or 8 waves), SwiGLU (4 waves) or "
                  "residual (8 or 16 waves)");
+  } else if (a.asrc == AS_WSTREAM) {
+    MS_CHECK_ARG(a.M <= kWaveRowsMax && a.rows.x && a.rows.ld >= a.K && !a.rows.gamma &&
+                     !a.rows.x_out && !a.rows.y_out && a.epi == EPI_RESID && a.P == 1 &&
+                     a.waves == 16 && a.K == 16 * 5 * kSuperK,
+                 "GEMV: streamed per-wave rows: at most 4 rows, residual, 16 waves, K = 10240");
   } else if (a.asrc == AS_ATTN) {
     MS_CHECK_ARG(a.M == 1 && a.P == 1 && a.waves == 8 && a.epi == EPI_RESID,
                  "GEMV: attention source: one row, one panel per block, 8 waves, residual");
@@ -1578,6 +1668,10 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     MS_GEMV_W(EPI_ACCUMULATE, 1, 8, 4)
 #undef MS_GEMV_W
     MS_CHECK_ARG(ok, "GEMV: per-wave rows: no instantiation for this shape");
+  }
+  if (!ok && a.asrc == AS_WSTREAM) {
+    MS_GEMV_L(1, EPI_RESID, 1, AS_WSTREAM, 16, 10 * kWaveRowsMax + 5);
+    ok = true;
   }
   if (!ok && a.asrc == AS_ATTN) {
     // the row-prologue template slot carries the head dim and the load pairs
