@@ -294,19 +294,6 @@ static int launch_proj(ms_model *m, GemvArgs a, const RowSrc &r, int waves, hipS
     if (int rc = launch_quant_rows3(r, a.M, a.K, g.a, st)) return rc;
     return launch_gemm(g, st);
   }
-  if (a.M <= kWaveRowsMax && waves == 16 && a.epi == EPI_RESID && a.P == 1 &&
-      a.K == 16 * 5 * kSuperK && !r.gamma && !r.x_out && !r.y_out) {
-    // one to four rows of the long residual projection (Down, K = 10240):
-    // per-wave slices quantized one super-tile at a time (the rows' limbs do
-    // not fit in LDS); the same limbs as the one-row per-wave GEMV, so a row
-    // gives the same result in a call of any row count.  (It replaced a
-    // quantization launch plus a GEMV reading the limbs from memory.)
-    GemvArgs w = a;
-    w.asrc = AS_WSTREAM;
-    w.rows = r;
-    w.waves = 16;
-    return launch_gemv_rec(w, st);
-  }
   a.asrc = AS_ROWS;
   a.rows = r;
   a.waves = waves;
@@ -338,6 +325,22 @@ static int launch_proj_row(ms_model *m, const RunCfg &rc, GemvArgs a, const RowS
   if (rc.one_row && a.M == 1 && !r.gamma && !r.x_out) {
     GemvArgs w = a;
     w.asrc = AS_WAVES;
+    w.rows = r;
+    w.waves = waves_row;
+    if (wave_shape_ok(w) && gemv_lds_need(w) <= kLdsLimit) return launch_gemv_rec(w, st);
+  }
+  // One to four rows of Q|K|V, O and Down: per-wave slices quantized one
+  // super-tile at a time (AS_WSTREAM; the same limbs as the one-row per-wave
+  // GEMV).  Measured at batch 4 against the block-wide row prologue (and for
+  // Down against a quantization launch plus a GEMV reading limbs from
+  // memory): Down 2,048 -> 2,255 tok/s, then Q|K|V and O 2,358; the demo
+  // harness step (four rows) 1.07 -> 1.00 ms.  Gate|Up keeps the block-wide
+  // prologue (2,215 against 2,260 tok/s streamed).  Down of the demo model
+  // (K = 4096) keeps its 8-wave row prologue.
+  if (a.M <= kWaveRowsMax && !r.gamma && !r.x_out && a.epi != EPI_SWIGLU &&
+      (waves_row != 16 || a.K == 16 * 5 * kSuperK)) {
+    GemvArgs w = a;
+    w.asrc = AS_WSTREAM;
     w.rows = r;
     w.waves = waves_row;
     if (wave_shape_ok(w) && gemv_lds_need(w) <= kLdsLimit) return launch_gemv_rec(w, st);

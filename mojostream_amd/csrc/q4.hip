@@ -1351,6 +1351,24 @@ __global__ __launch_bounds__(64 * W, W == 4 ? 3 : 1) void k_gemv(GemvArgs a) {
         }
       }
     }
+    if constexpr (WS) {
+      // the normalized rows (block 0): lane l holds row l / 16's groups
+      const int m = lane >> 4, j = lane & 15;
+      if (blockIdx.x == 0 && rs.y_out && m < M) {
+        float f = inv[0];
+#pragma unroll
+        for (int mm = 1; mm < MR; ++mm)
+          if (mm < M && m == mm) f = inv[mm];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float *o = rs.y_out + (size_t)m * K + wave * U * 128 + 128 * u + 8 * j;
+          *reinterpret_cast<float4 *>(o) =
+              float4{ys[u][0] * f, ys[u][1] * f, ys[u][2] * f, ys[u][3] * f};
+          *reinterpret_cast<float4 *>(o + 4) =
+              float4{ys[u][4] * f, ys[u][5] * f, ys[u][6] * f, ys[u][7] * f};
+        }
+      }
+    }
     if constexpr (PF) {
       if (blockIdx.x == 0 && (int)threadIdx.x < pf.half) {
         pf.rope_cur[threadIdx.x] = pf_cs[0];
@@ -1581,9 +1599,11 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
                  "residual (8 or 16 waves)");
   } else if (a.asrc == AS_WSTREAM) {
     MS_CHECK_ARG(a.M <= kWaveRowsMax && a.rows.x && a.rows.ld >= a.K && !a.rows.gamma &&
-                     !a.rows.x_out && !a.rows.y_out && a.epi == EPI_RESID && a.P == 1 &&
-                     a.waves == 16 && a.K == 16 * 5 * kSuperK,
-                 "GEMV: streamed per-wave rows: at most 4 rows, residual, 16 waves, K = 10240");
+                     !a.rows.x_out && wave_shape_ok(a) && a.epi != EPI_ACCUMULATE &&
+                     !(a.epi == EPI_STORE && a.waves != 4),
+                 "GEMV: streamed per-wave rows: at most 4 rows, K = waves * tpw * 128: "
+                 "store or SwiGLU on 4 waves (tpw 2 or 5), residual on 8 (tpw 1, 2, 4) "
+                 "or 16 waves (tpw 2, 5)");
   } else if (a.asrc == AS_ATTN) {
     MS_CHECK_ARG(a.M == 1 && a.P == 1 && a.waves == 8 && a.epi == EPI_RESID,
                  "GEMV: attention source: one row, one panel per block, 8 waves, residual");
@@ -1670,8 +1690,23 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     MS_CHECK_ARG(ok, "GEMV: per-wave rows: no instantiation for this shape");
   }
   if (!ok && a.asrc == AS_WSTREAM) {
-    MS_GEMV_L(1, EPI_RESID, 1, AS_WSTREAM, 16, 10 * kWaveRowsMax + 5);
-    ok = true;
+    const int tpw = a.K / (a.waves * kSuperK);
+#define MS_GEMV_S(EP, PP, WW, T)                                            \
+  if (!ok && a.epi == EP && a.waves == WW && tpw == T) {                    \
+    MS_GEMV_L(1, EP, PP, AS_WSTREAM, WW, 10 * kWaveRowsMax + T);            \
+    ok = true;                                                              \
+  }
+    MS_GEMV_S(EPI_STORE, 1, 4, 5)
+    MS_GEMV_S(EPI_STORE, 1, 4, 2)
+    MS_GEMV_S(EPI_SWIGLU, 2, 4, 5)
+    MS_GEMV_S(EPI_SWIGLU, 2, 4, 2)
+    MS_GEMV_S(EPI_RESID, 1, 16, 5)
+    MS_GEMV_S(EPI_RESID, 1, 16, 2)
+    MS_GEMV_S(EPI_RESID, 1, 8, 1)
+    MS_GEMV_S(EPI_RESID, 1, 8, 2)
+    MS_GEMV_S(EPI_RESID, 1, 8, 4)
+#undef MS_GEMV_S
+    MS_CHECK_ARG(ok, "GEMV: streamed per-wave rows: no instantiation for this shape");
   }
   if (!ok && a.asrc == AS_ATTN) {
     // the row-prologue template slot carries the head dim and the load pairs
