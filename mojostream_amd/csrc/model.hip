@@ -334,11 +334,10 @@ static int launch_proj_row(ms_model *m, const RunCfg &rc, GemvArgs a, const RowS
   // GEMV).  Measured at batch 4 against the block-wide row prologue (and for
   // Down against a quantization launch plus a GEMV reading limbs from
   // memory): Down 2,048 -> 2,255 tok/s, then Q|K|V and O 2,358; the demo
-  // harness step (four rows) 1.07 -> 1.00 ms.  Gate|Up keeps the block-wide
-  // prologue (2,215 against 2,260 tok/s streamed).  Down of the demo model
-  // (K = 4096) keeps its 8-wave row prologue.
-  if (a.M <= kWaveRowsMax && !r.gamma && !r.x_out && a.epi != EPI_SWIGLU &&
-      (waves_row != 16 || a.K == 16 * 5 * kSuperK)) {
+  // harness step (four rows) 1.07 -> 1.00 ms, and with the demo model's Down
+  // (K = 4096) streamed too 0.96 ms.  Gate|Up keeps the block-wide prologue
+  // (streamed: 2,305 against 2,352 tok/s; quantized up front per wave: 2,265).
+  if (a.M <= kWaveRowsMax && !r.gamma && !r.x_out && a.epi != EPI_SWIGLU) {
     GemvArgs w = a;
     w.asrc = AS_WSTREAM;
     w.rows = r;
