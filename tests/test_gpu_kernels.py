@@ -164,6 +164,43 @@ def test_q4_matmul_accumulates(gpu, oracle):
     assert rel_max(dC.download(np.float32, (M, N)), ref) < 1e-5
 
 
+@pytest.mark.parametrize("K", [1024, 2048, 4096, 2560])
+def test_q4_matmul_small_rows_equal_single_rows(gpu, oracle, K):
+    """Two to four rows go through one launch whose waves quantize their own
+    K slices of every row (a shift per row and wave, the same limbs as one row
+    alone), so each row of a 2-4 row call, stored or accumulated, equals that
+    row's one-row call bit for bit, whatever the other rows' scales; and is
+    within 1e-5 of the f64 product.  K = 1024, 2048, 4096: 8 waves of 1, 2, 4
+    super-tiles; K = 2560: 4 waves of 5 (store only)."""
+    ms = gpu
+    N = 768
+    say(f"q4_matmul 2-4 rows against single rows, K={K}")
+    q4 = ms.host_random_u8(K * N // 2, 41, K).reshape(K, N // 2)
+    _, d_pk = packed(ms, q4, K, N)
+    A = (RNG.standard_normal((4, K)) * np.array([[1e-3], [30.0], [1.0], [1e3]])).astype(np.float32)
+    C0 = RNG.standard_normal((4, N)).astype(np.float32)
+    single = {}
+    for acc in (0, 1):
+        if acc and K == 2560:
+            continue
+        for i in range(4):
+            dA = ms.DeviceBuffer.from_array(np.ascontiguousarray(A[i:i + 1]))
+            dC = ms.DeviceBuffer.from_array(np.ascontiguousarray(C0[i:i + 1]))
+            ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pk.ptr, 1, K, N, 0.1, acc))
+            single[acc, i] = dC.download(np.float32, (1, N))[0]
+        for M in (2, 3, 4):
+            dA = ms.DeviceBuffer.from_array(np.ascontiguousarray(A[:M]))
+            dC = ms.DeviceBuffer.from_array(np.ascontiguousarray(C0[:M]))
+            ms.check(ms.lib().ms_q4_matmul(dC.ptr, dA.ptr, d_pk.ptr, M, K, N, 0.1, acc))
+            c = dC.download(np.float32, (M, N))
+            for i in range(M):
+                assert np.array_equal(c[i], single[acc, i]), (acc, M, i)
+        ref = oracle.matmul_f64(A, q4, N, 0.1) + (C0 if acc else 0.0)
+        full = np.stack([single[acc, i] for i in range(4)])
+        for i in range(4):
+            assert rel_max(full[i:i + 1], ref[i:i + 1]) < 1e-5, (acc, i)
+
+
 def test_elementwise_kernels(gpu, oracle):
     ms = gpu
     lib = ms.lib()
