@@ -111,11 +111,13 @@ int ms_dequant_q4_packed(float *d_out, const uint8_t *d_packed, int K, int N,
 /* C (+)= A . deq(W): matmul_q4_bpack_raw, kernels.mojo:201-267 (and
  * matmul_q4_bpack :122-193 on a Q4Matrix).  A fp32 [M][K], W panel layout,
  * C fp32 [M][N].  accumulate=1 keeps the reference's C += semantics,
- * accumulate=0 overwrites.  Rows are processed in chunks of 16 (each row
- * quantized to a 31-bit fixed-point value, exact integer dot products); up to
- * four rows with K = 1024, 2048 or 4096 (or 2560 without accumulate) in one
- * launch with a fixed-point shift per row and slice of 128 to 640 values of K;
- * K <= 16384. */
+ * accumulate=0 overwrites.  Each row is quantized to fixed point and the dot
+ * products are exact integers: up to four rows with K = 1024, 2048 or 4096 (or
+ * 2560 without accumulate) in one launch, 31 bits with a shift per row and
+ * slice of 128 to 640 values of K; other calls of up to 16 rows quantize the
+ * rows (31 bits, a shift per row), then one GEMV; more rows are quantized to
+ * 22 bits (three int8 limbs) for the MFMA GEMM.  Every path is within 1e-5 of
+ * the f64 product; K <= 16384. */
 int ms_q4_matmul(float *d_C, const float *d_A, const uint8_t *d_packed, int M,
                  int K, int N, float scale, int accumulate);
 /* ms_q4_matmul without any allocation.  No counterpart in the reference: it is
