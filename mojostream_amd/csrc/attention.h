@@ -67,7 +67,15 @@ inline size_t dec_part_floats(int B, int n_heads, int hd) {
 // Chunks a partials launch covers (the host's position bound, else the cache).
 int dec_part_chunks(const AttnArgs &a);
 bool dec_part_ok(const AttnArgs &a);
-int launch_attention_partials(const AttnArgs &a, hipStream_t st);
+// Counters a model keeps for the decode attention (zero between launches):
+// k_attn_decode uses one per (sequence, kv head), the merging partials one per
+// (sequence, kv head, pair of query heads).
+inline size_t attn_ctr_count(int max_seqs, int n_kv) { return (size_t)max_seqs * n_kv * 2; }
+// merge = true: the same blocks, the RoPE factors from the tables at each
+// sequence's position, and the last block of each (sequence, kv head, pair of
+// query heads) merges the chunks into a.out [B][q_dim] (a.ctr: B * n_kv * 2
+// counters, zero between launches).
+int launch_attention_partials(const AttnArgs &a, hipStream_t st, bool merge = false);
 // Two to four rows of one sequence on a linear cache (attn_rows_ok): the
 // chunk scheme of the decode step per row (k_attn_rows), then the chunks
 // merged per row and query head into a.out [T][q_dim].  The partials need

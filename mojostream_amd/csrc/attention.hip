@@ -1488,9 +1488,11 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs args) {
 // the chunks, so no block waits for another.  Sixteen waves keep every SIMD
 // busy and every dependent step short.
 // ------------------------------------------------------------------------------
-template <int HD, int GQ>
+template <int HD, int GQ, bool MRG>
 __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs args) {
   extern __shared__ __align__(16) float lds[];
+  __shared__ int s_last;
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   constexpr int CH = kDecPartChunk;
   static_assert(CH == 32, "32 keys per chunk: one key per 32 lanes");
@@ -1566,11 +1568,13 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs args) {
     const bool on = e < nq;
     qx[u] = ld1(rq, on, q0 + d);
     qy[u] = ld1(rq, on, q0 + rope_partner(p, d));
-    const bool rot = p.apply_rope && d < p.rot;
-    const int ri = d < p.half ? d : d - p.half;
-    const float cv = ld1(rr, rot, ri);
-    qs[u] = ld1(rr, rot, p.half + ri);
-    qc[u] = rot ? cv : 1.f;
+    if constexpr (!MRG) {
+      const bool rot = p.apply_rope && d < p.rot;
+      const int ri = d < p.half ? d : d - p.half;
+      const float cv = ld1(rr, rot, ri);
+      qs[u] = ld1(rr, rot, p.half + ri);
+      qc[u] = rot ? cv : 1.f;
+    }
   }
   // fresh k, v: dim tid (threads below HD)
   const int df = tid < HD ? tid : 0;
@@ -1578,11 +1582,14 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs args) {
   const float kx = ld1(rq, tid < HD, k0 + df);
   const float ky = ld1(rq, tid < HD, k0 + rope_partner(p, df));
   const float vx = ld1(rq, tid < HD, p.q_dim + p.kv_dim + h * HD + df);
-  const bool krot = p.apply_rope && df < p.rot;
-  const int kri = df < p.half ? df : df - p.half;
-  const float kcv = ld1(rr, krot, kri);
-  const float ks_ = ld1(rr, krot, p.half + kri);
-  const float kc_ = krot ? kcv : 1.f;
+  float kc_ = 1.f, ks_ = 0.f;
+  if constexpr (!MRG) {
+    const bool krot = p.apply_rope && df < p.rot;
+    const int kri = df < p.half ? df : df - p.half;
+    const float kcv = ld1(rr, krot, kri);
+    ks_ = ld1(rr, krot, p.half + kri);
+    kc_ = krot ? kcv : 1.f;
+  }
   // every load above goes out here, before the position arrives (the
   // compiler would otherwise sink the fresh row's loads past the position
   // test into the block that uses them, one memory round trip later)
@@ -1598,6 +1605,12 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs args) {
   const bool fresh_here = fslot < nslots && fslot / CH == c;
   const int kf = fslot - c * CH;  // key of the fresh row in this chunk
   const bool own_fresh = fresh_here && key == kf;
+  if constexpr (MRG) {
+    // the RoPE factors of this sequence's position, from the tables
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) rope_cs(p, (tid + NT * u) % HD, base, qc[u], qs[u]);
+    if (fresh_here) rope_cs(p, df, base, kc_, ks_);
+  }
   if (slot >= nslots) {
 #pragma unroll
     for (int i = 0; i < NF; ++i) {
@@ -1696,21 +1709,119 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs args) {
   const int nhq = p.n_heads;
   float *po = p.part + (size_t)b * kDecPartMaxChunks * nhq * (HD + 2);
   float *pml = po + (size_t)kDecPartMaxChunks * nhq * HD;
+  f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
   if (tid < NU && t < Gl) {
-    float4 o = so[u];
 #pragma unroll
-    for (int g = 1; g < NKG; ++g) {
+    for (int g = 0; g < NKG; ++g) {
       const float4 w = so[g * NU + u];
-      o.x += w.x;
-      o.y += w.y;
-      o.z += w.z;
-      o.w += w.w;
+      o += f32x4{w.x, w.y, w.z, w.w};
     }
-    *reinterpret_cast<float4 *>(po + ((size_t)c * nhq + h * G + g0 + t) * HD + 4 * d4) = o;
   }
-  if (tid < Gl)
-    *reinterpret_cast<float2 *>(pml + ((size_t)c * nhq + h * G + g0 + tid) * 2) =
-        float2{sm[tid], sl[tid]};
+  if constexpr (!MRG) {
+    if (tid < NU && t < Gl)
+      *reinterpret_cast<float4 *>(po + ((size_t)c * nhq + h * G + g0 + t) * HD + 4 * d4) =
+          float4{o.x, o.y, o.z, o.w};
+    if (tid < Gl)
+      *reinterpret_cast<float2 *>(pml + ((size_t)c * nhq + h * G + g0 + tid) * 2) =
+          float2{sm[tid], sl[tid]};
+    return;
+  } else {
+    // MRG: the chunks merged here, into out [B][q_dim]
+    float *orow = p.out + (size_t)b * p.q_dim + (h * G + g0) * HD;
+    if (n_active == 1) {
+      // the only chunk: o / l, as the merge would form it
+      if (tid < NU && t < Gl) {
+        const float w = 1.0f / sl[t];
+        *reinterpret_cast<float4 *>(orow + t * HD + 4 * d4) =
+            float4{o.x * w, o.y * w, o.z * w, o.w * w};
+      }
+      return;
+    }
+    const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(
+        po, 0, (uint32_t)(kDecPartMaxChunks * nhq * HD * 4), 0x00020000);
+    if (tid < NU && t < Gl)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          o, rs_o, ((c * nhq + h * G + g0 + t) * HD + 4 * d4) * 4, 0, kSc1);
+    if (tid < Gl) {
+      st_agent(pml + (c * nhq + h * G + g0 + tid) * 2, sm[tid]);
+      st_agent(pml + (c * nhq + h * G + g0 + tid) * 2 + 1, sl[tid]);
+    }
+    // count this block done; the last block of (sequence, kv head, head pair)
+    // merges (k_attn_decode's protocol: device-scope partial stores waited
+    // for, a barrier, an agent-scope release + acquire increment; the last
+    // block reads the partials after the others' releases and resets the
+    // counter for the next launch)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      unsigned *ctr = p.ctr + ((size_t)b * p.n_kv + h) * NS + s;
+      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old + 1 == (unsigned)n_active;
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // log-sum-exp over the chunks: thread (unit u, chunk group kq) sums
+    // w_c o_c over chunks kq, kq + NKG, ..; its first batch of o partials is
+    // loaded before the weights are formed.  Wave t < Gl turns query head t's
+    // (m, l) pairs into w_c = e^(m_c - M) (one chunk per lane) and 1 / sum_c
+    // l_c w_c.  The group sums meet through LDS.
+    constexpr int MB = 4;  // chunks per thread per load batch
+    const __amdgpu_buffer_rsrc_t rs_ml = __builtin_amdgcn_make_buffer_rsrc(
+        pml, 0, (uint32_t)(kDecPartMaxChunks * nhq * 2 * 4), 0x00020000);
+    const uint32_t ou = ((h * G + g0 + (t < Gl ? t : 0)) * HD + 4 * d4) * 4;
+    f32x4 ov[MB];
+    auto load_o = [&](int c0) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const int cc = c0 + NKG * i;
+        ov[i] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rs_o, cc < n_active ? (uint32_t)cc * nhq * HD * 4 + ou : kOut, 0, 0));
+      }
+    };
+    load_o(kq);
+    float *wsh = sq;   // [kDecPartMaxChunks][GQ] chunk weights (queries no longer read)
+    float *sinv = sm;  // [GQ] 1 / l
+    const int wave = tid >> 6, lane = tid & 63;
+    static_assert(kDecPartMaxChunks == 64, "one chunk per lane");
+    if (wave < Gl) {
+      const bool on = lane < n_active;
+      const f32x2 ml = __builtin_bit_cast(
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                     rs_ml, on ? (uint32_t)(lane * nhq + h * G + g0 + wave) * 8 : kOut, 0, 0));
+      const float M = wave64_max(on ? ml.x : -INFINITY);
+      const float w = on ? expf(ml.x - M) : 0.f;
+      const float l = wave64_sum(on ? ml.y * w : 0.f);
+      wsh[lane * GQ + wave] = w;
+      if (lane == 0) sinv[wave] = 1.0f / l;
+    }
+    __syncthreads();
+    f32x4 oa = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = kq; c0 < n_active; c0 += NKG * MB) {
+      if (c0 != kq) load_o(c0);
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const int cc = c0 + NKG * i;
+        const float w = cc < n_active && t < Gl ? wsh[cc * GQ + t] : 0.f;
+        oa += w * ov[i];
+      }
+    }
+    so[kq * NU + u] = float4{oa.x, oa.y, oa.z, oa.w};
+    __syncthreads();
+    if (tid < NU && t < Gl) {
+      f32x4 r = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < NKG; ++q) {
+        const float4 w = so[q * NU + u];
+        r += f32x4{w.x, w.y, w.z, w.w};
+      }
+      const float inv = sinv[t];
+      *reinterpret_cast<float4 *>(orow + t * HD + 4 * d4) =
+          float4{r.x * inv, r.y * inv, r.z * inv, r.w * inv};
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------
@@ -2071,9 +2182,10 @@ int launch_rope_cur(const AttnArgs &a, hipStream_t st) {
   return MS_OK;
 }
 
-int launch_attention_partials(const AttnArgs &a, hipStream_t st) {
+int launch_attention_partials(const AttnArgs &a, hipStream_t st, bool merge) {
   MS_CHECK_ARG(dec_part_ok(a), "attention partials: unsupported shape");
-  MS_CHECK_ARG(a.qkv && a.part && a.pos && a.kc && a.vc && a.rope_cur,
+  MS_CHECK_ARG(a.qkv && a.part && a.pos && a.kc && a.vc &&
+                   (merge ? a.ctr && a.out && a.cos_t && a.sin_t : a.rope_cur != nullptr),
                "attention partials: missing buffers");
   AttnArgs a2 = a;
   a2.grid_chunks = dec_part_chunks(a);
@@ -2085,8 +2197,13 @@ int launch_attention_partials(const AttnArgs &a, hipStream_t st) {
   constexpr int CH = kDecPartChunk;
   // sv, sq, sf, ss, sm / sl (4 + 4 floats), so (16 KB at every head dim)
   const size_t shmem = (size_t)(CH * a.hd + GQ * a.hd + a.hd + GQ * CH + 8) * 4 + 16384;
-  if (a.hd == 256) hipLaunchKernelGGL((k_attn_part<256, GQ>), grid, dim3(1024), shmem, st, a2);
-  else hipLaunchKernelGGL((k_attn_part<512, GQ>), grid, dim3(1024), shmem, st, a2);
+  if (merge) {
+    if (a.hd == 256) hipLaunchKernelGGL((k_attn_part<256, GQ, true>), grid, dim3(1024), shmem, st, a2);
+    else hipLaunchKernelGGL((k_attn_part<512, GQ, true>), grid, dim3(1024), shmem, st, a2);
+  } else {
+    if (a.hd == 256) hipLaunchKernelGGL((k_attn_part<256, GQ, false>), grid, dim3(1024), shmem, st, a2);
+    else hipLaunchKernelGGL((k_attn_part<512, GQ, false>), grid, dim3(1024), shmem, st, a2);
+  }
   MS_HIP_TRY(hipGetLastError());
   return MS_OK;
 }

@@ -114,7 +114,7 @@ struct ms_model {
   int quant_k = 0;
   float *qkv = nullptr, *attn_part = nullptr;
   float *rope_cur = nullptr;  // one-row decode: RoPE factors at the position [2][256]
-  unsigned *attn_ctr = nullptr;  // decode chunk counters [seq][kv head], kept zero
+  unsigned *attn_ctr = nullptr;  // decode attention counters (attn_ctr_count), kept zero
   // prefill: rows per chunk (0: no prefill workspace), attention rows per
   // launch inside a chunk and their base positions on the device
   int prefill_rows = 0;
@@ -453,6 +453,11 @@ static int enqueue_layer(ms_model *m, int l, const RunCfg &rc, hipStream_t st) {
       }
       if (int rc2 = launch_attention_partials(a, st)) return rc2;
       merged_in_o = true;
+    } else if (rc.T == 1 && dec_part_ok(a)) {
+      // one row per sequence (a batch decode step, a one-row forward): the
+      // same chunk blocks, merged by the last block of each (sequence, kv
+      // head, head pair), the RoPE factors from the tables at each position
+      if (int rc2 = launch_attention_partials(a, st, true)) return rc2;
     } else if (attn_rows_ok(a)) {
       // two to four rows of one sequence: chunk partials per row, merged
       if (int rc2 = launch_attention_rows(a, st)) return rc2;
@@ -906,7 +911,7 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   if ((rc = dmalloc(m, (void **)&m->qkv, (size_t)M * m->qkv_max * 4)) ||
       (rc = dmalloc(m, (void **)&m->attn_part, max_part * 4)) ||
       (rc = dmalloc(m, (void **)&m->rope_cur, 512 * 4)) ||
-      (rc = dmalloc(m, (void **)&m->attn_ctr, (size_t)d.max_seqs * m->nkv_max * 4)) ||
+      (rc = dmalloc(m, (void **)&m->attn_ctr, attn_ctr_count(d.max_seqs, m->nkv_max) * 4)) ||
 
       (rc = dmalloc(m, (void **)&m->pos, 64 * 4)) ||
       (hipHostMalloc((void **)&m->h_pos_pin, 64 * 4, hipHostMallocDefault) != hipSuccess &&
@@ -918,7 +923,7 @@ extern "C" int ms_model_create(const ms_model_desc *desc, const ms_layer_desc *l
   if (hipMemset(m->pos, 0, 64 * 4) != hipSuccess || hipMemset(m->step, 0, 64 * 4) != hipSuccess ||
       hipMemset(m->attn_part, 0, max_part * 4) != hipSuccess ||
       hipMemset(m->tok, 0, 64 * 4) != hipSuccess ||
-      hipMemset(m->attn_ctr, 0, (size_t)d.max_seqs * m->nkv_max * 4) != hipSuccess)
+      hipMemset(m->attn_ctr, 0, attn_ctr_count(d.max_seqs, m->nkv_max) * 4) != hipSuccess)
     return cleanup(fail(MS_E_HIP, "model: memset failed"));
   // KV caches (zero-initialised like the reference's resized Lists)
   for (auto &Ly : m->L) {
@@ -1164,7 +1169,7 @@ extern "C" int ms_model_reset(ms_model *m) {
   // The decode attention's chunk counters are left zero by every completed
   // launch; clearing them here also recovers from an interrupted one.
   if (int rc = require_init()) return rc;
-  MS_HIP_TRY(hipMemset(m->attn_ctr, 0, (size_t)m->d.max_seqs * m->nkv_max * 4));
+  MS_HIP_TRY(hipMemset(m->attn_ctr, 0, attn_ctr_count(m->d.max_seqs, m->nkv_max) * 4));
   if (m->shist_n) MS_HIP_TRY(hipMemset(m->shist_n, 0, (size_t)m->d.max_seqs * 4));
   std::fill(m->h_hist_n.begin(), m->h_hist_n.end(), 0);
   if (m->samp_ctr) MS_HIP_TRY(hipMemset(m->samp_ctr, 0, 4));
