@@ -217,6 +217,25 @@ def test_decode_past_window_balanced(gpu, oracle16):
                    "balanced wrap", penalty=1.2)
 
 
+def test_decode_batch2_past_512_balanced(gpu, oracle16):
+    """Two sequences at different positions past 512 (prompts of 560 and 600
+    tokens, 8 steps): the batch step's attention merges each sequence's chunks
+    in the chunk kernel, and a full layer's 18-19 chunks take more than one
+    load pass of that merge (16 chunks per pass at head dim 512); the sliding
+    caches have wrapped.  Each sequence against its own teacher-forced oracle
+    run."""
+    ms = gpu
+    say("E4B balanced, batch 2: prompts of 560 and 600 tokens + 8 steps")
+    max_pos = 640
+    prompts = [prompt_ids(560, 262144, 6), prompt_ids(600, 262144, 7)]
+    keep = (7,)
+    pre, ids, logits, hid = gpu_decode(ms, True, prompts, 8, keep, max_pos, penalty=1.2)
+    hw = HostWeights(ms.arch_e4b(max_full_seq=max_pos), SEED, balanced=True)
+    for b, p in enumerate(prompts):
+        check_sequence(hw.model(oracle16), p, pre[b], ids, logits, hid, b, keep,
+                       f"batch 2 seq {b}", penalty=1.2)
+
+
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
